@@ -1,0 +1,253 @@
+/*
+ * roserlhf_amd.h — C ABI of the gfx950 (MI355X) kernels behind the
+ * rosellm_amd.roserlhf Python package.
+ *
+ * The reference (rosellm.roserlhf) is pure PyTorch and has no native layer; each
+ * entry point below replaces the ATen op sequence of one reference function,
+ * cited as file:line into rosellm/roserlhf/.  Python (rosellm_amd/_native.py)
+ * binds these with ctypes; INTEGRATION.md shows the binding.
+ *
+ * Conventions shared by every entry point:
+ *   - Every pointer is a device pointer unless named *_host.  All outputs and
+ *     workspaces are allocated by the caller; nothing here allocates.
+ *   - Calls are asynchronous and ordered on `stream` (a hipStream_t; NULL is the
+ *     legacy default stream).  They are reentrant and thread-safe.
+ *   - Return 0 on success or a negative rrl_status; rrl_last_error() then holds
+ *     a message for the calling thread.
+ *   - Data-dependent errors (an empty mask, a target id outside [0, V), an
+ *     invalid turn id) cannot be seen on the host without a sync, so kernels OR
+ *     rrl_flag bits into a caller-provided device int32 `status` word.  The
+ *     caller reads it once after the call and raises.
+ *   - A 2-D operand [rows, cols] is passed as an rrl_view: element (r, c) lives
+ *     at ptr + r*s_row + c*s_col elements.  s_col = 0 broadcasts a per-row value
+ *     over columns and s_row = 0 broadcasts one row (torch expand() views).
+ *   - Arithmetic is float32 unless an input is float64, in which case it is
+ *     float64 ("acc" type below).  16-bit inputs are widened on load.
+ */
+#ifndef ROSERLHF_AMD_H
+#define ROSERLHF_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RRL_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define RRL_API __attribute__((visibility("default")))
+#else
+#define RRL_API
+#endif
+
+/* Element types.  BOOL is one byte, nonzero = true. */
+enum rrl_dtype {
+  RRL_F32 = 0,
+  RRL_F64 = 1,
+  RRL_BF16 = 2,
+  RRL_F16 = 3,
+  RRL_BOOL = 4,
+  RRL_U8 = 5,
+  RRL_I8 = 6,
+  RRL_I16 = 7,
+  RRL_I32 = 8,
+  RRL_I64 = 9
+};
+
+enum rrl_status {
+  RRL_OK = 0,
+  RRL_EINVAL = -1,  /* bad size, stride, null pointer or parameter */
+  RRL_EDTYPE = -2,  /* dtype not supported for this operand */
+  RRL_ELAUNCH = -3, /* kernel launch failed (HIP error text in rrl_last_error) */
+  RRL_EALIGN = -4   /* pointer alignment below the element size */
+};
+
+/* Bits written (OR-ed) into the device `status` word. */
+enum rrl_flag {
+  RRL_FLAG_EMPTY_MASK = 1,       /* global mask weight sum is zero        (losses.py:48-49)   */
+  RRL_FLAG_EMPTY_ROW = 2,        /* some row has no action token          (losses.py:250-251) */
+  RRL_FLAG_TARGET_RANGE = 4,     /* target id outside [0, V)              (gather, losses.py:36) */
+  RRL_FLAG_INVALID_TURN = 8      /* unmasked token with invalid turn id   (advantages.py:284-286) */
+};
+
+/* Policy objectives (losses.py). */
+enum rrl_objective {
+  RRL_OBJ_PPO = 0,        /* clipped_policy_loss      losses.py:426-486 */
+  RRL_OBJ_SAO = 1,        /* sao_policy_loss          losses.py:127-203 */
+  RRL_OBJ_GSPO = 2,       /* gspo_policy_loss         losses.py:206-273 */
+  RRL_OBJ_GSPO_TOKEN = 3, /* gspo_token_policy_loss   losses.py:276-352 */
+  RRL_OBJ_SAPO = 4        /* sapo_policy_loss         losses.py:355-423 */
+};
+
+/* Scalar outputs of rrl_policy_fwd, in this order (acc dtype):
+ *   PPO:        objective, approximate_kl, clip_fraction, mean_ratio
+ *   SAO:        objective, approximate_kl, rejected_fraction, mean_ratio
+ *   GSPO(/tok): objective, sequence_ratio_divergence, sequence_clip_fraction,
+ *               mean_sequence_ratio
+ *   SAPO:       objective, approximate_kl, mean_ratio, mean_gradient_gate
+ * Slots 4..7 are reserved.  rrl_policy_bwd takes upstream gradients in the
+ * same slots (non-differentiable slots are ignored). */
+#define RRL_NSCALARS 8
+
+typedef struct rrl_view {
+  const void* ptr;
+  int32_t dtype;
+  int64_t s_row;
+  int64_t s_col;
+} rrl_view;
+
+typedef struct rrl_policy_params {
+  int32_t kind;          /* rrl_objective */
+  int32_t detach_ratio;  /* SAO only (losses.py:185) */
+  int32_t mask_is_weight;/* 1: mask is cast to the value dtype and used as a
+                            weight (masked_mean, losses.py:46); 0: mask != 0 */
+  int32_t reserved;
+  double clip_low;       /* thresholds are formed as acc(1 - clip_low) etc. */
+  double clip_high;
+  double max_log_ratio;
+  double tau_positive;   /* SAPO */
+  double tau_negative;   /* SAPO */
+} rrl_policy_params;
+
+RRL_API const char* rrl_last_error(void);
+RRL_API int rrl_abi_version(void);
+
+/* ---- a1/a2: token log-probs (losses.py:14-38) and their backward ---------
+ * logits: [B, T, V] with the vocabulary contiguous; row (b, t) starts at
+ * logits + b*ls_b + t*ls_t elements (a causal shift logits[:, :-1] is such a
+ * view).  dtype F32, F64, BF16 or F16.  targets: [B, T] view, I32 or I64.
+ * Outputs are contiguous [B*T]: logp in logp_dtype (F32 or F64), lse in acc. */
+RRL_API int rrl_logprob_fwd(const void* logits, int32_t logits_dtype, int64_t B, int64_t T,
+                    int64_t V, int64_t ls_b, int64_t ls_t, rrl_view targets,
+                    void* logp_out, int32_t logp_dtype, void* lse_out,
+                    int32_t* status, void* stream);
+
+/* dlogits[b,t,v] (+)= g[b*T+t] * ([v == target] - exp(x[b,t,v] - lse[b*T+t])),
+ * the composed gather_backward + log_softmax_backward.  g and lse are
+ * contiguous acc-typed [B*T]; dlogits has its own (ds_b, ds_t) row strides and
+ * dtype.  accumulate = 1 adds into dlogits.  dlogits may alias logits when the
+ * strides match (in-place). */
+RRL_API int rrl_logprob_bwd(const void* logits, int32_t logits_dtype, int64_t B, int64_t T,
+                    int64_t V, int64_t ls_b, int64_t ls_t, rrl_view targets,
+                    const void* lse, const void* g, void* dlogits, int32_t dl_dtype,
+                    int64_t ds_b, int64_t ds_t, int32_t accumulate, void* stream);
+
+/* dlogits[b,t,:] *= scale[0] unless scale[0] == skip_if (no memory touched
+ * then).  scale is a device acc scalar, so the caller never syncs. */
+RRL_API int rrl_scale_rows(void* dlogits, int32_t dl_dtype, int64_t B, int64_t T, int64_t V,
+                   int64_t ds_b, int64_t ds_t, const void* scale, int32_t scale_dtype,
+                   double skip_if, void* stream);
+
+/* ---- a3-a8: policy objectives over [B, T] log-probs ---------------------
+ * cur, old: [B, T] log-prob views; adv: [B, T] view, or [B] broadcast with
+ * s_col = 0 for GSPO (sequence advantages); mask: [B, T] any dtype.
+ * workspace: rrl_policy_workspace_bytes(B, acc) bytes, written by fwd and read
+ * by bwd (per-row statistics).  scalars_out: acc[RRL_NSCALARS].
+ * seq_out: acc[B] sequence ratios for GSPO kinds (else may be NULL).
+ * trusted_out: uint8 [B*T] SAO trust mask intersected with the action mask
+ * (else may be NULL).  status gets EMPTY_MASK / EMPTY_ROW. */
+RRL_API size_t rrl_policy_workspace_bytes(int64_t B, int32_t acc_dtype);
+
+RRL_API int rrl_policy_fwd(const rrl_policy_params* params, int64_t B, int64_t T, rrl_view cur,
+                   rrl_view old, rrl_view adv, rrl_view mask, int32_t acc_dtype,
+                   void* workspace, void* scalars_out, void* seq_out,
+                   uint8_t* trusted_out, int32_t* status, void* stream);
+
+/* grad_cur[b*T+t] (acc, contiguous) = sum_k grad_scalars[k] * d scalar_k / d cur[b,t]
+ * (+ sum_b grad_seq[b] * d seq_ratio_b / d cur for GSPO kinds; grad_seq may be
+ * NULL).  grad_scalars: device acc[RRL_NSCALARS]. */
+RRL_API int rrl_policy_bwd(const rrl_policy_params* params, int64_t B, int64_t T, rrl_view cur,
+                   rrl_view old, rrl_view adv, rrl_view mask, int32_t acc_dtype,
+                   const void* workspace, const void* grad_scalars, const void* grad_seq,
+                   void* grad_cur, void* stream);
+
+/* ---- single pass: log-prob + token-local objective gradient --------------
+ * For PPO, SAO and SAPO, d loss / d logp is token-local once the mask
+ * denominators are known, so one sweep over each logits row produces logp,
+ * lse and dlogits = d(-objective)/d logits.  rrl_policy_row_coef first writes
+ * row_coef[b] (acc, [B]): 1/sum(mask weight) for PPO/SAO, 1/(B*L_b) for SAPO,
+ * and flags EMPTY_MASK / EMPTY_ROW.  The objective scalars then come from
+ * rrl_policy_fwd on the returned logp. */
+RRL_API int rrl_policy_row_coef(const rrl_policy_params* params, int64_t B, int64_t T,
+                        rrl_view mask, int32_t acc_dtype, void* row_coef,
+                        void* workspace, int32_t* status, void* stream);
+
+RRL_API int rrl_fused_logprob_policy(const rrl_policy_params* params, const void* logits,
+                             int32_t logits_dtype, int64_t B, int64_t T, int64_t V,
+                             int64_t ls_b, int64_t ls_t, rrl_view targets, rrl_view old,
+                             rrl_view adv, rrl_view mask, const void* row_coef,
+                             void* logp_out, void* lse_out, void* dlogits,
+                             int32_t dl_dtype, int64_t ds_b, int64_t ds_t,
+                             int32_t* status, void* stream);
+
+/* ---- a4, a9: masked_mean (losses.py:41-50), sequence_log_ratio (:489-512)
+ * masked_mean: out = acc[1] = sum(values * w) / sum(w), w = mask cast to the
+ * value dtype; flags EMPTY_MASK.  The workspace keeps the denominator for the
+ * backward.  sequence_log_ratio: out, counts_out = acc[B]; flags EMPTY_ROW. */
+RRL_API size_t rrl_reduce_workspace_bytes(int64_t n);
+RRL_API int rrl_masked_mean_fwd(int64_t B, int64_t T, rrl_view values, rrl_view mask,
+                        int32_t acc_dtype, void* workspace, void* out, int32_t* status,
+                        void* stream);
+/* grad_values[b*T+t] = grad[0] * w[b,t] / sum(w); workspace as written by fwd. */
+RRL_API int rrl_masked_mean_bwd(int64_t B, int64_t T, rrl_view mask, int32_t acc_dtype,
+                        const void* workspace, const void* grad, void* grad_values,
+                        void* stream);
+RRL_API int rrl_sequence_log_ratio_fwd(int64_t B, int64_t T, rrl_view cur, rrl_view old,
+                               rrl_view mask, int32_t length_normalize, int32_t acc_dtype,
+                               void* out, void* counts_out, int32_t* status, void* stream);
+RRL_API int rrl_sequence_log_ratio_bwd(int64_t B, int64_t T, rrl_view mask, int32_t length_normalize,
+                               int32_t acc_dtype, const void* counts, const void* grad,
+                               void* grad_cur, void* stream);
+
+/* direct_double_sided_mask (losses.py:104-124): out = (r > lo) & (r < hi), strict.
+ * lo = 1 - clip_low and hi = 1 + clip_high must already be rounded to the
+ * ratio dtype (torch compares a tensor with a Python scalar in the tensor's
+ * dtype). */
+RRL_API int rrl_double_sided_mask(int64_t n, const void* ratios, int32_t dtype, double lo, double hi,
+                          uint8_t* out, void* stream);
+
+/* ---- a10-a17: estimators (advantages.py) ----------------------------------
+ * Sequences are rows of [B, T] views; reverse recurrences run as segmented
+ * affine scans.  terminated / valid may have ptr = NULL (all false / all true).
+ * bootstrap: [B] view (s_col ignored) or ptr = NULL for zero.  Outputs are
+ * contiguous [B*T] in out_dtype. */
+RRL_API int rrl_discounted_returns(int64_t B, int64_t T, rrl_view rewards, rrl_view terminated,
+                           rrl_view valid, rrl_view bootstrap, double gamma,
+                           void* out, int32_t out_dtype, void* stream);
+
+RRL_API int rrl_gae(int64_t B, int64_t T, rrl_view rewards, rrl_view values, rrl_view terminated,
+            rrl_view valid, rrl_view bootstrap, double gamma, double gae_lambda,
+            void* adv_out, void* targets_out, int32_t out_dtype, void* stream);
+
+RRL_API int rrl_skip_observation_gae(int64_t B, int64_t T, rrl_view rewards,
+                             rrl_view action_end_values, rrl_view next_action_values,
+                             rrl_view terminated, rrl_view valid, double gamma,
+                             double gae_lambda, void* adv_out, void* targets_out,
+                             int32_t out_dtype, void* stream);
+
+/* Groups are rows of a [n_groups, G] view. */
+RRL_API int rrl_group_standardize(int64_t n_groups, int64_t G, rrl_view rewards, double eps,
+                          void* out, int32_t out_dtype, void* stream);
+RRL_API int rrl_leave_one_out(int64_t n_groups, int64_t G, rrl_view rewards, void* out,
+                      int32_t out_dtype, void* stream);
+
+/* out[b,t] = mask[b,t] ? turn_adv[b, turn_ids[b,t]] : 0; flags INVALID_TURN. */
+RRL_API int rrl_broadcast_turn(int64_t B, int64_t K, int64_t T, rrl_view turn_adv,
+                       rrl_view turn_ids, rrl_view mask, void* out, int32_t out_dtype,
+                       int32_t* status, void* stream);
+
+/* Masked whitening over all tokens with mask != 0 (no reference function):
+ * out = mask ? (x - mean) / (std_pop + eps) : 0, mean and population std over
+ * the masked tokens; shift_mean = 0 keeps the mean (out = mask ? x/(std+eps)
+ * : 0).  workspace: rrl_reduce_workspace_bytes(B*T).  Flags EMPTY_MASK. */
+RRL_API int rrl_masked_whiten(int64_t B, int64_t T, rrl_view x, rrl_view mask, double eps,
+                      int32_t shift_mean, int32_t acc_dtype, void* workspace, void* out,
+                      int32_t out_dtype, int32_t* status, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ROSERLHF_AMD_H */

@@ -1,0 +1,53 @@
+"""MI355X-native RoseRLHF hot path: same public names as ``rosellm.roserlhf``
+(rosellm/roserlhf/__init__.py:8-48), backed by gfx950 HIP kernels.
+
+``fused_policy_loss`` and ``masked_whiten`` are additions of this package;
+``losses.masked_mean`` and ``losses.sequence_log_ratio`` stay module-level as
+in the reference.
+"""
+
+from .advantages import (
+    broadcast_turn_advantages,
+    discounted_returns,
+    generalized_advantage_estimation,
+    group_standardized_advantages,
+    leave_one_out_advantages,
+    masked_whiten,
+    skip_observation_generalized_advantage_estimation,
+)
+from .losses import (
+    GspoPolicyLossOutput,
+    PolicyLossOutput,
+    SapoPolicyLossOutput,
+    SaoPolicyLossOutput,
+    clipped_policy_loss,
+    direct_double_sided_mask,
+    fused_policy_loss,
+    gather_token_logprobs,
+    gspo_policy_loss,
+    gspo_token_policy_loss,
+    sapo_policy_loss,
+    sao_policy_loss,
+)
+
+__all__ = [
+    "GspoPolicyLossOutput",
+    "PolicyLossOutput",
+    "SapoPolicyLossOutput",
+    "SaoPolicyLossOutput",
+    "broadcast_turn_advantages",
+    "clipped_policy_loss",
+    "discounted_returns",
+    "direct_double_sided_mask",
+    "fused_policy_loss",
+    "gather_token_logprobs",
+    "generalized_advantage_estimation",
+    "group_standardized_advantages",
+    "leave_one_out_advantages",
+    "gspo_policy_loss",
+    "gspo_token_policy_loss",
+    "masked_whiten",
+    "sapo_policy_loss",
+    "sao_policy_loss",
+    "skip_observation_generalized_advantage_estimation",
+]
