@@ -125,14 +125,17 @@ RRL_API int rrl_logprob_fwd(const void* logits, int32_t logits_dtype, int64_t B,
                     int32_t* status, void* stream);
 
 /* dlogits[b,t,v] (+)= g[b*T+t] * ([v == target] - exp(x[b,t,v] - lse[b*T+t])),
- * the composed gather_backward + log_softmax_backward.  g and lse are
- * contiguous acc-typed [B*T]; dlogits has its own (ds_b, ds_t) row strides and
- * dtype.  accumulate = 1 adds into dlogits.  dlogits may alias logits when the
- * strides match (in-place). */
+ * the composed gather_backward + log_softmax_backward (autograd of
+ * losses.py:34-38).  g, lse and logp are contiguous acc-typed [B*T] (logp as
+ * written by rrl_logprob_fwd; may be NULL, in which case the target column is
+ * formed from lse, losing relative precision when p_target -> 1); dlogits has
+ * its own (ds_b, ds_t) row strides and dtype.  accumulate = 1 adds into
+ * dlogits.  dlogits may alias logits when the strides match (in-place). */
 RRL_API int rrl_logprob_bwd(const void* logits, int32_t logits_dtype, int64_t B, int64_t T,
                     int64_t V, int64_t ls_b, int64_t ls_t, rrl_view targets,
-                    const void* lse, const void* g, void* dlogits, int32_t dl_dtype,
-                    int64_t ds_b, int64_t ds_t, int32_t accumulate, void* stream);
+                    const void* lse, const void* logp, const void* g, void* dlogits,
+                    int32_t dl_dtype, int64_t ds_b, int64_t ds_t, int32_t accumulate,
+                    void* stream);
 
 /* dlogits[b,t,:] *= scale[0] unless scale[0] == skip_if (no memory touched
  * then).  scale is a device acc scalar, so the caller never syncs. */

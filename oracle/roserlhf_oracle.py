@@ -27,10 +27,17 @@ from torch import Tensor
 # ---------------------------------------------------------------------------
 
 
-def token_logprobs(logits: Tensor, targets: Tensor) -> Tensor:
-    """log p(target) per position: the vocabulary log-softmax, then a gather."""
+def token_logprobs(logits: Tensor, targets: Tensor, *, exact: bool = False) -> Tensor:
+    """log p(target) per position: the vocabulary log-softmax, then a gather.
 
-    x = logits.float() if logits.dtype in (torch.bfloat16, torch.float16) else logits
+    ``exact=True`` evaluates on the float64 upcast of the logits (exact for
+    every float dtype), which is the value a float32 kernel is held to.
+    """
+
+    if exact:
+        x = logits.double()
+    else:
+        x = logits.float() if logits.dtype in (torch.bfloat16, torch.float16) else logits
     logsm = F.log_softmax(x, dim=-1)
     return torch.take_along_dim(logsm, targets.long().unsqueeze(-1), dim=-1).squeeze(-1)
 
@@ -344,12 +351,24 @@ def grpo_step(logits: Tensor, targets: Tensor, old: Tensor, adv: Tensor, mask: T
 
 
 def policy_step(kind: str, logits: Tensor, targets: Tensor, old: Tensor, adv: Tensor,
-                mask: Tensor, **kw) -> Tuple[Dict[str, Tensor], Tensor, Tensor]:
-    """Like grpo_step for any objective name ('ppo', 'sao', 'gspo', 'gspo_token', 'sapo')."""
+                mask: Tensor, *, exact: bool = False, **kw
+                ) -> Tuple[Dict[str, Tensor], Tensor, Tensor]:
+    """Like grpo_step for any objective name ('ppo', 'sao', 'gspo', 'gspo_token', 'sapo').
+
+    ``exact=True`` runs the whole composition in float64 on exact upcasts of
+    the inputs (the reference's math without float32 rounding).
+    """
 
     fns = {"ppo": ppo_clip, "sao": sao, "gspo": gspo, "gspo_token": gspo_token, "sapo": sapo}
     x = logits.detach()
-    x = (x.float() if x.dtype in (torch.bfloat16, torch.float16) else x.clone()).requires_grad_()
+    if exact:
+        x = x.double().requires_grad_()
+        old, adv = old.double(), adv.double()
+        if mask.is_floating_point():
+            mask = mask.double()
+    else:
+        x = (x.float() if x.dtype in (torch.bfloat16, torch.float16) else x.clone())
+        x.requires_grad_()
     lp = token_logprobs(x, targets)
     lp.retain_grad()
     out = fns[kind](lp, old, adv, mask, **kw)

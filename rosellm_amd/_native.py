@@ -79,7 +79,7 @@ SIGNATURES = {
     "rrl_last_error": (ctypes.c_char_p, []),
     "rrl_abi_version": (ctypes.c_int, []),
     "rrl_logprob_fwd": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I64, _V, _P, _I32, _P, _P, _P]),
-    "rrl_logprob_bwd": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I64, _V, _P, _P, _P, _I32, _I64, _I64, _I32, _P]),
+    "rrl_logprob_bwd": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I64, _V, _P, _P, _P, _P, _I32, _I64, _I64, _I32, _P]),
     "rrl_scale_rows": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _D, _P]),
     "rrl_policy_workspace_bytes": (ctypes.c_size_t, [_I64, _I32]),
     "rrl_policy_fwd": (ctypes.c_int, [_PP, _I64, _I64, _V, _V, _V, _V, _I32, _P, _P, _P, _P, _P, _P]),
@@ -128,8 +128,33 @@ def lib() -> ctypes.CDLL:
     return _lib if _lib is not None else load()
 
 
+# Optional per-entry-point launch timing: name -> list of (start, end)
+# torch.cuda.Event pairs recorded on the stream the call is launched on.
+_timed: dict = {}
+
+
+def time_calls(*names: str) -> dict:
+    """Record a HIP event pair around every later call of each named entry
+    point (on torch's current stream, where the call launches its kernels).
+    Returns the live name -> [(start, end), ...] mapping; ``time_calls()``
+    with no names stops recording."""
+
+    _timed.clear()
+    for n in names:
+        _timed[n] = []
+    return _timed
+
+
 def call(name: str, *args) -> None:
+    events = _timed.get(name) if _timed else None
+    if events is not None:
+        start = torch.cuda.Event(enable_timing=True)
+        start.record()
     rc = getattr(lib(), name)(*args)
+    if events is not None:
+        end = torch.cuda.Event(enable_timing=True)
+        end.record()
+        events.append((start, end))
     if rc != 0:
         msg = lib().rrl_last_error().decode(errors="replace")
         raise RuntimeError(f"{name} failed ({rc}): {msg}")

@@ -25,85 +25,77 @@ __global__ __launch_bounds__(NT) void row_kernel(RowArgs a) {
   constexpr int VEC = Tag::VEC;
   __shared__ Acc sh_m[NT / 64];
   __shared__ Acc sh_s[NT / 64];
-  __shared__ Acc sh_g;
-  __shared__ int64_t sh_tgt;
 
   const int64_t rows = a.B * a.T;
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     const int64_t b = r / a.T, t = r - (r / a.T) * a.T;
     const S* row = static_cast<const S*>(a.logits) + b * a.ls_b + t * a.ls_t;
     const RowSplit sp = RowSplit::make<S, VEC>(row, a.V);
+    // The target id and logit are uniform over the workgroup.
+    const int64_t tgt = load_index(a.tgt.ptr, a.tgt.dt, b * a.tgt.sr + t * a.tgt.sc);
+    const bool tgt_ok = tgt >= 0 && tgt < a.V;
+    const int64_t tgt_safe = tgt_ok ? tgt : 0;  // never address outside the row
+    const Acc xt = tgt_ok ? Tag::cvt(row[tgt_safe]) : M<Acc>::nan();
 
-    Acc lse = Acc(0), g = Acc(0);
+    Acc lse, g, logp;
+    bool have_logp = true;
     if (MODE == MODE_BWD) {
       lse = static_cast<const Acc*>(a.lse)[r];
       g = static_cast<const Acc*>(a.g)[r];
-      if (threadIdx.x == 0) {
-        const int64_t tgt = load_index(a.tgt.ptr, a.tgt.dt, b * a.tgt.sr + t * a.tgt.sc);
-        if (tgt < 0 || tgt >= a.V) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
-        sh_tgt = tgt;
-      }
+      have_logp = a.logp_in != nullptr;
+      logp = have_logp ? static_cast<const Acc*>(a.logp_in)[r] : Acc(0);
+      if (threadIdx.x == 0 && !tgt_ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
     } else {
-      // Sweep 1: online max / sum of exp.
+      // Sweep 1: online max / sum of exp over the non-target columns.
       Acc m = -M<Acc>::inf(), s = Acc(0);
       for (int64_t i = threadIdx.x; i < sp.head; i += NT) {
         Acc x[1] = {Tag::cvt(row[i])};
-        online_update<Acc, 1>(m, s, x);
+        online_update<Acc, 1>(m, s, x, i == tgt ? 0 : -1);
       }
       const S* body = row + sp.head;
       for (int64_t k = threadIdx.x; k < sp.nvec; k += NT) {
         Acc x[VEC];
         Tag::load_vec(body + k * VEC, x);
-        online_update<Acc, VEC>(m, s, x);
+        const int64_t rel = tgt - (sp.head + k * VEC);
+        online_update<Acc, VEC>(m, s, x, (rel >= 0 && rel < VEC) ? (int)rel : -1);
       }
-      const S* tail = body + sp.nvec * VEC;
+      const int64_t tail0 = sp.head + sp.nvec * VEC;
       for (int64_t i = threadIdx.x; i < sp.tail; i += NT) {
-        Acc x[1] = {Tag::cvt(tail[i])};
-        online_update<Acc, 1>(m, s, x);
+        Acc x[1] = {Tag::cvt(row[tail0 + i])};
+        online_update<Acc, 1>(m, s, x, tail0 + i == tgt ? 0 : -1);
       }
       block_online_combine<NT, Acc>(m, s, sh_m, sh_s);
-      lse = (m == -M<Acc>::inf()) ? -M<Acc>::inf() : m + M<Acc>::log(s);
-      if (m != m || s != s) lse = M<Acc>::nan();
-
+      const RowLogprob<Acc> fr = finish_row<Acc>(m, s, xt);
+      lse = fr.lse;
+      logp = fr.logp;
+      if (!tgt_ok) logp = M<Acc>::nan();
+      g = Acc(0);
+      if (MODE == MODE_FUSED) {
+        const PolicyConsts<Acc> c = PolicyConsts<Acc>::make(a.pp);
+        const Acc o = a.old.get<Acc>(b, t);
+        const Acc A = a.adv.get<Acc>(b, t);
+        const Acc w = mask_weight<Acc>(c, a.mask, b, t);
+        const Acc coef = static_cast<const Acc*>(a.row_coef)[b];
+        // loss = -objective, so dlogits carries d(-objective)/d logp.
+        g = -((w * coef) * token_local_grad<Acc>(c, logp, o, A));
+      }
       if (threadIdx.x == 0) {
-        const int64_t tgt = load_index(a.tgt.ptr, a.tgt.dt, b * a.tgt.sr + t * a.tgt.sc);
-        Acc xt;
-        if (tgt < 0 || tgt >= a.V) {
-          raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
-          xt = M<Acc>::nan();
-        } else {
-          xt = Tag::cvt(row[tgt]);
-        }
-        const Acc l = xt - lse;
-        store_as<Acc>(a.logp, a.logp_dt, r, l);
+        if (!tgt_ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+        store_as<Acc>(a.logp, a.logp_dt, r, logp);
         static_cast<Acc*>(a.lse_out)[r] = lse;
-        sh_tgt = tgt;
-        if (MODE == MODE_FUSED) {
-          const PolicyConsts<Acc> c = PolicyConsts<Acc>::make(a.pp);
-          const Acc o = a.old.get<Acc>(b, t);
-          const Acc A = a.adv.get<Acc>(b, t);
-          const Acc w = mask_weight<Acc>(c, a.mask, b, t);
-          const Acc coef = static_cast<const Acc*>(a.row_coef)[b];
-          // loss = -objective, so dlogits carries d(-objective)/d logp.
-          sh_g = -((w * coef) * token_local_grad<Acc>(c, l, o, A));
-        }
       }
     }
 
     if (MODE == MODE_BWD || MODE == MODE_FUSED) {
       // Sweep 2: dlogits = g * ([v == target] - exp(x - lse)).
-      __syncthreads();
-      const int64_t target = sh_tgt;
-      if (MODE == MODE_FUSED) g = sh_g;
-      __syncthreads();
       void* drow = static_cast<char*>(a.dl) +
                    (b * a.ds_b + t * a.ds_t) * (int64_t)dtype_size_dev(a.dl_dt);
       const bool zero_row = (g == Acc(0)) && (lse - lse == Acc(0));
-      if (zero_row && a.accumulate) continue;
-      write_row_grad<Tag, NT>(row, sp, drow, a.dl_dt, a.V, target, g, lse, zero_row,
-                              a.accumulate);
-    } else {
-      __syncthreads();
+      if (!(zero_row && a.accumulate)) {
+        const Acc tgt_d = target_grad<Acc>(g, logp, have_logp, xt, lse);
+        write_row_grad<Tag, NT>(row, sp, drow, a.dl_dt, a.V, tgt, g, lse, tgt_d, zero_row,
+                                a.accumulate);
+      }
     }
   }
 }
@@ -188,8 +180,9 @@ extern "C" int rrl_logprob_fwd(const void* logits, int32_t logits_dtype, int64_t
 
 extern "C" int rrl_logprob_bwd(const void* logits, int32_t logits_dtype, int64_t B, int64_t T,
                                int64_t V, int64_t ls_b, int64_t ls_t, rrl_view targets,
-                               const void* lse, const void* g, void* dlogits, int32_t dl_dtype,
-                               int64_t ds_b, int64_t ds_t, int32_t accumulate, void* stream) {
+                               const void* lse, const void* logp, const void* g, void* dlogits,
+                               int32_t dl_dtype, int64_t ds_b, int64_t ds_t, int32_t accumulate,
+                               void* stream) {
   clear_error();
   int rc = validate_logits(logits, logits_dtype, B, T, V, targets);
   if (rc) return rc;
@@ -198,7 +191,7 @@ extern "C" int rrl_logprob_bwd(const void* logits, int32_t logits_dtype, int64_t
   RowArgs a{};
   a.logits = logits; a.B = B; a.T = T; a.V = V; a.ls_b = ls_b; a.ls_t = ls_t;
   a.tgt = to_view(targets);
-  a.lse = lse; a.g = g; a.dl = dlogits; a.dl_dt = dl_dtype; a.ds_b = ds_b; a.ds_t = ds_t;
+  a.lse = lse; a.logp_in = logp; a.g = g; a.dl = dlogits; a.dl_dt = dl_dtype; a.ds_b = ds_b; a.ds_t = ds_t;
   a.accumulate = accumulate;
   bool launched = false;
   rc = maybe_launch_resident(a, 1, logits_dtype, as_stream(stream), &launched);

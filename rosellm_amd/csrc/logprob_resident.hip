@@ -1,14 +1,283 @@
-// Register-resident bf16 row kernels (fast path of rrl_logprob_bwd and
-// rrl_fused_logprob_policy).
+// Register-resident 16-bit row kernel: the fast path of
+// rrl_fused_logprob_policy (log-prob + token-local objective gradient in one
+// read of the logits, losses.py:14-38 composed with :426-486 / :127-203 /
+// :355-423).
+//
+// Layout and schedule (gfx950, wave64):
+//   * A persistent grid of one 1024-lane workgroup per CU walks rows
+//     r = blockIdx.x, blockIdx.x + gridDim.x, ...
+//   * A row of V 16-bit logits is held in VGPRs as SL slabs of one 16-byte
+//     vector per lane: slab k, lane j holds vector k*1024 + j.  V = 151936
+//     (bf16) is 18992 vectors, SL = 19 of the SL = 20 variant, i.e. 80 VGPRs.
+//   * Sweep 1 (registers only): online max / sum of exp over the non-target
+//     columns per lane, one LDS combine across the 16 waves.
+//   * Sweep 2: each slab becomes g * (onehot - exp(x - lse)), is packed back to
+//     16 bits and stored with a non-temporal buffer store; the same registers
+//     are immediately refilled with the matching slab of the workgroup's next
+//     row, so the next row's HBM reads overlap this row's arithmetic and
+//     stores.
+// Every access is a raw buffer load/store whose descriptor covers exactly one
+// row, so a lane past the end of the row reads zeros and its stores are
+// dropped by the hardware range check.
+#include <hip/hip_runtime.h>
+
+#include "policy_math.hpp"
 #include "row_common.hpp"
 
 namespace rrl {
 
+namespace {
+
+constexpr int RNT = 1024;                 // lanes per workgroup (16 waves)
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource over `bytes` bytes at `base`.  The last dword selects a
+// non-zero 32-bit data format, which enables raw (untyped) accesses; stride 0
+// makes num_records a byte count checked against each access's offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// Cache-policy bits of a buffer access on gfx950: bit 1 = non-temporal.
+constexpr int kAuxLoad = 0;
+constexpr int kAuxStoreNT = 2;
+
+template <class Tag> struct Pack16;
+template <> struct Pack16<TagBF16> {
+  static __device__ __forceinline__ void unpack(const u32x4& u, float (&x)[8]) {
+    x[0] = __uint_as_float(u.x << 16); x[1] = __uint_as_float(u.x & 0xffff0000u);
+    x[2] = __uint_as_float(u.y << 16); x[3] = __uint_as_float(u.y & 0xffff0000u);
+    x[4] = __uint_as_float(u.z << 16); x[5] = __uint_as_float(u.z & 0xffff0000u);
+    x[6] = __uint_as_float(u.w << 16); x[7] = __uint_as_float(u.w & 0xffff0000u);
+  }
+  static __device__ __forceinline__ u32x4 pack(const float (&d)[8]) {
+    u32x4 o;
+    o.x = f32x2_to_bf16x2_bits(d[0], d[1]);
+    o.y = f32x2_to_bf16x2_bits(d[2], d[3]);
+    o.z = f32x2_to_bf16x2_bits(d[4], d[5]);
+    o.w = f32x2_to_bf16x2_bits(d[6], d[7]);
+    return o;
+  }
+};
+template <> struct Pack16<TagF16> {
+  static __device__ __forceinline__ void unpack(const u32x4& u, float (&x)[8]) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = f16_bits_to_f32((uint16_t)(w[i] & 0xffffu));
+      x[2 * i + 1] = f16_bits_to_f32((uint16_t)(w[i] >> 16));
+    }
+  }
+  static __device__ __forceinline__ u32x4 pack(const float (&d)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)f32_to_f16_bits(d[2 * i]) | ((uint32_t)f32_to_f16_bits(d[2 * i + 1]) << 16);
+    u32x4 o;
+    o.x = w[0]; o.y = w[1]; o.z = w[2]; o.w = w[3];
+    return o;
+  }
+};
+
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <class Tag, int SL>
+__global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t nvec) {
+  __shared__ float sh_m[RNT / 64];
+  __shared__ float sh_s[RNT / 64];
+  __shared__ float sh_xt;
+
+  const int tid = threadIdx.x;
+  const int64_t rows = a.B * a.T;
+  const uint32_t row_bytes = (uint32_t)(a.V * 2);
+  const int voff = tid * 16;
+  const uint16_t* logits = static_cast<const uint16_t*>(a.logits);
+  uint16_t* dl = static_cast<uint16_t*>(a.dl);
+  const PolicyConsts<float> c = PolicyConsts<float>::make(a.pp);
+
+  // Row indices fit in 32 bits (checked on the host); 32-bit division keeps the
+  // per-row address arithmetic short.
+  const uint32_t T32 = (uint32_t)a.T;
+  const uint32_t rows32 = (uint32_t)rows;
+  uint32_t r = blockIdx.x;
+  if (r >= rows32) return;
+
+  u32x4 x[SL];
+  {
+    const uint32_t b = r / T32, t = r - b * T32;
+    const __amdgpu_buffer_rsrc_t src =
+        row_rsrc(logits + (int64_t)b * a.ls_b + (int64_t)t * a.ls_t, row_bytes);
+#pragma unroll
+    for (int k = 0; k < SL; ++k)
+      x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
+  }
+
+  for (; r < rows32; r += gridDim.x) {
+    const uint32_t b = r / T32, t = r - b * T32;
+    // An opaque per-row copy of the lane id: the per-slab compares below are
+    // then recomputed each row instead of being hoisted (and spilled) as 2*SL
+    // loop-invariant masks.
+    int lane = tid;
+    asm volatile("" : "+v"(lane));
+    // Per-row scalars (uniform): issued before the sweep so their latency hides.
+    const int64_t tgt = load_index(a.tgt.ptr, a.tgt.dt, (int64_t)b * a.tgt.sr + (int64_t)t * a.tgt.sc);
+    const bool tgt_ok = tgt >= 0 && tgt < a.V;
+    // Slab k of this lane holds the target iff rel == k * RNT.
+    const int rel = tgt_ok ? (int)(tgt >> 3) - lane : -1;
+    const int ti = (int)(tgt & 7);
+    const float o = a.old.get<float>(b, t);
+    const float A = a.adv.get<float>(b, t);
+    const float w = mask_weight<float>(c, a.mask, b, t);
+    const float coef = static_cast<const float*>(a.row_coef)[b];
+
+    // Sweep 1: per-lane online (max, sum exp) over the resident slabs.
+    float m = -__builtin_huge_valf(), s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < SL; ++k) {
+      if (lane < nvec - k * RNT) {
+        float v[8];
+        Pack16<Tag>::unpack(x[k], v);
+        int skip = -1;
+        if (rel == k * RNT) {
+          skip = ti;
+          float xt = v[0];
+#pragma unroll
+          for (int i = 1; i < 8; ++i) xt = (i == ti) ? v[i] : xt;
+          sh_xt = xt;
+        }
+        online_update<float, 8>(m, s, v, skip);
+      }
+    }
+    if (!tgt_ok && tid == 0) sh_xt = __builtin_nanf("");
+    // Workgroup combine.  sh_xt is written before the first barrier and read
+    // before the second, so the next row's write cannot overtake a read.
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float m2 = __shfl_xor(m, off, 64);
+      const float s2 = __shfl_xor(s, off, 64);
+      online_merge(m, s, m2, s2);
+    }
+    if ((tid & 63) == 0) {
+      sh_m[tid >> 6] = m;
+      sh_s[tid >> 6] = s;
+    }
+    __syncthreads();
+    m = sh_m[0];
+    s = sh_s[0];
+#pragma unroll
+    for (int i = 1; i < RNT / 64; ++i) online_merge(m, s, sh_m[i], sh_s[i]);
+    const float xt = sh_xt;
+    __syncthreads();
+
+    // Opaque to the optimiser: sweep 2 re-expands the packed slabs instead of
+    // keeping sweep 1's widened copies live (twice the registers).
+#pragma unroll
+    for (int k = 0; k < SL; ++k) asm volatile("" : "+v"(x[k]));
+
+    const RowLogprob<float> fr = finish_row<float>(m, s, xt);
+    const float lse = fr.lse;
+    const float logp = tgt_ok ? fr.logp : __builtin_nanf("");
+    const float g = -((w * coef) * token_local_grad<float>(c, logp, o, A));
+    const float tgt_d = target_grad<float>(g, logp, true, xt, lse);
+    if (tid == 0) {
+      if (!tgt_ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+      store_as<float>(a.logp, a.logp_dt, r, logp);
+      static_cast<float*>(a.lse_out)[r] = lse;
+    }
+
+    // Sweep 2: dlogits, then refill the slab with the next row.
+    const uint32_t rn = r + gridDim.x;
+    const bool has_next = rn < rows32;
+    const uint32_t bn = rn / T32, tn = rn - bn * T32;
+    const __amdgpu_buffer_rsrc_t src = row_rsrc(
+        logits + (has_next ? (int64_t)bn * a.ls_b + (int64_t)tn * a.ls_t : 0),
+        has_next ? row_bytes : 0u);
+    const __amdgpu_buffer_rsrc_t dst =
+        row_rsrc(dl + (int64_t)b * a.ds_b + (int64_t)t * a.ds_t, row_bytes);
+    const bool zero_row = (g == 0.0f) && (lse - lse == 0.0f);
+    const float lse2 = lse * kLog2e;
+#pragma unroll
+    for (int k = 0; k < SL; ++k) {
+      float d[8];
+      if (zero_row) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d[i] = 0.0f;
+      } else {
+        float v[8];
+        Pack16<Tag>::unpack(x[k], v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d[i] = -g * exp2_hw(__builtin_fmaf(v[i], kLog2e, -lse2));
+        if (rel == k * RNT) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) d[i] = (i == ti) ? tgt_d : d[i];
+        }
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(Pack16<Tag>::pack(d), dst, voff, k * RNT * 16,
+                                             kAuxStoreNT);
+      if (has_next)
+        x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
+    }
+  }
+}
+
+// Variants by slab count; a row needs ceil(nvec / 1024) slabs.
+template <class Tag>
+int launch_resident(const RowArgs& a, int32_t nvec, hipStream_t stream) {
+  const int need = (nvec + RNT - 1) / RNT;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return check_launch("hipGetDevice");
+  static int cu_count[64] = {0};
+  if (dev < 0 || dev >= 64) dev = 0;
+  if (cu_count[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cu_count[dev] = n;
+  }
+  const int64_t rows = a.B * a.T;
+  const unsigned grid = (unsigned)(rows < cu_count[dev] ? rows : cu_count[dev]);
+#define RRL_RESIDENT_CASE(SLV)                                                                \
+  if (need <= SLV) {                                                                          \
+    hipLaunchKernelGGL((resident_fused_kernel<Tag, SLV>), dim3(grid), dim3(RNT), 0, stream, a, \
+                       nvec);                                                                 \
+    return check_launch("resident_fused_kernel");                                             \
+  }
+  RRL_RESIDENT_CASE(4)
+  RRL_RESIDENT_CASE(8)
+  RRL_RESIDENT_CASE(12)
+  RRL_RESIDENT_CASE(16)
+  RRL_RESIDENT_CASE(20)
+#undef RRL_RESIDENT_CASE
+  set_error("resident_fused_kernel: row too long");
+  return RRL_EINVAL;
+}
+
+constexpr int64_t kMaxResidentVec = 20 * RNT;  // SL = 20 fits 128 VGPRs without spills
+
+}  // namespace
+
+// Takes the fused single-pass call when the row fits the register budget and
+// every row of logits and dlogits is 16-byte aligned; otherwise leaves
+// *launched false so the caller runs the generic row kernel.
 int maybe_launch_resident(const RowArgs& a, int mode, int logits_dtype, hipStream_t stream,
                           bool* launched) {
-  (void)a; (void)mode; (void)logits_dtype; (void)stream;
   *launched = false;
-  return RRL_OK;
+  if (mode != 2) return RRL_OK;
+  if (logits_dtype != RRL_BF16 && logits_dtype != RRL_F16) return RRL_OK;
+  if (a.dl_dt != logits_dtype || a.accumulate) return RRL_OK;
+  if (a.B * a.T == 0 || a.V % 8 != 0 || a.V / 8 > kMaxResidentVec) return RRL_OK;
+  const auto al16 = [](int64_t elems) { return ((elems * 2) % 16) == 0; };
+  if (((uintptr_t)a.logits % 16) || ((uintptr_t)a.dl % 16)) return RRL_OK;
+  if (!al16(a.ls_b) || !al16(a.ls_t) || !al16(a.ds_b) || !al16(a.ds_t)) return RRL_OK;
+  if (a.logp_dt != RRL_F32) return RRL_OK;
+  if (a.B * a.T >= ((int64_t)1 << 31) || a.T >= ((int64_t)1 << 31)) return RRL_OK;
+  *launched = true;
+  const int32_t nvec = (int32_t)(a.V / 8);
+  return logits_dtype == RRL_BF16 ? launch_resident<TagBF16>(a, nvec, stream)
+                                  : launch_resident<TagF16>(a, nvec, stream);
 }
 
 }  // namespace rrl

@@ -14,9 +14,10 @@ struct RowArgs {
   void* logp;
   int logp_dt;
   void* lse_out;
-  // backward inputs
+  // backward inputs (logp_in may be null: the target column then uses lse)
   const void* lse;
   const void* g;
+  const void* logp_in;
   // dlogits
   void* dl;
   int dl_dt;
@@ -104,10 +105,13 @@ struct RowSplit {
 template <typename Acc>
 __device__ __forceinline__ Acc exp_diff(Acc x, Acc m) { return M<Acc>::fast_exp(x - m); }
 
-// Fold N new values into a running (max, sum exp(x - max)).  Values equal to
-// -inf contribute zero; NaN reaches the sum through exp.
+// Fold N new values into a running (max, sum exp(x - max)).  The max covers
+// every value; element `skip` (the target column, or -1 for none) is left out
+// of the sum so that the target's log-prob can be formed without cancellation
+// (finish_row).  Values equal to -inf contribute zero; NaN reaches the sum
+// through exp.
 template <typename Acc, int N>
-__device__ __forceinline__ void online_update(Acc& m, Acc& s, const Acc (&x)[N]) {
+__device__ __forceinline__ void online_update(Acc& m, Acc& s, const Acc (&x)[N], int skip) {
   Acc mc = x[0];
 #pragma unroll
   for (int i = 1; i < N; ++i) mc = fmax(mc, x[i]);
@@ -116,13 +120,49 @@ __device__ __forceinline__ void online_update(Acc& m, Acc& s, const Acc (&x)[N])
     m = mc;
   }
   if (m != -M<Acc>::inf()) {
+    if (skip < 0) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) s += exp_diff<Acc>(x[i], m);
+      for (int i = 0; i < N; ++i) s += exp_diff<Acc>(x[i], m);
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) s += (i == skip) ? Acc(0) : exp_diff<Acc>(x[i], m);
+    }
   } else {
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      if (x[i] != x[i]) s += x[i];
+      if (x[i] != x[i] && i != skip) s += x[i];
   }
+}
+
+// Row log-sum-exp and target log-prob from the row max M (over all columns),
+// S_other = sum over the non-target columns of exp(x - M), and the target
+// logit xt.  With e_t = exp(xt - M):
+//   lse  = M + log(S_other + e_t)
+//   logp = -log1p(S_other / e_t)          when xt is within 1 of the max,
+//          (xt - M) - log(S_other + e_t)  otherwise.
+// The first form keeps full relative precision as logp -> 0 (a dominant
+// target), where xt - lse would cancel.  An all -inf row gives NaN, as
+// log_softmax does; NaN or +inf anywhere in the row gives NaN.
+template <typename Acc>
+struct RowLogprob {
+  Acc lse, logp;
+};
+
+template <typename Acc>
+__device__ __forceinline__ RowLogprob<Acc> finish_row(Acc Mx, Acc S_other, Acc xt) {
+  // Branch-free: both forms are evaluated and selected, which keeps the
+  // results in registers.
+  const bool empty = Mx == -M<Acc>::inf();
+  const Acc dt = xt - Mx;
+  const Acc et = M<Acc>::exp(dt);
+  const Acc S = S_other + et;
+  const Acc lse = Mx + M<Acc>::log(S);
+  const Acc near = -M<Acc>::log1p(S_other / et);
+  const Acc far = dt - M<Acc>::log(S);
+  RowLogprob<Acc> r;
+  r.lse = empty ? -M<Acc>::inf() : ((S != S) ? M<Acc>::nan() : lse);
+  r.logp = empty ? M<Acc>::nan() : ((dt > Acc(-1)) ? near : far);
+  return r;
 }
 
 template <typename Acc>
@@ -186,14 +226,17 @@ __device__ __forceinline__ void store_run(void* drow, int dt, int64_t col, const
   for (int i = 0; i < N; ++i) store_as<Acc>(drow, dt, col + i, d[i]);
 }
 
-// Sweep 2 over one row: d[v] = ([v == target] ? g : 0) - exp(x[v] - lse) * g,
-// the composition of gather's and log_softmax's backward (losses.py:34-38).
+// Sweep 2 over one row: d[v] = -g * exp(x[v] - lse) for v != target and
+// d[target] = tgt_d, the composition of gather's and log_softmax's backward
+// (losses.py:34-38).  The caller forms tgt_d = g * (1 - p_target) as
+// -g * expm1(logp) so that it keeps its relative precision when p_target -> 1.
 // zero_row skips reading the logits (g == 0 and a finite lse give exact zeros).
 template <class Tag, int NT>
 __device__ __forceinline__ void write_row_grad(const typename Tag::S* row, const RowSplit& sp,
                                                void* drow, int dl_dt, int64_t V, int64_t target,
                                                typename Tag::Acc g, typename Tag::Acc lse,
-                                               bool zero_row, int accumulate) {
+                                               typename Tag::Acc tgt_d, bool zero_row,
+                                               int accumulate) {
   using Acc = typename Tag::Acc;
   constexpr int VEC = Tag::VEC;
   const int osz = dtype_size_dev(dl_dt);
@@ -202,8 +245,7 @@ __device__ __forceinline__ void write_row_grad(const typename Tag::S* row, const
   const bool vec_ok = !accumulate && (body_addr % (uintptr_t)need) == 0;
 
   auto elem = [&](int64_t col, Acc x) -> Acc {
-    const Acc pg = M<Acc>::fast_exp(x - lse) * g;
-    Acc d = (col == target ? g : Acc(0)) - pg;
+    Acc d = (col == target) ? tgt_d : -(M<Acc>::fast_exp(x - lse) * g);
     if (accumulate) d += load_as<Acc>(drow, dl_dt, col);
     return d;
   };
@@ -232,6 +274,14 @@ __device__ __forceinline__ void write_row_grad(const typename Tag::S* row, const
     Acc d[1] = {zero_row ? Acc(0) : elem(tail0 + i, Tag::cvt(row[tail0 + i]))};
     store_run<Acc, 1>(drow, dl_dt, tail0 + i, d, false);
   }
+}
+
+// Target-column gradient g * (1 - p_target).  With the row's log-prob at hand
+// it is -g * expm1(logp); otherwise it falls back to g - g * exp(xt - lse).
+template <typename Acc>
+__device__ __forceinline__ Acc target_grad(Acc g, Acc logp, bool have_logp, Acc xt, Acc lse) {
+  if (have_logp) return -(g * M<Acc>::expm1(logp));
+  return g - M<Acc>::exp(xt - lse) * g;
 }
 
 }  // namespace rrl

@@ -154,6 +154,8 @@ template <typename T> struct M;
 template <> struct M<float> {
   static __device__ __forceinline__ float exp(float x) { return expf(x); }
   static __device__ __forceinline__ float log(float x) { return logf(x); }
+  static __device__ __forceinline__ float log1p(float x) { return log1pf(x); }
+  static __device__ __forceinline__ float expm1(float x) { return expm1f(x); }
   // v_exp_f32-based; used in the vocabulary sweeps where ~2 ulp is ample.
   static __device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
   static __device__ __forceinline__ float sqrt(float x) { return __fsqrt_rn(x); }
@@ -164,6 +166,8 @@ template <> struct M<double> {
   static __device__ __forceinline__ double exp(double x) { return ::exp(x); }
   static __device__ __forceinline__ double fast_exp(double x) { return ::exp(x); }
   static __device__ __forceinline__ double log(double x) { return ::log(x); }
+  static __device__ __forceinline__ double log1p(double x) { return ::log1p(x); }
+  static __device__ __forceinline__ double expm1(double x) { return ::expm1(x); }
   static __device__ __forceinline__ double sqrt(double x) { return ::sqrt(x); }
   static __device__ __forceinline__ double inf() { return __builtin_huge_val(); }
   static __device__ __forceinline__ double nan() { return __builtin_nan(""); }

@@ -126,7 +126,9 @@ class _TokenLogprobs(torch.autograd.Function):
         )
         if B * T and nat.read_status(status) & nat.FLAG_TARGET_RANGE:
             _raise_target_range()
-        ctx.save_for_backward(x, tkeep, lse)
+        # The backward forms the target column from logp (-g * expm1(logp)); a
+        # private copy keeps it independent of in-place edits to the output.
+        ctx.save_for_backward(x, tkeep, lse, logp.clone())
         ctx.meta = (B, T, V, s_b, s_t, tuple(logits.shape), logits.dtype)
         ctx.set_materialize_grads(False)
         return logp.view(logits.shape[:-1])
@@ -135,15 +137,15 @@ class _TokenLogprobs(torch.autograd.Function):
     def backward(ctx, grad: Optional[Tensor]):
         if grad is None or not ctx.needs_input_grad[0]:
             return None, None
-        x, tkeep, lse = ctx.saved_tensors
+        x, tkeep, lse, logp = ctx.saved_tensors
         B, T, V, s_b, s_t, shape, dtype = ctx.meta
         g = grad.reshape(-1).to(lse.dtype).contiguous()
         dl = torch.empty(shape, dtype=dtype, device=x.device)
         tview, _ = nat.rows_view(tkeep, B, T)
         nat.call(
             "rrl_logprob_bwd", x.data_ptr(), nat.dtype_code(x.dtype), B, T, V, s_b, s_t, tview,
-            lse.data_ptr(), g.data_ptr(), dl.data_ptr(), nat.dtype_code(dtype), T * V, V, 0,
-            nat.stream_ptr(x.device),
+            lse.data_ptr(), logp.data_ptr(), g.data_ptr(), dl.data_ptr(), nat.dtype_code(dtype),
+            T * V, V, 0, nat.stream_ptr(x.device),
         )
         return dl, None
 
@@ -793,8 +795,8 @@ class _FusedPolicy(torch.autograd.Function):
         out = dl if dl is not None else torch.empty((B, T, V), dtype=dtype, device=dev)
         tview, _ = nat.rows_view(tkeep, B, T)
         nat.call("rrl_logprob_bwd", x.data_ptr(), nat.dtype_code(x.dtype), B, T, V, s_b, s_t,
-                 tview, lse.data_ptr(), g.data_ptr(), out.data_ptr(), nat.dtype_code(dtype),
-                 T * V, V, 0, stream)
+                 tview, lse.data_ptr(), logp.data_ptr(), g.data_ptr(), out.data_ptr(),
+                 nat.dtype_code(dtype), T * V, V, 0, stream)
         ctx.dl = None
         return (*nones, out.view(shape), None, None, None, None)
 

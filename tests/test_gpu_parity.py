@@ -1,8 +1,14 @@
 """HIP path vs the CPU oracle on identical seeded inputs (MI355X).
 
 Tolerances (north star): float32 results within 1e-5 relative, bf16-input
-log-probs and losses within 2e-3 relative; bf16 dlogits by per-row norm-wise
-relative error (an element-wise 2e-3 bound is below bf16's own rounding step).
+log-probs and losses within 2e-3 relative; 16-bit dlogits within 2e-3 by
+per-row norm-wise relative error (an element-wise 2e-3 bound is below bf16's
+own rounding step of 2^-8), and every 16-bit element within one ulp of the
+correctly rounded exact value.  Log-probs and dlogits are held against the
+float64 evaluation of the reference's math on exact upcasts of the same
+inputs (``exact=True``): a float32 evaluation, the reference's own, carries
+cancellation error of several float32 ulps of the row log-sum-exp where
+log p -> 0, which a 1e-5 relative bound cannot absorb.
 Index, mask and alignment outputs are compared bit-exactly, except decisions
 whose oracle ratio sits within float32 rounding of a threshold (excluded by
 distance, reported by count).
@@ -32,9 +38,15 @@ def _close(got, want, rtol, atol, what=""):
     err = (got - want).abs()
     bound = atol + rtol * want.abs()
     bad = ~(err <= bound) & ~(torch.isnan(got) & torch.isnan(want))
-    assert not bad.any(), (
-        f"{what}: {int(bad.sum())} of {got.numel()} outside tol; max err {err.max().item():.3e}"
-    )
+    if bad.any():
+        excess = torch.where(bad, err / bound.clamp_min(1e-300), torch.zeros_like(err))
+        i = int(excess.reshape(-1).argmax())
+        idx = np.unravel_index(i, tuple(got.shape)) if got.dim() else ()
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} of {got.numel()} outside tol; worst at {idx}: "
+            f"got {got.reshape(-1)[i].item():.9g} want {want.reshape(-1)[i].item():.9g} "
+            f"(err {err.reshape(-1)[i].item():.3e}, bound {bound.reshape(-1)[i].item():.3e})"
+        )
 
 
 def _rownorm(got, want, tol, what=""):
@@ -117,22 +129,23 @@ def test_logprob_forward_backward(device, dtype, V, B, T):
     lp = R.gather_token_logprobs(xd, t.to(device))
     acc = torch.float64 if dtype == torch.float64 else torch.float32
     assert lp.dtype == acc
-    xo = (x.float() if dtype in (torch.bfloat16, torch.float16) else x.clone()).requires_grad_()
-    lpo = o.token_logprobs(xo, t)
+    xo = x.double().requires_grad_()
+    lpo = o.token_logprobs(xo, t, exact=True)
     rtol = 1e-12 if dtype == torch.float64 else F32_RTOL
-    _close(lp, lpo, rtol, 1e-6 if dtype != torch.float64 else 1e-12, "logp")
+    _close(lp, lpo, rtol, 1e-7 if dtype != torch.float64 else 1e-12, "logp")
 
     (lp * up.to(device).to(acc)).sum().backward()
-    (lpo * up.to(acc)).sum().backward()
+    (lpo * up).sum().backward()
     dl, dlo = xd.grad, xo.grad
     assert dl.dtype == dtype and dl.shape == x.shape
     if dtype in (torch.bfloat16, torch.float16):
         exact = _ulp16(dl, dlo, "dlogits")
         assert exact > 0.98, exact
-        _rownorm(dl, dlo, 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11, "dlogits")
+        _rownorm(dl, dlo, 2e-3 if dtype == torch.bfloat16 else 2.0 ** -11, "dlogits")
+    elif dtype == torch.float64:
+        _close(dl, dlo, 1e-12, 1e-14, "dlogits")
     else:
-        _close(dl, dlo, 1e-12 if dtype == torch.float64 else F32_RTOL,
-               1e-14 if dtype == torch.float64 else 1e-7, "dlogits")
+        _close_rows_by_g(dl, dlo, up, F32_RTOL, "dlogits")
 
 
 def test_logprob_causal_shift_views(device):
@@ -144,9 +157,9 @@ def test_logprob_causal_shift_views(device):
     ids = torch.randint(0, V, (B, S), generator=g)
     xd = x.to(device).requires_grad_()
     lp = R.gather_token_logprobs(xd[:, :-1], ids.to(device)[:, 1:])
-    xo = x.clone().requires_grad_()
-    lpo = o.token_logprobs(xo[:, :-1], ids[:, 1:])
-    _close(lp, lpo, F32_RTOL, 1e-6, "shifted logp")
+    xo = x.double().requires_grad_()
+    lpo = o.token_logprobs(xo[:, :-1], ids[:, 1:], exact=True)
+    _close(lp, lpo, F32_RTOL, 1e-7, "shifted logp")
     lp.sum().backward()
     lpo.sum().backward()
     _close(xd.grad, xo.grad, F32_RTOL, 1e-7, "shifted dlogits")
@@ -157,7 +170,7 @@ def test_logprob_int32_targets_and_rank2(device):
     x = torch.randn(17, 129, generator=g)
     t = torch.randint(0, 129, (17,), generator=g, dtype=torch.int32)
     lp = R.gather_token_logprobs(x.to(device), t.to(device))
-    _close(lp, o.token_logprobs(x, t), F32_RTOL, 1e-6, "rank-2 logp")
+    _close(lp, o.token_logprobs(x, t, exact=True), F32_RTOL, 1e-7, "rank-2 logp")
 
 
 def test_logprob_target_out_of_range_raises(device):
@@ -534,8 +547,8 @@ def test_fused_matches_oracle(device, objective, dtype, V):
                                   **kw)
     out.loss.backward()
     kind = {"clipped": "ppo"}.get(objective, objective)
-    out_o, lpo, dlo = o.policy_step(kind, x, t, old, a, mask, **kw)
-    _close(lp, lpo, F32_RTOL, 1e-6, "logp")
+    out_o, lpo, dlo = o.policy_step(kind, x, t, old, a, mask, exact=True, **kw)
+    _close(lp, lpo, F32_RTOL, 1e-7, "logp")
     # The loss is a signed sum of per-token terms of size ~|A| that largely
     # cancel (group-standardized A has mean 0), so its relative tolerance is
     # taken against the terms' scale, not the near-zero sum.
@@ -547,7 +560,7 @@ def test_fused_matches_oracle(device, objective, dtype, V):
         _close_rows_by_g(xd.grad, dlo, out_o["dloss_dlogp"], F32_RTOL, "dlogits")
     else:
         assert _ulp16(xd.grad, dlo, "dlogits") > 0.98
-        _rownorm(xd.grad, dlo, 2.0 ** -8, "dlogits")
+        _rownorm(xd.grad, dlo, 2e-3, "dlogits")
 
 
 def test_fused_equals_composition_and_grad_scaling(device):
@@ -586,3 +599,32 @@ def test_fused_inplace(device):
                                 objective="sapo", inplace=True)
     _close(out_i.loss, out_r.loss, 1e-6, 1e-8, "inplace loss")
     assert torch.equal(buf.detach().cpu(), ref.grad.cpu()), "in-place dlogits differ"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("objective", ["clipped", "sao", "sapo"])
+def test_fused_many_rows_persistent(device, dtype, objective):
+    """More rows than workgroups: every workgroup carries several rows and
+    prefetches the next one into its registers (16-bit resident path).  V =
+    20000 leaves the last register slab of each row partially filled."""
+
+    print(f"[fused-many] objective={objective} dtype={dtype}", flush=True)
+    B, T, V = 64, 40, 20000
+    x, t, old, adv, mask = _fused_inputs(34, B, T, V, dtype)
+    kw = {"clipped": dict(clip_low=0.2, clip_high=0.28),
+          "sao": dict(clip_low=0.2, clip_high=0.28),
+          "sapo": dict(tau_positive=1.0, tau_negative=1.05)}[objective]
+    xd = x.to(device).requires_grad_()
+    out, lp = R.fused_policy_loss(xd, t.to(device), old.to(device), adv.to(device),
+                                  mask.to(device), objective=objective, return_logprobs=True,
+                                  **kw)
+    out.loss.backward()
+    kind = {"clipped": "ppo"}.get(objective, objective)
+    out_o, lpo, dlo = o.policy_step(kind, x, t, old, adv, mask, exact=True, **kw)
+    _close(lp, lpo, F32_RTOL, 1e-7, "logp")
+    scale = max(abs(out_o["loss"].item()), adv.abs().mean().item())
+    assert abs(out.loss.item() - out_o["loss"].item()) <= 2e-3 * scale
+    assert _ulp16(xd.grad, dlo, "dlogits") > 0.98
+    _rownorm(xd.grad, dlo, 2e-3, "dlogits")
+    # masked rows carry exactly zero gradient
+    assert torch.count_nonzero(xd.grad[~mask.to(device)]).item() == 0
