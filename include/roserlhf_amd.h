@@ -69,7 +69,16 @@ enum rrl_flag {
   RRL_FLAG_EMPTY_MASK = 1,       /* global mask weight sum is zero        (losses.py:48-49)   */
   RRL_FLAG_EMPTY_ROW = 2,        /* some row has no action token          (losses.py:250-251) */
   RRL_FLAG_TARGET_RANGE = 4,     /* target id outside [0, V)              (gather, losses.py:36) */
-  RRL_FLAG_INVALID_TURN = 8      /* unmasked token with invalid turn id   (advantages.py:284-286) */
+  RRL_FLAG_INVALID_TURN = 8,     /* unmasked token with invalid turn id   (advantages.py:284-286) */
+  RRL_FLAG_FAST_RANGE = 16       /* rrl_fused_logprob_policy's 16-bit register-resident kernel met a
+                                    row with finite |log-sum-exp| > 2e38, outside its exponent range;
+                                    that call's outputs are undefined: rerun it with
+                                    RRL_POLICY_GENERIC set (no reference counterpart) */
+};
+
+/* rrl_policy_params.flags bits. */
+enum rrl_policy_flag {
+  RRL_POLICY_GENERIC = 1 /* rrl_fused_logprob_policy: use the generic row kernel only */
 };
 
 /* Policy objectives (losses.py). */
@@ -103,7 +112,7 @@ typedef struct rrl_policy_params {
   int32_t detach_ratio;  /* SAO only (losses.py:185) */
   int32_t mask_is_weight;/* 1: mask is cast to the value dtype and used as a
                             weight (masked_mean, losses.py:46); 0: mask != 0 */
-  int32_t reserved;
+  int32_t flags;         /* rrl_policy_flag bits */
   double clip_low;       /* thresholds are formed as acc(1 - clip_low) etc. */
   double clip_high;
   double max_log_ratio;

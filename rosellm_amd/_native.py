@@ -38,6 +38,10 @@ FLAG_EMPTY_MASK = 1
 FLAG_EMPTY_ROW = 2
 FLAG_TARGET_RANGE = 4
 FLAG_INVALID_TURN = 8
+FLAG_FAST_RANGE = 16
+
+# rrl_policy_flag
+POLICY_GENERIC = 1
 
 # rrl_objective
 OBJ_PPO, OBJ_SAO, OBJ_GSPO, OBJ_GSPO_TOKEN, OBJ_SAPO = range(5)
@@ -58,7 +62,7 @@ class RrlPolicyParams(ctypes.Structure):
         ("kind", ctypes.c_int32),
         ("detach_ratio", ctypes.c_int32),
         ("mask_is_weight", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
         ("clip_low", ctypes.c_double),
         ("clip_high", ctypes.c_double),
         ("max_log_ratio", ctypes.c_double),
@@ -139,9 +143,8 @@ def time_calls(*names: str) -> dict:
     Returns the live name -> [(start, end), ...] mapping; ``time_calls()``
     with no names stops recording."""
 
-    _timed.clear()
-    for n in names:
-        _timed[n] = []
+    global _timed
+    _timed = {n: [] for n in names}
     return _timed
 
 

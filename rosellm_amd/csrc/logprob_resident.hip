@@ -133,22 +133,38 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     const float w = mask_weight<float>(c, a.mask, b, t);
     const float coef = static_cast<const float*>(a.row_coef)[b];
 
-    // Sweep 1: per-lane online (max, sum exp) over the resident slabs.
+    // Sweep 1: per-lane online (max, sum exp) over the resident slabs.  The
+    // running max starts at -inf; `mg` (the max as an exponent offset) is
+    // kept finite so that slabs of -inf contribute exp(-inf) = 0 rather than
+    // exp(-inf + inf) = NaN, while NaN and +inf still poison the row as in
+    // log_softmax.  The target column is left out of the sum in the one lane
+    // and slab that hold it.
     float m = -__builtin_huge_valf(), s = 0.0f;
 #pragma unroll
     for (int k = 0; k < SL; ++k) {
       if (lane < nvec - k * RNT) {
         float v[8];
         Pack16<Tag>::unpack(x[k], v);
-        int skip = -1;
-        if (rel == k * RNT) {
-          skip = ti;
-          float xt = v[0];
+        const float mc = fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])),
+                               fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
+        const float mn = fmaxf(m, mc);
+        const float mg = fmaxf(mn, -__FLT_MAX__);
+        float e[8];
 #pragma unroll
-          for (int i = 1; i < 8; ++i) xt = (i == ti) ? v[i] : xt;
+        for (int i = 0; i < 8; ++i) e[i] = exp2_hw((v[i] - mg) * kLog2e);
+        float s8 = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+        if (rel == k * RNT) {
+          float xt = v[0], so = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            xt = (i == ti) ? v[i] : xt;
+            so += (i == ti) ? 0.0f : e[i];
+          }
+          s8 = so;
           sh_xt = xt;
         }
-        online_update<float, 8>(m, s, v, skip);
+        s = __builtin_fmaf(s, exp2_hw((m - mg) * kLog2e), s8);
+        m = mn;
       }
     }
     if (!tgt_ok && tid == 0) sh_xt = __builtin_nanf("");
@@ -198,7 +214,19 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     const __amdgpu_buffer_rsrc_t dst =
         row_rsrc(dl + (int64_t)b * a.ds_b + (int64_t)t * a.ds_t, row_bytes);
     const bool zero_row = (g == 0.0f) && (lse - lse == 0.0f);
-    const float lse2 = lse * kLog2e;
+    // lse * log2e overflows for finite |lse| > 2.3e38 (logits near the 16-bit
+    // maximum): such a row is flagged and the host reruns the call on the
+    // generic kernel.  Non-finite lse needs no care: NaN propagates as in
+    // log_softmax.
+    if (tid == 0 && fabsf(lse) > 2e38f && fabsf(lse) != __builtin_huge_valf())
+      raise_flag(a.status, RRL_FLAG_FAST_RANGE);
+    // -g * exp(x - lse) = -sign(g) * exp2(x*log2e + (log2|g| - lse*log2e)):
+    // one FMA and one v_exp_f32 per element; the sign is applied to the packed
+    // 16-bit words with one XOR per two elements.
+    const float cg = __log2f(fabsf(g)) - lse * kLog2e;
+    const bool flip = g > 0.0f;
+    const uint32_t sgn = flip ? 0x80008000u : 0u;
+    const float tgt_pre = flip ? -tgt_d : tgt_d;  // the XOR restores tgt_d
 #pragma unroll
     for (int k = 0; k < SL; ++k) {
       float d[8];
@@ -209,16 +237,20 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
         float v[8];
         Pack16<Tag>::unpack(x[k], v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) d[i] = -g * exp2_hw(__builtin_fmaf(v[i], kLog2e, -lse2));
+        for (int i = 0; i < 8; ++i) d[i] = exp2_hw(__builtin_fmaf(v[i], kLog2e, cg));
         if (rel == k * RNT) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) d[i] = (i == ti) ? tgt_d : d[i];
+          for (int i = 0; i < 8; ++i) d[i] = (i == ti) ? tgt_pre : d[i];
         }
       }
-      __builtin_amdgcn_raw_buffer_store_b128(Pack16<Tag>::pack(d), dst, voff, k * RNT * 16,
-                                             kAuxStoreNT);
+      u32x4 o = Pack16<Tag>::pack(d);
+      o.x ^= sgn; o.y ^= sgn; o.z ^= sgn; o.w ^= sgn;
+      __builtin_amdgcn_raw_buffer_store_b128(o, dst, voff, k * RNT * 16, kAuxStoreNT);
       if (has_next)
         x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
+      // Keep slab k's refill after its own store: hoisting the next row's loads
+      // above earlier slabs would hold two rows in registers.
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -265,7 +297,7 @@ constexpr int64_t kMaxResidentVec = 20 * RNT;  // SL = 20 fits 128 VGPRs without
 int maybe_launch_resident(const RowArgs& a, int mode, int logits_dtype, hipStream_t stream,
                           bool* launched) {
   *launched = false;
-  if (mode != 2) return RRL_OK;
+  if (mode != 2 || (a.pp.flags & RRL_POLICY_GENERIC)) return RRL_OK;
   if (logits_dtype != RRL_BF16 && logits_dtype != RRL_F16) return RRL_OK;
   if (a.dl_dt != logits_dtype || a.accumulate) return RRL_OK;
   if (a.B * a.T == 0 || a.V % 8 != 0 || a.V / 8 > kMaxResidentVec) return RRL_OK;

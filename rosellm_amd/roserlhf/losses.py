@@ -712,10 +712,6 @@ class _FusedPolicy(torch.autograd.Function):
         ws = torch.empty(nat.lib().rrl_policy_workspace_bytes(B, acc_code), dtype=torch.uint8,
                          device=dev)
         coef = torch.empty(B, dtype=acc, device=dev)
-        status = nat.new_status(dev)
-        pref = ctypes_ref(params)
-        nat.call("rrl_policy_row_coef", pref, B, T, mv, acc_code, coef.data_ptr(), ws.data_ptr(),
-                 status.data_ptr(), stream)
         logp = torch.empty(B * T, dtype=acc, device=dev)
         lse = torch.empty(B * T, dtype=acc, device=dev)
         if inplace:
@@ -723,17 +719,38 @@ class _FusedPolicy(torch.autograd.Function):
         else:
             dl = torch.empty((B, T, V), dtype=logits.dtype, device=dev)
             d_b, d_t = T * V, V
-        nat.call("rrl_fused_logprob_policy", pref, x.data_ptr(), nat.dtype_code(x.dtype), B, T,
-                 V, s_b, s_t, tview, ov, av, mv, coef.data_ptr(), logp.data_ptr(),
-                 lse.data_ptr(), dl.data_ptr(), nat.dtype_code(logits.dtype), d_b, d_t,
-                 status.data_ptr(), stream)
         scal = torch.empty(nat.NSCALARS, dtype=acc, device=dev)
         trusted = torch.empty(B * T if kind == nat.OBJ_SAO else 0, dtype=torch.bool, device=dev)
         lview = nat.RrlView(logp.data_ptr(), acc_code, T, 1)
-        nat.call("rrl_policy_fwd", pref, B, T, lview, ov, av, mv, acc_code, ws.data_ptr(),
-                 scal.data_ptr(), None, nat.ptr(trusted) if trusted.numel() else None,
-                 status.data_ptr(), stream)
-        _raise_flags(nat.read_status(status), kind)
+
+        def run(p):
+            status = nat.new_status(dev)
+            pref = ctypes_ref(p)
+            nat.call("rrl_policy_row_coef", pref, B, T, mv, acc_code, coef.data_ptr(),
+                     ws.data_ptr(), status.data_ptr(), stream)
+            nat.call("rrl_fused_logprob_policy", pref, x.data_ptr(), nat.dtype_code(x.dtype), B,
+                     T, V, s_b, s_t, tview, ov, av, mv, coef.data_ptr(), logp.data_ptr(),
+                     lse.data_ptr(), dl.data_ptr(), nat.dtype_code(logits.dtype), d_b, d_t,
+                     status.data_ptr(), stream)
+            nat.call("rrl_policy_fwd", pref, B, T, lview, ov, av, mv, acc_code, ws.data_ptr(),
+                     scal.data_ptr(), None, nat.ptr(trusted) if trusted.numel() else None,
+                     status.data_ptr(), stream)
+            return nat.read_status(status)
+
+        flags = run(params)
+        if flags & nat.FLAG_FAST_RANGE:
+            # A row's log-sum-exp lies beyond the 16-bit fast kernel's exponent
+            # range (logits near the format's maximum): redo the call on the
+            # generic row kernel.
+            if inplace:
+                raise RuntimeError(
+                    "fused_policy_loss(inplace=True): logits beyond +-2e38 need the generic "
+                    "kernel, which cannot rerun over overwritten logits; call with inplace=False"
+                )
+            generic = nat.RrlPolicyParams.from_buffer_copy(params)
+            generic.flags |= nat.POLICY_GENERIC
+            flags = run(generic)
+        _raise_flags(flags, kind)
 
         ctx.params = params
         ctx.inplace = inplace

@@ -1,10 +1,13 @@
 """HIP path vs the CPU oracle on identical seeded inputs (MI355X).
 
 Tolerances (north star): float32 results within 1e-5 relative, bf16-input
-log-probs and losses within 2e-3 relative; 16-bit dlogits within 2e-3 by
-per-row norm-wise relative error (an element-wise 2e-3 bound is below bf16's
-own rounding step of 2^-8), and every 16-bit element within one ulp of the
-correctly rounded exact value.  Log-probs and dlogits are held against the
+log-probs and losses within 2e-3 relative.  16-bit dlogits: every element
+within one ulp of the correctly rounded exact value (at least 98% of them
+bit-identical to it), and each row within 2e-3 norm-wise relative error of
+that correctly rounded row.  The rounded row is the reference point because
+bf16's unit roundoff is 2^-8 = 3.9e-3: a correctly rounded row whose norm is
+carried by one element (the target column) can itself sit 3.5e-3 from the
+exact values, and f16 flushes whole rows of ~1e-9 gradients to zero.  Log-probs and dlogits are held against the
 float64 evaluation of the reference's math on exact upcasts of the same
 inputs (``exact=True``): a float32 evaluation, the reference's own, carries
 cancellation error of several float32 ulps of the row log-sum-exp where
@@ -57,6 +60,21 @@ def _rownorm(got, want, tol, what=""):
     rel = torch.where(den > 0, num / den.clamp_min(1e-30), num)
     assert rel.max().item() <= tol, f"{what}: worst row-norm rel err {rel.max().item():.3e}"
     return rel.max().item()
+
+
+def _rownorm16(got, want_exact, tol=2e-3, what=""):
+    """16-bit rows against the correctly rounded exact rows (see module doc);
+    prints the distance to the unrounded values for the record."""
+
+    rounded = want_exact.detach().cpu().float().to(got.dtype)
+    worst = _rownorm(got, rounded, tol, what)
+    g = got.detach().double().cpu().reshape(-1, got.shape[-1])
+    w = want_exact.detach().double().cpu().reshape(-1, got.shape[-1])
+    den = w.norm(dim=-1)
+    vs_exact = torch.where(den > 0, (g - w).norm(dim=-1) / den.clamp_min(1e-30), den * 0)
+    print(f"{what}: worst row-norm rel err vs rounded {worst:.3e}, vs exact "
+          f"{vs_exact.max().item():.3e}", flush=True)
+    return worst
 
 
 def _close_rows_by_g(got, want, g, rtol, what=""):
@@ -141,7 +159,7 @@ def test_logprob_forward_backward(device, dtype, V, B, T):
     if dtype in (torch.bfloat16, torch.float16):
         exact = _ulp16(dl, dlo, "dlogits")
         assert exact > 0.98, exact
-        _rownorm(dl, dlo, 2e-3 if dtype == torch.bfloat16 else 2.0 ** -11, "dlogits")
+        _rownorm16(dl, dlo, 2e-3, "dlogits")
     elif dtype == torch.float64:
         _close(dl, dlo, 1e-12, 1e-14, "dlogits")
     else:
@@ -560,7 +578,7 @@ def test_fused_matches_oracle(device, objective, dtype, V):
         _close_rows_by_g(xd.grad, dlo, out_o["dloss_dlogp"], F32_RTOL, "dlogits")
     else:
         assert _ulp16(xd.grad, dlo, "dlogits") > 0.98
-        _rownorm(xd.grad, dlo, 2e-3, "dlogits")
+        _rownorm16(xd.grad, dlo, 2e-3, "dlogits")
 
 
 def test_fused_equals_composition_and_grad_scaling(device):
@@ -625,6 +643,41 @@ def test_fused_many_rows_persistent(device, dtype, objective):
     scale = max(abs(out_o["loss"].item()), adv.abs().mean().item())
     assert abs(out.loss.item() - out_o["loss"].item()) <= 2e-3 * scale
     assert _ulp16(xd.grad, dlo, "dlogits") > 0.98
-    _rownorm(xd.grad, dlo, 2e-3, "dlogits")
+    _rownorm16(xd.grad, dlo, 2e-3, "dlogits")
     # masked rows carry exactly zero gradient
     assert torch.count_nonzero(xd.grad[~mask.to(device)]).item() == 0
+
+
+def test_fused_extreme_logits(device):
+    """Rows at the edge of the 16-bit range: an all -inf row but one entry, a
+    half -inf (masked vocabulary) row, and a row whose log-sum-exp (3e38)
+    exceeds the register-resident kernel's exponent range, which the host then
+    reruns on the generic kernel.  All must match the float64 oracle."""
+
+    B, T, V = 2, 8, 4096
+    x, t, old, adv, mask = _fused_inputs(35, B, T, V, torch.bfloat16)
+    xf = x.float()
+    xf[0, 1, :] = -float("inf")
+    xf[0, 1, 5] = 0.0
+    t[0, 1] = 5
+    xf[0, 2, : V // 2] = -float("inf")
+    t[0, 2] = V - 3
+    xf[1, 3, 7] = 3.0e38
+    t[1, 3] = 7
+    xf[1, 4, 9] = 3.0e38
+    t[1, 4] = 11  # log-prob of about -3e38: the ratio clamps at max_log_ratio
+    x = xf.to(torch.bfloat16)
+    mask[:, :6] = True
+    old = o.token_logprobs(x, t, exact=True).float() + 0.05
+    old[1, 4] = -5.0
+    kw = dict(clip_low=0.2, clip_high=0.28)
+    xd = x.to(device).requires_grad_()
+    out, lp = R.fused_policy_loss(xd, t.to(device), old.to(device), adv.to(device),
+                                  mask.to(device), return_logprobs=True, **kw)
+    out.loss.backward()
+    out_o, lpo, dlo = o.policy_step("ppo", x, t, old, adv, mask, exact=True, **kw)
+    _close(lp, lpo, F32_RTOL, 1e-7, "logp")
+    scale = max(abs(out_o["loss"].item()), adv.abs().mean().item())
+    assert abs(out.loss.item() - out_o["loss"].item()) <= 2e-3 * scale
+    assert _ulp16(xd.grad, dlo, "dlogits") > 0.98
+    _rownorm16(xd.grad, dlo, 2e-3, "dlogits")
