@@ -181,16 +181,21 @@ RRL_API int rrl_policy_bwd(const rrl_policy_params* params, int64_t B, int64_t T
  * lse and dlogits = d(-objective)/d logits.  rrl_policy_row_coef first writes
  * row_coef[b] (acc, [B]): 1/sum(mask weight) for PPO/SAO, 1/(B*L_b) for SAPO,
  * and flags EMPTY_MASK / EMPTY_ROW.  The objective scalars then come from
- * rrl_policy_fwd on the returned logp. */
+ * rrl_policy_fwd on the returned logp.
+ * records: caller workspace of rrl_fused_records_bytes(B, T) bytes, where the
+ * 16-bit fast path packs each token's target, old log-prob, advantage and
+ * mask weight * row_coef (16 bytes per token) for one scalar load per row. */
 RRL_API int rrl_policy_row_coef(const rrl_policy_params* params, int64_t B, int64_t T,
                         rrl_view mask, int32_t acc_dtype, void* row_coef,
                         void* workspace, int32_t* status, void* stream);
+
+RRL_API size_t rrl_fused_records_bytes(int64_t B, int64_t T);
 
 RRL_API int rrl_fused_logprob_policy(const rrl_policy_params* params, const void* logits,
                              int32_t logits_dtype, int64_t B, int64_t T, int64_t V,
                              int64_t ls_b, int64_t ls_t, rrl_view targets, rrl_view old,
                              rrl_view adv, rrl_view mask, const void* row_coef,
-                             void* logp_out, void* lse_out, void* dlogits,
+                             void* records, void* logp_out, void* lse_out, void* dlogits,
                              int32_t dl_dtype, int64_t ds_b, int64_t ds_t,
                              int32_t* status, void* stream);
 

@@ -203,9 +203,10 @@ extern "C" int rrl_fused_logprob_policy(const rrl_policy_params* params, const v
                                         int32_t logits_dtype, int64_t B, int64_t T, int64_t V,
                                         int64_t ls_b, int64_t ls_t, rrl_view targets,
                                         rrl_view old, rrl_view adv, rrl_view mask,
-                                        const void* row_coef, void* logp_out, void* lse_out,
-                                        void* dlogits, int32_t dl_dtype, int64_t ds_b,
-                                        int64_t ds_t, int32_t* status, void* stream) {
+                                        const void* row_coef, void* records, void* logp_out,
+                                        void* lse_out, void* dlogits, int32_t dl_dtype,
+                                        int64_t ds_b, int64_t ds_t, int32_t* status,
+                                        void* stream) {
   clear_error();
   RRL_REQUIRE(params != nullptr, RRL_EINVAL, "params is null");
   RRL_REQUIRE(params->kind == RRL_OBJ_PPO || params->kind == RRL_OBJ_SAO ||
@@ -227,11 +228,15 @@ extern "C" int rrl_fused_logprob_policy(const rrl_policy_params* params, const v
   a.lse_out = lse_out;
   a.dl = dlogits; a.dl_dt = dl_dtype; a.ds_b = ds_b; a.ds_t = ds_t;
   a.pp = *params; a.old = to_view(old); a.adv = to_view(adv); a.mask = to_view(mask);
-  a.row_coef = row_coef; a.status = status;
+  a.row_coef = row_coef; a.records = records; a.status = status;
   bool launched = false;
   rc = maybe_launch_resident(a, 2, logits_dtype, as_stream(stream), &launched);
   if (rc || launched) return rc;
   return dispatch_row<MODE_FUSED>(a, logits_dtype, as_stream(stream));
+}
+
+extern "C" size_t rrl_fused_records_bytes(int64_t B, int64_t T) {
+  return (size_t)(B * T > 0 ? B * T : 0) * sizeof(TokenRecord) + 256;
 }
 
 extern "C" int rrl_scale_rows(void* dlogits, int32_t dl_dtype, int64_t B, int64_t T, int64_t V,

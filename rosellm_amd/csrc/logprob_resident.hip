@@ -84,11 +84,72 @@ template <> struct Pack16<TagF16> {
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
-template <class Tag, int SL>
+// Per-token records for the resident kernel (TokenRecord): the views' dtype
+// and stride handling happens here, once per token, so that the row loop reads
+// its scalars with one uniform 16-byte load.
+__global__ __launch_bounds__(256) void pack_records_kernel(RowArgs a) {
+  const PolicyConsts<float> c = PolicyConsts<float>::make(a.pp);
+  TokenRecord* rec = static_cast<TokenRecord*>(a.records);
+  const float* coef = static_cast<const float*>(a.row_coef);
+  const int64_t n = a.B * a.T;
+  for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t b = i / a.T, t = i - (i / a.T) * a.T;
+    const int64_t tgt = load_index(a.tgt.ptr, a.tgt.dt, b * a.tgt.sr + t * a.tgt.sc);
+    const bool ok = tgt >= 0 && tgt < a.V;
+    if (!ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+    TokenRecord r;
+    r.target = ok ? (int32_t)tgt : -1;
+    r.old = a.old.get<float>(b, t);
+    r.adv = a.adv.get<float>(b, t);
+    r.wcoef = mask_weight<float>(c, a.mask, b, t) * coef[b];
+    rec[i] = r;
+  }
+}
+
+// The records are read-only for the resident kernel, so they can come through
+// the scalar data cache: a uniform load from the constant address space is a
+// single s_load_dwordx4, waited on with lgkmcnt and never behind the
+// vector-memory queue of slab loads and stores.
+__device__ __forceinline__ TokenRecord load_record(const void* base, uint32_t r) {
+  typedef __attribute__((address_space(4))) const u32x4 ConstWords;
+  const u32x4 q = reinterpret_cast<ConstWords*>(reinterpret_cast<uintptr_t>(base))[r];
+  TokenRecord rec;
+  rec.target = (int32_t)q.x;
+  rec.old = __uint_as_float(q.y);
+  rec.adv = __uint_as_float(q.z);
+  rec.wcoef = __uint_as_float(q.w);
+  return rec;
+}
+
+// Workgroup barrier for the combine's LDS exchange.  __syncthreads()'s release
+// fence would also wait for the ring's in-flight DMA (vmcnt(0)), draining the
+// prefetch; the exchange only needs this wave's LDS accesses to have landed,
+// so wait on lgkmcnt alone.  s_waitcnt immediate (gfx9 layout): vmcnt 63 and
+// expcnt 7 (no wait), lgkmcnt 0.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Slabs of the next row staged through LDS (16 KB each): P = 8 uses 128 KB of
+// the CU's 160 KB.
+#ifndef RRL_RESIDENT_LDS_SLABS
+#define RRL_RESIDENT_LDS_SLABS 0
+#endif
+
+template <class Tag, int SL, int PF>
 __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t nvec) {
+  // P of the SL slabs travel through an LDS ring: the DMA for the next row is
+  // issued right after sweep 1, so those bytes are in flight during the
+  // combine and sweep 2 as well; the other SL - P slabs are refilled straight
+  // into registers during sweep 2.
+  constexpr int P = PF < SL ? PF : SL;
   __shared__ float sh_m[RNT / 64];
   __shared__ float sh_s[RNT / 64];
   __shared__ float sh_xt;
+  __shared__ __attribute__((aligned(16))) uint32_t ring[P > 0 ? P * RNT * 4 : 4];
 
   const int tid = threadIdx.x;
   const int64_t rows = a.B * a.T;
@@ -97,6 +158,10 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
   const uint16_t* logits = static_cast<const uint16_t*>(a.logits);
   uint16_t* dl = static_cast<uint16_t*>(a.dl);
   const PolicyConsts<float> c = PolicyConsts<float>::make(a.pp);
+  // This wave's 1 KB window of ring slab k is ring + k*RNT*4 + wave*256 words;
+  // the DMA writes lane j's 16 bytes at window + 16*j, which is where lane j
+  // reads them back.
+  uint32_t* ring_wave = ring + (tid >> 6) * 256;
 
   // Row indices fit in 32 bits (checked on the host); 32-bit division keeps the
   // per-row address arithmetic short.
@@ -105,16 +170,28 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
   uint32_t r = blockIdx.x;
   if (r >= rows32) return;
 
+  auto row_src = [&](uint32_t rr) {
+    const uint32_t bb = rr / T32, tt = rr - bb * T32;
+    return row_rsrc(logits + (int64_t)bb * a.ls_b + (int64_t)tt * a.ls_t, row_bytes);
+  };
+  auto stage = [&](const __amdgpu_buffer_rsrc_t& src) {
+#pragma unroll
+    for (int k = 0; k < P; ++k)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          src, (__attribute__((address_space(3))) void*)(ring_wave + k * RNT * 4), 16, voff,
+          k * RNT * 16, 0, kAuxLoad);
+  };
+
   u32x4 x[SL];
   {
-    const uint32_t b = r / T32, t = r - b * T32;
-    const __amdgpu_buffer_rsrc_t src =
-        row_rsrc(logits + (int64_t)b * a.ls_b + (int64_t)t * a.ls_t, row_bytes);
+    const __amdgpu_buffer_rsrc_t src = row_src(r);
+    stage(src);
 #pragma unroll
-    for (int k = 0; k < SL; ++k)
+    for (int k = P; k < SL; ++k)
       x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
   }
 
+  TokenRecord rec_next = load_record(a.records, r);
   for (; r < rows32; r += gridDim.x) {
     const uint32_t b = r / T32, t = r - b * T32;
     // An opaque per-row copy of the lane id: the per-slab compares below are
@@ -122,26 +199,22 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     // loop-invariant masks.
     int lane = tid;
     asm volatile("" : "+v"(lane));
-    // Per-row scalars (uniform): issued before the sweep so their latency hides.
-    const int64_t tgt = load_index(a.tgt.ptr, a.tgt.dt, (int64_t)b * a.tgt.sr + (int64_t)t * a.tgt.sc);
-    const bool tgt_ok = tgt >= 0 && tgt < a.V;
+    // Per-row scalars: one scalar-cache load, issued a row ahead.
+    const TokenRecord rec = rec_next;
+    const int32_t tgt = rec.target;
+    const bool tgt_ok = tgt >= 0;
     // Slab k of this lane holds the target iff rel == k * RNT.
-    const int rel = tgt_ok ? (int)(tgt >> 3) - lane : -1;
-    const int ti = (int)(tgt & 7);
-    const float o = a.old.get<float>(b, t);
-    const float A = a.adv.get<float>(b, t);
-    const float w = mask_weight<float>(c, a.mask, b, t);
-    const float coef = static_cast<const float*>(a.row_coef)[b];
+    const int rel = tgt_ok ? (tgt >> 3) - lane : -1;
+    const int ti = tgt & 7;
 
-    // Sweep 1: per-lane online (max, sum exp) over the resident slabs.  The
-    // running max starts at -inf; `mg` (the max as an exponent offset) is
-    // kept finite so that slabs of -inf contribute exp(-inf) = 0 rather than
+    // Sweep 1: per-lane online (max, sum exp) over the slabs.  The running max
+    // starts at -inf; `mg` (the max as an exponent offset) is kept finite so
+    // that slabs of -inf contribute exp(-inf) = 0 rather than
     // exp(-inf + inf) = NaN, while NaN and +inf still poison the row as in
     // log_softmax.  The target column is left out of the sum in the one lane
     // and slab that hold it.
     float m = -__builtin_huge_valf(), s = 0.0f;
-#pragma unroll
-    for (int k = 0; k < SL; ++k) {
+    auto fold = [&](int k) {
       if (lane < nvec - k * RNT) {
         float v[8];
         Pack16<Tag>::unpack(x[k], v);
@@ -166,7 +239,27 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
         s = __builtin_fmaf(s, exp2_hw((m - mg) * kLog2e), s8);
         m = mn;
       }
+    };
+    // Ring slabs first, then the register slabs; then the ring is re-armed
+    // with the next row's first P slabs, whose DMA runs during the combine and
+    // sweep 2.  Each lane rewrites only the 16 bytes it has read (and
+    // consumed), in program order.  (Issued any earlier, the DMA would be
+    // waited for by the register slabs' vmcnt waits.)
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+      x[k] = *reinterpret_cast<const u32x4*>(ring_wave + k * RNT * 4 + (tid & 63) * 4);
+      fold(k);
     }
+    const uint32_t rn = r + gridDim.x;
+    const bool has_next = rn < rows32;
+    const __amdgpu_buffer_rsrc_t src = has_next ? row_src(rn) : row_rsrc(logits, 0u);
+#pragma unroll
+    for (int k = P; k < SL; ++k) fold(k);
+    if (has_next) {
+      stage(src);
+      rec_next = load_record(a.records, rn);
+    }
+
     if (!tgt_ok && tid == 0) sh_xt = __builtin_nanf("");
     // Workgroup combine.  sh_xt is written before the first barrier and read
     // before the second, so the next row's write cannot overtake a read.
@@ -180,13 +273,13 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
       sh_m[tid >> 6] = m;
       sh_s[tid >> 6] = s;
     }
-    __syncthreads();
+    lds_barrier();
     m = sh_m[0];
     s = sh_s[0];
 #pragma unroll
     for (int i = 1; i < RNT / 64; ++i) online_merge(m, s, sh_m[i], sh_s[i]);
     const float xt = sh_xt;
-    __syncthreads();
+    lds_barrier();
 
     // Opaque to the optimiser: sweep 2 re-expands the packed slabs instead of
     // keeping sweep 1's widened copies live (twice the registers).
@@ -196,21 +289,14 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     const RowLogprob<float> fr = finish_row<float>(m, s, xt);
     const float lse = fr.lse;
     const float logp = tgt_ok ? fr.logp : __builtin_nanf("");
-    const float g = -((w * coef) * token_local_grad<float>(c, logp, o, A));
+    const float g = -(rec.wcoef * token_local_grad<float>(c, logp, rec.old, rec.adv));
     const float tgt_d = target_grad<float>(g, logp, true, xt, lse);
     if (tid == 0) {
-      if (!tgt_ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
       store_as<float>(a.logp, a.logp_dt, r, logp);
       static_cast<float*>(a.lse_out)[r] = lse;
     }
 
-    // Sweep 2: dlogits, then refill the slab with the next row.
-    const uint32_t rn = r + gridDim.x;
-    const bool has_next = rn < rows32;
-    const uint32_t bn = rn / T32, tn = rn - bn * T32;
-    const __amdgpu_buffer_rsrc_t src = row_rsrc(
-        logits + (has_next ? (int64_t)bn * a.ls_b + (int64_t)tn * a.ls_t : 0),
-        has_next ? row_bytes : 0u);
+    // Sweep 2: dlogits, then refill the register slabs with the next row.
     const __amdgpu_buffer_rsrc_t dst =
         row_rsrc(dl + (int64_t)b * a.ds_b + (int64_t)t * a.ds_t, row_bytes);
     const bool zero_row = (g == 0.0f) && (lse - lse == 0.0f);
@@ -246,7 +332,7 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
       u32x4 o = Pack16<Tag>::pack(d);
       o.x ^= sgn; o.y ^= sgn; o.z ^= sgn; o.w ^= sgn;
       __builtin_amdgcn_raw_buffer_store_b128(o, dst, voff, k * RNT * 16, kAuxStoreNT);
-      if (has_next)
+      if (k >= P)  // src covers 0 bytes past the last row: the load returns zeros
         x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
       // Keep slab k's refill after its own store: hoisting the next row's loads
       // above earlier slabs would hold two rows in registers.
@@ -270,11 +356,14 @@ int launch_resident(const RowArgs& a, int32_t nvec, hipStream_t stream) {
     cu_count[dev] = n;
   }
   const int64_t rows = a.B * a.T;
+  const unsigned pgrid = (unsigned)((rows + 255) / 256 < 65536 ? (rows + 255) / 256 : 65536);
+  hipLaunchKernelGGL(pack_records_kernel, dim3(pgrid), dim3(256), 0, stream, a);
+  if (int rc = check_launch("pack_records_kernel")) return rc;
   const unsigned grid = (unsigned)(rows < cu_count[dev] ? rows : cu_count[dev]);
 #define RRL_RESIDENT_CASE(SLV)                                                                \
   if (need <= SLV) {                                                                          \
-    hipLaunchKernelGGL((resident_fused_kernel<Tag, SLV>), dim3(grid), dim3(RNT), 0, stream, a, \
-                       nvec);                                                                 \
+    hipLaunchKernelGGL((resident_fused_kernel<Tag, SLV, RRL_RESIDENT_LDS_SLABS>), dim3(grid),   \
+                       dim3(RNT), 0, stream, a, nvec);                                       \
     return check_launch("resident_fused_kernel");                                             \
   }
   RRL_RESIDENT_CASE(4)
@@ -304,7 +393,8 @@ int maybe_launch_resident(const RowArgs& a, int mode, int logits_dtype, hipStrea
   const auto al16 = [](int64_t elems) { return ((elems * 2) % 16) == 0; };
   if (((uintptr_t)a.logits % 16) || ((uintptr_t)a.dl % 16)) return RRL_OK;
   if (!al16(a.ls_b) || !al16(a.ls_t) || !al16(a.ds_b) || !al16(a.ds_t)) return RRL_OK;
-  if (a.logp_dt != RRL_F32) return RRL_OK;
+  if (a.logp_dt != RRL_F32 || a.records == nullptr) return RRL_OK;
+  if ((uintptr_t)a.records % 16) return RRL_OK;
   if (a.B * a.T >= ((int64_t)1 << 31) || a.T >= ((int64_t)1 << 31)) return RRL_OK;
   *launched = true;
   const int32_t nvec = (int32_t)(a.V / 8);

@@ -27,7 +27,18 @@ struct RowArgs {
   rrl_policy_params pp;
   View old, adv, mask;
   const void* row_coef;
+  void* records;  // 16-bit fast path: packed per-token records (TokenRecord)
   int32_t* status;
+};
+
+// One token's inputs to the single-pass kernel, packed for a single 16-byte
+// scalar load per row: target id (-1 when outside [0, V)), old log-prob,
+// advantage and mask weight * row coefficient.
+struct TokenRecord {
+  int32_t target;
+  float old;
+  float adv;
+  float wcoef;
 };
 
 __device__ __forceinline__ int dtype_size_dev(int dt) {

@@ -712,6 +712,8 @@ class _FusedPolicy(torch.autograd.Function):
         ws = torch.empty(nat.lib().rrl_policy_workspace_bytes(B, acc_code), dtype=torch.uint8,
                          device=dev)
         coef = torch.empty(B, dtype=acc, device=dev)
+        records = torch.empty(nat.lib().rrl_fused_records_bytes(B, T), dtype=torch.uint8,
+                              device=dev)
         logp = torch.empty(B * T, dtype=acc, device=dev)
         lse = torch.empty(B * T, dtype=acc, device=dev)
         if inplace:
@@ -729,9 +731,9 @@ class _FusedPolicy(torch.autograd.Function):
             nat.call("rrl_policy_row_coef", pref, B, T, mv, acc_code, coef.data_ptr(),
                      ws.data_ptr(), status.data_ptr(), stream)
             nat.call("rrl_fused_logprob_policy", pref, x.data_ptr(), nat.dtype_code(x.dtype), B,
-                     T, V, s_b, s_t, tview, ov, av, mv, coef.data_ptr(), logp.data_ptr(),
-                     lse.data_ptr(), dl.data_ptr(), nat.dtype_code(logits.dtype), d_b, d_t,
-                     status.data_ptr(), stream)
+                     T, V, s_b, s_t, tview, ov, av, mv, coef.data_ptr(), records.data_ptr(),
+                     logp.data_ptr(), lse.data_ptr(), dl.data_ptr(),
+                     nat.dtype_code(logits.dtype), d_b, d_t, status.data_ptr(), stream)
             nat.call("rrl_policy_fwd", pref, B, T, lview, ov, av, mv, acc_code, ws.data_ptr(),
                      scal.data_ptr(), None, nat.ptr(trusted) if trusted.numel() else None,
                      status.data_ptr(), stream)
