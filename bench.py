@@ -44,17 +44,25 @@ HBM_PEAK_GBS = 8000.0
 SIDE_BYTES = 21  # per token: 8 target + 4 old logp + 4 advantage + 1 mask + 4 logp out
 
 CONFIGS = {
-    # name: (prompts, group, T, V, logits dtype, sigma, hot fraction, old-logp noise,
-    #        length range, clip_low, clip_high)
+    # c2 is the headline workload; the others are run on request (--config).
     "c2": dict(prompts=32, group=8, T=1024, V=151936, dtype="bfloat16", sigma=3.0, hot=0.05,
-               noise=0.1, lengths=(64, 1024), clip_low=0.2, clip_high=0.28,
+               noise=0.1, lengths=(64, 1024), rewards="uniform01", objective="clipped",
+               kw=dict(clip_low=0.2, clip_high=0.28),
                workload="C2: GRPO token-level PPO-clip fwd+bwd, 256x1024 tokens, V=151936 bf16"),
     "c1": dict(prompts=8, group=4, T=128, V=50257, dtype="float32", sigma=2.0, hot=0.0,
-               noise=0.05, lengths=(16, 128), clip_low=0.2, clip_high=None,
+               noise=0.05, lengths=(16, 128), rewards="bernoulli0.3", objective="clipped",
+               kw=dict(clip_low=0.2, clip_high=None),
                workload="C1: GRPO token-level PPO-clip fwd+bwd, 32x128 tokens, V=50257 fp32"),
+    "c3": dict(prompts=32, group=8, T=1024, V=151936, dtype="bfloat16", sigma=3.0, hot=0.05,
+               noise=0.1, lengths=(64, 1024), rewards="bernoulli0.5", objective="gspo",
+               kw=dict(clip_low=3e-4, clip_high=4e-4),
+               workload="C3: GSPO sequence-level objective fwd+bwd, 256x1024 tokens, V=151936 bf16"),
+    "c4": dict(prompts=64, group=1, T=8192, V=151936, dtype="bfloat16", sigma=3.0, hot=0.05,
+               noise=0.1, lengths=(1024, 8192), rewards="terminal_normal", objective="sapo",
+               kw=dict(tau_positive=1.0, tau_negative=1.0),
+               workload="C4: GAE(gamma 1, lambda 0.95) + masked whitening + SAPO fwd+bwd, "
+                        "64x8192 tokens, V=151936 bf16, dlogits in place"),
 }
-
-
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -66,10 +74,14 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=2)
     p.add_argument("--config", choices=sorted(CONFIGS), default="c2")
     p.add_argument("--path", choices=["fused", "composed"], default="fused")
+    p.add_argument("--objective", choices=["gspo", "gspo_token"], default=None,
+                   help="config c3 only: GSPO (default) or GSPO-token")
     p.add_argument("--cpu-sample-seqs", type=int, default=2,
                    help="sequences of the batch timed on the CPU oracle")
     p.add_argument("--cpu-runs", type=int, default=3)
     p.add_argument("--skip-cpu", action="store_true")
+    p.add_argument("--no-variants", action="store_true",
+                   help="do not also time the skip_masked_rows variant of the fused path")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also launch one device copy of known size (HBM counter calibration)")
     p.add_argument("--seed", type=int, default=1234)
@@ -108,40 +120,70 @@ def make_inputs(cfg, device, seed):
         del xf, u
     actions = actions.view(B, T)
     old = (logp + cfg["noise"] * torch.randn(B * T, device=device, generator=gens[4])).view(B, T)
-    rewards = torch.randint(0, 2, (cfg["prompts"], cfg["group"]), device=device,
-                            generator=gens[5]).float()
     lo, hi = cfg["lengths"]
     lengths = torch.randint(lo, hi + 1, (B,), device=device, generator=gens[6])
     mask = torch.arange(T, device=device)[None, :] < lengths[:, None]
-    return dict(logits=logits, actions=actions, old=old, rewards=rewards, mask=mask, B=B, T=T,
-                V=V)
+    shape = (cfg["prompts"], cfg["group"])
+    values = None
+    if cfg["rewards"] == "uniform01":
+        rewards = torch.randint(0, 2, shape, device=device, generator=gens[5]).float()
+    elif cfg["rewards"].startswith("bernoulli"):
+        p = float(cfg["rewards"][len("bernoulli"):])
+        rewards = (torch.rand(shape, device=device, generator=gens[5]) < p).float()
+    else:  # per-token rewards: 0 except a terminal N(0, 1) at t = length - 1
+        rewards = torch.zeros(B, T, device=device)
+        rewards[torch.arange(B, device=device), lengths - 1] = torch.randn(
+            B, device=device, generator=gens[5])
+        values = 0.5 * torch.randn(B, T, device=device, generator=gens[7])
+    return dict(logits=logits, actions=actions, old=old, rewards=rewards, values=values,
+                mask=mask, B=B, T=T, V=V)
 
 
-def make_step(inp, cfg, path):
-    import torch
+def make_step(inp, cfg, path, objective, skip_masked=False):
+    """One timed step of the config's training-step hot path."""
 
     from rosellm_amd import roserlhf as R
 
     logits = inp["logits"].requires_grad_()
     actions, old, rewards, mask = inp["actions"], inp["old"], inp["rewards"], inp["mask"]
     B, T = inp["B"], inp["T"]
-    kw = dict(clip_low=cfg["clip_low"], clip_high=cfg["clip_high"])
+    kw = cfg["kw"]
+
+    if objective == "sapo":
+        # Config 4: GAE over the valid tokens, whitened, then SAPO.  dlogits
+        # overwrite the logits (logits + dlogits would need 318.6 GB), so each
+        # step after the first runs on the previous step's dlogits: the same
+        # work on different values.
+        def step():
+            logits.grad = None
+            adv, _ = R.generalized_advantage_estimation(rewards, inp["values"], gamma=1.0,
+                                                        gae_lambda=0.95, valid_mask=mask)
+            adv = R.masked_whiten(adv, mask)
+            out = R.fused_policy_loss(logits, actions, old, adv, mask, objective="sapo",
+                                      inplace=True, **kw)
+            out.loss.backward()
+            return out
+        return step
 
     def advantages():
         seq = R.group_standardized_advantages(rewards).reshape(-1)
-        return seq[:, None].expand(B, T)
+        return seq if objective == "gspo" else seq[:, None].expand(B, T)
 
     if path == "fused":
         def step():
             logits.grad = None
-            out = R.fused_policy_loss(logits, actions, old, advantages(), mask, **kw)
+            out = R.fused_policy_loss(logits, actions, old, advantages(), mask,
+                                      objective=objective, skip_masked_rows=skip_masked, **kw)
             out.loss.backward()
             return out
     else:
+        fn = {"clipped": R.clipped_policy_loss, "gspo": R.gspo_policy_loss,
+              "gspo_token": R.gspo_token_policy_loss}[objective]
+
         def step():
             logits.grad = None
             lp = R.gather_token_logprobs(logits, actions)
-            out = R.clipped_policy_loss(lp, old, advantages(), mask, **kw)
+            out = fn(lp, old, advantages(), mask, **kw)
             out.loss.backward()
             return out
     return step
@@ -160,13 +202,20 @@ def cpu_baseline(inp, cfg, n_seq, runs):
     t = inp["actions"][:n_seq].cpu()
     old = inp["old"][:n_seq].cpu()
     mask = inp["mask"][:n_seq].cpu()
-    seq_adv = o.group_standardize(inp["rewards"].cpu()).reshape(-1)[:n_seq]
-    adv = seq_adv[:, None].expand(n_seq, T)
+    objective = cfg["objective"]
+    if objective == "sapo":
+        adv, _ = o.gae(inp["rewards"][:n_seq].cpu(), inp["values"][:n_seq].cpu(), gamma=1.0,
+                       gae_lambda=0.95, valid_mask=mask)
+        adv = o.masked_whiten(adv, mask)
+    else:
+        seq_adv = o.group_standardize(inp["rewards"].cpu()).reshape(-1)[:n_seq]
+        adv = seq_adv if objective == "gspo" else seq_adv[:, None].expand(n_seq, T)
+    kind = {"clipped": "ppo"}.get(objective, objective)
     threads = torch.get_num_threads()
     times = []
     for i in range(runs + 1):
         t0 = time.perf_counter()
-        o.grpo_step(x, t, old, adv, mask, clip_low=cfg["clip_low"], clip_high=cfg["clip_high"])
+        o.policy_step(kind, x, t, old, adv, mask, **cfg["kw"])
         dt = time.perf_counter() - t0
         if i > 0:
             times.append(dt)
@@ -178,7 +227,8 @@ def cpu_baseline(inp, cfg, n_seq, runs):
         "cores": threads,
         "kind": "port",
         "sample": (f"first {n_seq} of {inp['B']} sequences ({n_seq * T} token rows, same "
-                   f"tensors), oracle log_softmax->gather->clip->autograd on the fp32 upcast, "
+                   f"tensors), oracle log_softmax->gather->{objective}->autograd on the fp32 "
+                   f"upcast, "
                    f"median of {runs} runs after 1 warm-up, torch threads={threads}, "
                    f"os.cpu_count()={os.cpu_count()}"),
     }
@@ -219,15 +269,25 @@ def main():
     torch.cuda.synchronize()
     log(f"[bench] inputs ready in {time.perf_counter() - t0:.1f} s")
     N, V = inp["B"] * inp["T"], inp["V"]
-    step = make_step(inp, cfg, args.path)
+    objective = cfg["objective"]
+    if args.objective:
+        if args.config != "c3":
+            raise SystemExit("--objective applies to config c3")
+        objective = args.objective
+    cfg = dict(cfg, objective=objective)
+    # GSPO needs every token's log-prob before any gradient: its fused entry is
+    # the two-kernel composition (forward sweep, backward sweep).
+    path = args.path if objective in ("clipped", "sapo") else "composed"
+    step = make_step(inp, cfg, path, objective)
 
     for i in range(args.warmup):
         step()
         torch.cuda.synchronize()
         log(f"[bench] warmup {i} done")
 
-    kernel = "rrl_fused_logprob_policy" if args.path == "fused" else "rrl_logprob_bwd"
-    timed = nat.time_calls(kernel)
+    kernels = (["rrl_fused_logprob_policy"] if path == "fused"
+               else ["rrl_logprob_fwd", "rrl_logprob_bwd"])
+    timed = nat.time_calls(*kernels)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -237,18 +297,27 @@ def main():
     nat.time_calls()
     ms_step = elapsed * 1e3 / args.steps
     tok_s = N / (elapsed / args.steps)
-    kms = [s.elapsed_time(e) for s, e in timed[kernel]]
-    k_avg = sum(kms) / len(kms)
-    log(f"[bench] {args.steps} steps: {ms_step:.3f} ms/step, {tok_s / 1e6:.3f} M tok/s; "
-        f"{kernel} avg {k_avg:.3f} ms over {len(kms)} launches; loss {out.loss.item():.6g}")
-
     in_b = inp["logits"].element_size()
-    alg_bytes = N * (V * (in_b + in_b) + SIDE_BYTES)
-    if args.path == "composed":
-        # the backward sweep alone: read logits, write dlogits, plus its row scalars
-        alg_bytes = N * (V * (in_b + in_b) + 8 + 4 + 4 + 4)
-    achieved = alg_bytes / (k_avg * 1e-3) / 1e9
-    workload_key = f"{args.config}-{args.path}"
+    # Algorithmic bytes per launch of each timed entry point.
+    alg = {
+        # read logits + write dlogits, 8 target + 4 old + 4 advantage + 1 mask + 4 logp
+        "rrl_fused_logprob_policy": N * (V * (in_b + in_b) + SIDE_BYTES),
+        # read logits, 8 target, write 4 logp + 4 lse
+        "rrl_logprob_fwd": N * (V * in_b + 8 + 4 + 4),
+        # read logits + write dlogits, 8 target + 4 lse + 4 logp + 4 g
+        "rrl_logprob_bwd": N * (V * (in_b + in_b) + 8 + 4 + 4 + 4),
+    }
+    kstats = {}
+    for k in kernels:
+        kms = [s.elapsed_time(e) for s, e in timed[k]]
+        kstats[k] = sum(kms) / len(kms)
+    kernel = max(kernels, key=lambda k: kstats[k])  # the dominant kernel
+    k_avg = kstats[kernel]
+    log(f"[bench] {args.steps} steps: {ms_step:.3f} ms/step, {tok_s / 1e6:.3f} M tok/s; "
+        + ", ".join(f"{k} avg {v:.3f} ms" for k, v in kstats.items())
+        + f"; loss {out.loss.item():.6g}")
+    achieved = alg[kernel] / (k_avg * 1e-3) / 1e9
+    workload_key = f"{args.config}-{path}" + (f"-{objective}" if args.config == "c3" else "")
     roofline = {
         "bound": "hbm",
         "kernel": kernel,
@@ -258,18 +327,57 @@ def main():
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": traffic_from_profiles(kernel, workload_key),
         "kernel_ms": round(k_avg, 4),
-        "alg_bytes_per_launch": alg_bytes,
+        "alg_bytes_per_launch": alg[kernel],
+        "kernels_ms": {k: round(v, 4) for k, v in kstats.items()},
+        # whole step against the algorithmic minimum of one logits read and one
+        # dlogits write
+        "step_frac": round(N * (V * 2 * in_b + SIDE_BYTES) / (ms_step * 1e-3) / 1e9
+                           / HBM_PEAK_GBS, 4),
     }
 
+    # The same step with skip_masked_rows=True (zero-weight rows are never
+    # read); reported beside the exact-semantics headline, not as `value`.
+    variants = {}
+    if path == "fused" and objective == "clipped" and not args.no_variants:
+        vstep = make_step(inp, cfg, path, objective, skip_masked=True)
+        for _ in range(args.warmup):
+            vstep()
+        vt = nat.time_calls(kernels[0])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            vout = vstep()
+        torch.cuda.synchronize()
+        v_el = time.perf_counter() - t0
+        nat.time_calls()
+        assert vout.loss.item() == out.loss.item(), "skip_masked_rows changed the loss"
+        v_ms = [s.elapsed_time(e) for s, e in vt[kernels[0]]]
+        v_k = sum(v_ms) / len(v_ms)
+        n_active = int(inp["mask"].sum().item())
+        v_alg = n_active * V * in_b + N * V * in_b + N * SIDE_BYTES
+        variants["skip_masked_rows"] = {
+            "value": round(N / (v_el / args.steps), 1),
+            "ms_per_step": round(v_el * 1e3 / args.steps, 4),
+            "kernel_ms": round(v_k, 4),
+            "active_rows": n_active,
+            "alg_bytes_per_launch": v_alg,
+            "achieved": round(v_alg / (v_k * 1e-3) / 1e9, 1),
+            "frac": round(v_alg / (v_k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        log(f"[bench] skip_masked_rows: {v_el * 1e3 / args.steps:.3f} ms/step, "
+            f"{N / (v_el / args.steps) / 1e6:.3f} M tok/s, kernel {v_k:.3f} ms")
+
     if args.calibrate_copy:
-        # 4 GiB device-to-device copy: FETCH_SIZE / WRITE_SIZE of this kernel
-        # give the counters' bytes-per-unit scale.
-        src = torch.empty(1 << 31, dtype=torch.int16, device=device).fill_(1)
-        dst = torch.empty_like(src)
+        # Calibration kernel of known traffic for the HBM counters: a bf16 ->
+        # float32 conversion of 2^30 random elements reads 2 GiB and writes
+        # 4 GiB (a same-dtype copy would run as a DMA blit, invisible to the
+        # counters; constant data can compress in the memory fabric).
+        src = torch.randn(1 << 30, dtype=torch.bfloat16, device=device)
+        dst = torch.empty(1 << 30, dtype=torch.float32, device=device)
         torch.cuda.synchronize()
         dst.copy_(src)
         torch.cuda.synchronize()
-        log(f"[bench] calibration copy: {src.numel() * 2} bytes read and written")
+        log(f"[bench] calibration conversion: {src.numel() * 2} B read, {dst.numel() * 4} B written")
         del src, dst
 
     cpu = None
@@ -292,7 +400,8 @@ def main():
         "data": "synthetic (config distributions, generated on the GPU, seed 1234+i)",
         "config": {
             "workload": cfg["workload"],
-            "path": args.path,
+            "objective": objective,
+            "path": path,
             "sequences": inp["B"],
             "seq_len": inp["T"],
             "vocab": V,
@@ -302,6 +411,8 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
+    if variants:
+        result["variants"] = variants
     print(json.dumps(result), flush=True)
 
 

@@ -78,7 +78,11 @@ enum rrl_flag {
 
 /* rrl_policy_params.flags bits. */
 enum rrl_policy_flag {
-  RRL_POLICY_GENERIC = 1 /* rrl_fused_logprob_policy: use the generic row kernel only */
+  RRL_POLICY_GENERIC = 1,     /* rrl_fused_logprob_policy: use the generic row kernel only */
+  RRL_POLICY_SKIP_MASKED = 2  /* rrl_fused_logprob_policy: a token whose mask weight is exactly 0
+                                 is not read; its dlogits row is written as zeros and its logp /
+                                 lse as 0 (equal to the reference for finite logits, where such a
+                                 row contributes exactly 0; no reference counterpart) */
 };
 
 /* Policy objectives (losses.py). */

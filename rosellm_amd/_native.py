@@ -42,6 +42,7 @@ FLAG_FAST_RANGE = 16
 
 # rrl_policy_flag
 POLICY_GENERIC = 1
+POLICY_SKIP_MASKED = 2
 
 # rrl_objective
 OBJ_PPO, OBJ_SAO, OBJ_GSPO, OBJ_GSPO_TOKEN, OBJ_SAPO = range(5)

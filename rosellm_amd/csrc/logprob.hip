@@ -45,6 +45,18 @@ __global__ __launch_bounds__(NT) void row_kernel(RowArgs a) {
       have_logp = a.logp_in != nullptr;
       logp = have_logp ? static_cast<const Acc*>(a.logp_in)[r] : Acc(0);
       if (threadIdx.x == 0 && !tgt_ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+    } else if (MODE == MODE_FUSED && (a.pp.flags & RRL_POLICY_SKIP_MASKED) &&
+               mask_weight<Acc>(PolicyConsts<Acc>::make(a.pp), a.mask, b, t) *
+                       static_cast<const Acc*>(a.row_coef)[b] == Acc(0)) {
+      // Zero-weight row under RRL_POLICY_SKIP_MASKED: never read.
+      lse = Acc(0);
+      logp = Acc(0);
+      g = Acc(0);
+      if (threadIdx.x == 0) {
+        if (!tgt_ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+        store_as<Acc>(a.logp, a.logp_dt, r, logp);
+        static_cast<Acc*>(a.lse_out)[r] = lse;
+      }
     } else {
       // Sweep 1: online max / sum of exp over the non-target columns.
       Acc m = -M<Acc>::inf(), s = Acc(0);

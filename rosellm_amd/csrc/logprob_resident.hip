@@ -9,8 +9,12 @@
 //   * A row of V 16-bit logits is held in VGPRs as SL slabs of one 16-byte
 //     vector per lane: slab k, lane j holds vector k*1024 + j.  V = 151936
 //     (bf16) is 18992 vectors, SL = 19 of the SL = 20 variant, i.e. 80 VGPRs.
+//   * Per-row scalars (target, old log-prob, advantage, mask weight * 1/M)
+//     come from a packed 16-byte record per token (pack_records_kernel), read
+//     a row ahead through the scalar cache.
 //   * Sweep 1 (registers only): online max / sum of exp over the non-target
-//     columns per lane, one LDS combine across the 16 waves.
+//     columns per lane, slab by slab as the loads land, then one LDS combine
+//     across the 16 waves.
 //   * Sweep 2: each slab becomes g * (onehot - exp(x - lse)), is packed back to
 //     16 bits and stored with a non-temporal buffer store; the same registers
 //     are immediately refilled with the matching slab of the workgroup's next
@@ -122,9 +126,9 @@ __device__ __forceinline__ TokenRecord load_record(const void* base, uint32_t r)
 }
 
 // Workgroup barrier for the combine's LDS exchange.  __syncthreads()'s release
-// fence would also wait for the ring's in-flight DMA (vmcnt(0)), draining the
-// prefetch; the exchange only needs this wave's LDS accesses to have landed,
-// so wait on lgkmcnt alone.  s_waitcnt immediate (gfx9 layout): vmcnt 63 and
+// fence waits for every outstanding vector-memory access (vmcnt(0)), which
+// would drain the next row's in-flight slab loads; the exchange only needs
+// this wave's LDS accesses to have landed, so wait on lgkmcnt alone.  s_waitcnt immediate (gfx9 layout): vmcnt 63 and
 // expcnt 7 (no wait), lgkmcnt 0.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
@@ -133,23 +137,11 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Slabs of the next row staged through LDS (16 KB each): P = 8 uses 128 KB of
-// the CU's 160 KB.
-#ifndef RRL_RESIDENT_LDS_SLABS
-#define RRL_RESIDENT_LDS_SLABS 0
-#endif
-
-template <class Tag, int SL, int PF>
+template <class Tag, int SL>
 __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t nvec) {
-  // P of the SL slabs travel through an LDS ring: the DMA for the next row is
-  // issued right after sweep 1, so those bytes are in flight during the
-  // combine and sweep 2 as well; the other SL - P slabs are refilled straight
-  // into registers during sweep 2.
-  constexpr int P = PF < SL ? PF : SL;
   __shared__ float sh_m[RNT / 64];
   __shared__ float sh_s[RNT / 64];
   __shared__ float sh_xt;
-  __shared__ __attribute__((aligned(16))) uint32_t ring[P > 0 ? P * RNT * 4 : 4];
 
   const int tid = threadIdx.x;
   const int64_t rows = a.B * a.T;
@@ -158,11 +150,6 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
   const uint16_t* logits = static_cast<const uint16_t*>(a.logits);
   uint16_t* dl = static_cast<uint16_t*>(a.dl);
   const PolicyConsts<float> c = PolicyConsts<float>::make(a.pp);
-  // This wave's 1 KB window of ring slab k is ring + k*RNT*4 + wave*256 words;
-  // the DMA writes lane j's 16 bytes at window + 16*j, which is where lane j
-  // reads them back.
-  uint32_t* ring_wave = ring + (tid >> 6) * 256;
-
   // Row indices fit in 32 bits (checked on the host); 32-bit division keeps the
   // per-row address arithmetic short.
   const uint32_t T32 = (uint32_t)a.T;
@@ -174,24 +161,25 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     const uint32_t bb = rr / T32, tt = rr - bb * T32;
     return row_rsrc(logits + (int64_t)bb * a.ls_b + (int64_t)tt * a.ls_t, row_bytes);
   };
-  auto stage = [&](const __amdgpu_buffer_rsrc_t& src) {
-#pragma unroll
-    for (int k = 0; k < P; ++k)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          src, (__attribute__((address_space(3))) void*)(ring_wave + k * RNT * 4), 16, voff,
-          k * RNT * 16, 0, kAuxLoad);
-  };
-
+  // RRL_POLICY_SKIP_MASKED: rows whose weight is exactly 0 are never read
+  // (their loads use a 0-byte descriptor: no memory traffic) and get zero
+  // dlogits and log-prob 0.
+  const bool skip_masked = (a.pp.flags & RRL_POLICY_SKIP_MASKED) != 0;
+  TokenRecord rec_next = load_record(a.records, r);
   u32x4 x[SL];
   {
-    const __amdgpu_buffer_rsrc_t src = row_src(r);
-    stage(src);
+    const bool skip0 = skip_masked && rec_next.wcoef == 0.0f;
+    const __amdgpu_buffer_rsrc_t src = skip0 ? row_rsrc(logits, 0u) : row_src(r);
+    // Issue in slab order, the order sweep 2 refills them: with one order on
+    // both paths into the row loop, sweep 1 waits for slab k only (older
+    // loads), not for the whole row.
 #pragma unroll
-    for (int k = P; k < SL; ++k)
+    for (int k = 0; k < SL; ++k) {
       x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
-  TokenRecord rec_next = load_record(a.records, r);
   for (; r < rows32; r += gridDim.x) {
     const uint32_t b = r / T32, t = r - b * T32;
     // An opaque per-row copy of the lane id: the per-slab compares below are
@@ -201,6 +189,10 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     asm volatile("" : "+v"(lane));
     // Per-row scalars: one scalar-cache load, issued a row ahead.
     const TokenRecord rec = rec_next;
+    const bool skip = skip_masked && rec.wcoef == 0.0f;
+    const uint32_t rn = r + gridDim.x;
+    const bool has_next = rn < rows32;
+    if (has_next) rec_next = load_record(a.records, rn);
     const int32_t tgt = rec.target;
     const bool tgt_ok = tgt >= 0;
     // Slab k of this lane holds the target iff rel == k * RNT.
@@ -240,46 +232,36 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
         m = mn;
       }
     };
-    // Ring slabs first, then the register slabs; then the ring is re-armed
-    // with the next row's first P slabs, whose DMA runs during the combine and
-    // sweep 2.  Each lane rewrites only the 16 bytes it has read (and
-    // consumed), in program order.  (Issued any earlier, the DMA would be
-    // waited for by the register slabs' vmcnt waits.)
+    float xt = 0.0f;
+    if (!skip) {  // uniform over the workgroup
 #pragma unroll
-    for (int k = 0; k < P; ++k) {
-      x[k] = *reinterpret_cast<const u32x4*>(ring_wave + k * RNT * 4 + (tid & 63) * 4);
-      fold(k);
-    }
-    const uint32_t rn = r + gridDim.x;
-    const bool has_next = rn < rows32;
-    const __amdgpu_buffer_rsrc_t src = has_next ? row_src(rn) : row_rsrc(logits, 0u);
+      for (int k = 0; k < SL; ++k) fold(k);
+      if (!tgt_ok && tid == 0) sh_xt = __builtin_nanf("");
+      // Workgroup combine.  sh_xt is written before the first barrier and read
+      // before the second, so the next row's write cannot overtake a read.
 #pragma unroll
-    for (int k = P; k < SL; ++k) fold(k);
-    if (has_next) {
-      stage(src);
-      rec_next = load_record(a.records, rn);
-    }
-
-    if (!tgt_ok && tid == 0) sh_xt = __builtin_nanf("");
-    // Workgroup combine.  sh_xt is written before the first barrier and read
-    // before the second, so the next row's write cannot overtake a read.
+      for (int off = 32; off > 0; off >>= 1) {
+        const float m2 = __shfl_xor(m, off, 64);
+        const float s2 = __shfl_xor(s, off, 64);
+        online_merge(m, s, m2, s2);
+      }
+      if ((tid & 63) == 0) {
+        sh_m[tid >> 6] = m;
+        sh_s[tid >> 6] = s;
+      }
+      lds_barrier();
+      m = sh_m[0];
+      s = sh_s[0];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float m2 = __shfl_xor(m, off, 64);
-      const float s2 = __shfl_xor(s, off, 64);
-      online_merge(m, s, m2, s2);
+      for (int i = 1; i < RNT / 64; ++i) online_merge(m, s, sh_m[i], sh_s[i]);
+      xt = sh_xt;
+      lds_barrier();
     }
-    if ((tid & 63) == 0) {
-      sh_m[tid >> 6] = m;
-      sh_s[tid >> 6] = s;
-    }
-    lds_barrier();
-    m = sh_m[0];
-    s = sh_s[0];
-#pragma unroll
-    for (int i = 1; i < RNT / 64; ++i) online_merge(m, s, sh_m[i], sh_s[i]);
-    const float xt = sh_xt;
-    lds_barrier();
+    // Past the last row (or for a skipped next row) the descriptor covers 0
+    // bytes: the refills return zeros without touching memory.
+    const bool skip_next = skip_masked && rec_next.wcoef == 0.0f;
+    const __amdgpu_buffer_rsrc_t src =
+        (has_next && !skip_next) ? row_src(rn) : row_rsrc(logits, 0u);
 
     // Opaque to the optimiser: sweep 2 re-expands the packed slabs instead of
     // keeping sweep 1's widened copies live (twice the registers).
@@ -287,9 +269,10 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     for (int k = 0; k < SL; ++k) asm volatile("" : "+v"(x[k]));
 
     const RowLogprob<float> fr = finish_row<float>(m, s, xt);
-    const float lse = fr.lse;
-    const float logp = tgt_ok ? fr.logp : __builtin_nanf("");
-    const float g = -(rec.wcoef * token_local_grad<float>(c, logp, rec.old, rec.adv));
+    const float lse = skip ? 0.0f : fr.lse;
+    const float logp = skip ? 0.0f : (tgt_ok ? fr.logp : __builtin_nanf(""));
+    const float g =
+        skip ? 0.0f : -(rec.wcoef * token_local_grad<float>(c, logp, rec.old, rec.adv));
     const float tgt_d = target_grad<float>(g, logp, true, xt, lse);
     if (tid == 0) {
       store_as<float>(a.logp, a.logp_dt, r, logp);
@@ -332,8 +315,7 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
       u32x4 o = Pack16<Tag>::pack(d);
       o.x ^= sgn; o.y ^= sgn; o.z ^= sgn; o.w ^= sgn;
       __builtin_amdgcn_raw_buffer_store_b128(o, dst, voff, k * RNT * 16, kAuxStoreNT);
-      if (k >= P)  // src covers 0 bytes past the last row: the load returns zeros
-        x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
+      x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
       // Keep slab k's refill after its own store: hoisting the next row's loads
       // above earlier slabs would hold two rows in registers.
       __builtin_amdgcn_sched_barrier(0);
@@ -362,8 +344,8 @@ int launch_resident(const RowArgs& a, int32_t nvec, hipStream_t stream) {
   const unsigned grid = (unsigned)(rows < cu_count[dev] ? rows : cu_count[dev]);
 #define RRL_RESIDENT_CASE(SLV)                                                                \
   if (need <= SLV) {                                                                          \
-    hipLaunchKernelGGL((resident_fused_kernel<Tag, SLV, RRL_RESIDENT_LDS_SLABS>), dim3(grid),   \
-                       dim3(RNT), 0, stream, a, nvec);                                       \
+    hipLaunchKernelGGL((resident_fused_kernel<Tag, SLV>), dim3(grid), dim3(RNT), 0, stream,   \
+                       a, nvec);                                                             \
     return check_launch("resident_fused_kernel");                                             \
   }
   RRL_RESIDENT_CASE(4)

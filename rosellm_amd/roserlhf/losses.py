@@ -836,6 +836,7 @@ def fused_policy_loss(
     tau_negative: float = 1.05,
     inplace: bool = False,
     return_logprobs: bool = False,
+    skip_masked_rows: bool = False,
 ):
     """``objective(gather_token_logprobs(logits, target_ids), ...)`` in one sweep.
 
@@ -851,6 +852,13 @@ def fused_policy_loss(
     ``inplace=True`` writes dlogits over the logits (halves the memory of the
     step; the logits are destroyed).  ``return_logprobs=True`` returns
     ``(output, logprobs)``.
+
+    ``skip_masked_rows=True`` (token-local objectives, without
+    ``return_logprobs``) never reads the logits of tokens whose mask weight is
+    exactly 0: their dlogits rows are written as zeros.  For finite logits the
+    loss and dlogits are bit-identical to the default; the one difference is
+    that a NaN/inf logit at a masked position no longer turns the loss into
+    NaN, as ``0 * NaN`` does in the reference's masked mean.
     """
 
     if objective not in _OBJECTIVES:
@@ -865,9 +873,13 @@ def fused_policy_loss(
     if target_ids.dtype not in (torch.int32, torch.int64):
         raise TypeError("target_ids must be an integer tensor")
 
+    if skip_masked_rows and return_logprobs:
+        raise ValueError("skip_masked_rows=True leaves masked log-probs uncomputed; "
+                         "it cannot be combined with return_logprobs=True")
     if kind in (nat.OBJ_GSPO, nat.OBJ_GSPO_TOKEN):
-        if inplace:
-            raise ValueError("inplace=True applies to the single-sweep objectives only")
+        if inplace or skip_masked_rows:
+            raise ValueError("inplace=True and skip_masked_rows=True apply to the single-sweep "
+                             "objectives only")
         logp = gather_token_logprobs(logits, target_ids)
         fn = gspo_policy_loss if kind == nat.OBJ_GSPO else gspo_token_policy_loss
         out = fn(logp, old_logprobs, advantages, action_mask, clip_low=clip_low,
@@ -905,6 +917,8 @@ def fused_policy_loss(
         p = _params(kind, max_log_ratio=max_log_ratio, tau_positive=tau_positive,
                     tau_negative=tau_negative, mask_is_weight=False)
 
+    if skip_masked_rows:
+        p.flags |= nat.POLICY_SKIP_MASKED
     mask = _on_device(action_mask, logits)
     obj, d1, d2, d3, logp, trusted = _FusedPolicy.apply(p, bool(inplace), logits, target_ids,
                                                         old_logprobs, advantages, mask)

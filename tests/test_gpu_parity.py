@@ -681,3 +681,33 @@ def test_fused_extreme_logits(device):
     assert abs(out.loss.item() - out_o["loss"].item()) <= 2e-3 * scale
     assert _ulp16(xd.grad, dlo, "dlogits") > 0.98
     _rownorm16(xd.grad, dlo, 2e-3, "dlogits")
+
+
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 151936), (torch.bfloat16, 20000),
+                                     (torch.float32, 3001)])
+@pytest.mark.parametrize("objective", ["clipped", "sapo"])
+def test_fused_skip_masked_rows_bit_identical(device, dtype, V, objective):
+    """skip_masked_rows=True never reads zero-weight rows; for finite logits the
+    loss, diagnostics and dlogits equal the default path bit for bit."""
+
+    print(f"[skip-masked] objective={objective} dtype={dtype} V={V}", flush=True)
+    B, T = 16, 24
+    x, t, old, adv, mask = _fused_inputs(37, B, T, V, dtype)
+    kw = {"clipped": dict(clip_low=0.2, clip_high=0.28),
+          "sapo": dict(tau_positive=1.0, tau_negative=1.05)}[objective]
+    d = lambda z: z.to(device)
+    outs, grads = [], []
+    for skip in (False, True):
+        xd = d(x).requires_grad_()
+        out = R.fused_policy_loss(xd, d(t), d(old), d(adv), d(mask), objective=objective,
+                                  skip_masked_rows=skip, **kw)
+        out.loss.backward()
+        outs.append(out)
+        grads.append(xd.grad)
+    for f in ("loss", "approximate_kl", "mean_ratio"):
+        assert torch.equal(getattr(outs[0], f), getattr(outs[1], f)), f
+    assert torch.equal(grads[0], grads[1])
+    assert torch.count_nonzero(grads[1][~d(mask)]).item() == 0
+    with pytest.raises(ValueError, match="return_logprobs"):
+        R.fused_policy_loss(d(x), d(t), d(old), d(adv), d(mask), objective=objective,
+                            skip_masked_rows=True, return_logprobs=True, **kw)
