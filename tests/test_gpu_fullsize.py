@@ -1,0 +1,213 @@
+"""The hot path at BASELINE.json's full sizes (configs 2, 3 and 4), checked
+through what does not depend on size:
+
+* a random sample of token rows against the float64 oracle (log-probs, and
+  dlogits rebuilt from the oracle's d loss / d logp over the whole batch);
+* every row's dlogits sums to zero (softmax rows sum to one) within the
+  16-bit output rounding;
+* masked tokens' dlogits rows are exactly zero;
+* the loss against the oracle objective evaluated in float64 on the returned
+  log-probs;
+* skip_masked_rows=True is bit-identical to the default (config 2).
+
+Inputs come from bench.py's generator (same distributions and seeds).  Each
+test frees its tensors; config 4 writes dlogits in place (159 GB of logits).
+"""
+
+from __future__ import annotations
+
+import gc
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import roserlhf_oracle as o
+from rosellm_amd import roserlhf as R
+
+pytestmark = pytest.mark.gpu
+
+N_SAMPLE = 48
+
+
+def _free():
+    gc.collect()
+    torch.cuda.empty_cache()
+
+
+def _sample_rows(N, mask, seed):
+    """Half masked-in rows, a quarter masked-out rows, the rest uniform."""
+
+    g = torch.Generator().manual_seed(seed)
+    m = mask.reshape(-1).cpu()
+    on = torch.nonzero(m).reshape(-1)
+    off = torch.nonzero(~m).reshape(-1)
+    pick = [on[torch.randint(0, on.numel(), (N_SAMPLE // 2,), generator=g)],
+            torch.randint(0, N, (N_SAMPLE // 4,), generator=g)]
+    if off.numel():
+        pick.append(off[torch.randint(0, off.numel(), (N_SAMPLE // 4,), generator=g)])
+    return torch.unique(torch.cat(pick))
+
+
+def _check_rows(x_rows, t_rows, lp_rows, dl_rows, g_rows, what):
+    """Sampled rows against the float64 oracle."""
+
+    lpo = o.token_logprobs(x_rows, t_rows, exact=True)
+    err = (lp_rows.double() - lpo).abs()
+    bound = 1e-5 * lpo.abs() + 1e-7
+    assert bool((err <= bound).all()), f"{what}: logp worst {float((err / bound).max()):.2f}x tol"
+    p = torch.softmax(x_rows.double(), dim=-1)
+    oh = torch.zeros_like(p)
+    oh.scatter_(1, t_rows.long()[:, None], 1.0)
+    want = g_rows.double()[:, None] * (oh - p)
+    rounded = want.float().to(dl_rows.dtype).double()
+    got = dl_rows.double()
+    num = (got - rounded).norm(dim=-1)
+    den = rounded.norm(dim=-1)
+    rel = torch.where(den > 0, num / den.clamp_min(1e-300), num)
+    assert float(rel.max()) <= 2e-3, f"{what}: dlogits row-norm err {float(rel.max()):.3e}"
+
+
+def _row_sums_vanish(dl, what, chunk=8192):
+    """sum_v dlogits[r, v] = g (1 - sum_v p_v) = 0 up to the output rounding."""
+
+    flat = dl.reshape(-1, dl.shape[-1])
+    worst = 0.0
+    for r0 in range(0, flat.shape[0], chunk):
+        c = flat[r0:r0 + chunk].float()
+        s = c.sum(dim=-1).abs()
+        a = c.abs().sum(dim=-1)
+        worst = max(worst, float(torch.where(a > 0, s / a.clamp_min(1e-30), s).max()))
+        del c
+    assert worst <= 2.0 ** -7, f"{what}: |row sum| / sum|row| = {worst:.3e}"
+
+
+def _masked_rows_zero(dl, mask, what, chunk=8192):
+    flat = dl.reshape(-1, dl.shape[-1])
+    m = mask.reshape(-1)
+    for r0 in range(0, flat.shape[0], chunk):
+        rows = ~m[r0:r0 + chunk]
+        assert int(torch.count_nonzero(flat[r0:r0 + chunk][rows])) == 0, what
+
+
+def _oracle_g(kind, lp, old, adv, mask, **kw):
+    """d loss / d logp of the oracle objective in float64 over the whole batch,
+    evaluated on the GPU's log-probs (pinned above on the sampled rows)."""
+
+    cur = lp.detach().double().cpu().requires_grad_()
+    fn = {"ppo": o.ppo_clip, "sapo": o.sapo, "gspo": o.gspo, "gspo_token": o.gspo_token}[kind]
+    out = fn(cur, old.double().cpu(), adv.double().cpu(), mask.cpu(), **kw)
+    out["loss"].backward()
+    return out, cur.grad.reshape(-1)
+
+
+def test_config2_grpo_fullsize(device):
+    print("[fullsize] config 2 fused GRPO", flush=True)
+    cfg = bench.CONFIGS["c2"]
+    with torch.no_grad():
+        inp = bench.make_inputs(cfg, device, 1234)
+    B, T, V = inp["B"], inp["T"], inp["V"]
+    x, t, old, mask = inp["logits"], inp["actions"], inp["old"], inp["mask"]
+    adv = R.group_standardized_advantages(inp["rewards"]).reshape(-1)[:, None].expand(B, T)
+    kw = cfg["kw"]
+    xd = x.requires_grad_()
+    out, lp = R.fused_policy_loss(xd, t, old, adv, mask, return_logprobs=True, **kw)
+    out.loss.backward()
+    dl = xd.grad
+    assert dl.dtype == torch.bfloat16 and dl.shape == x.shape
+    out_o, g = _oracle_g("ppo", lp, old, adv, mask, **kw)
+    scale = max(abs(float(out_o["loss"])), float(adv.abs().mean()))
+    assert abs(float(out.loss) - float(out_o["loss"])) <= 1e-5 * scale
+    for f in ("approximate_kl", "clip_fraction", "mean_ratio"):
+        assert abs(float(getattr(out, f)) - float(out_o[f])) <= 1e-5 * max(1.0, abs(float(out_o[f])))
+    rows = _sample_rows(B * T, mask, 7)
+    xf = x.detach().reshape(-1, V)
+    _check_rows(xf[rows.to(device)].cpu(), t.reshape(-1)[rows.to(device)].cpu(),
+                lp.reshape(-1)[rows.to(device)].cpu(), dl.reshape(-1, V)[rows.to(device)].cpu(),
+                g[rows], "c2")
+    _row_sums_vanish(dl, "c2")
+    _masked_rows_zero(dl, mask, "c2")
+    # skip_masked_rows: same loss and dlogits, bit for bit
+    loss0 = out.loss.detach().clone()
+    xd.grad = None
+    out2 = R.fused_policy_loss(xd, t, old, adv, mask, skip_masked_rows=True, **kw)
+    out2.loss.backward()
+    assert torch.equal(out2.loss, loss0)
+    flat0, flat1 = dl.reshape(-1, V), xd.grad.reshape(-1, V)
+    for r0 in range(0, B * T, 16384):
+        assert torch.equal(flat0[r0:r0 + 16384], flat1[r0:r0 + 16384]), r0
+    del xd, x, dl, flat0, flat1, out, out2, inp
+    _free()
+
+
+@pytest.mark.parametrize("objective", ["gspo", "gspo_token"])
+def test_config3_gspo_fullsize(device, objective):
+    print(f"[fullsize] config 3 {objective}", flush=True)
+    cfg = bench.CONFIGS["c3"]
+    with torch.no_grad():
+        inp = bench.make_inputs(cfg, device, 1234)
+    B, T, V = inp["B"], inp["T"], inp["V"]
+    x, t, old, mask = inp["logits"], inp["actions"], inp["old"], inp["mask"]
+    seq = R.group_standardized_advantages(inp["rewards"]).reshape(-1)
+    adv = seq if objective == "gspo" else seq[:, None].expand(B, T)
+    kw = cfg["kw"]
+    xd = x.requires_grad_()
+    out, lp = R.fused_policy_loss(xd, t, old, adv, mask, objective=objective,
+                                  return_logprobs=True, **kw)
+    out.loss.backward()
+    dl = xd.grad
+    out_o, g = _oracle_g(objective, lp, old, adv, mask, **kw)
+    scale = max(abs(float(out_o["loss"])), float(seq.abs().mean()))
+    assert abs(float(out.loss) - float(out_o["loss"])) <= 1e-5 * scale
+    torch.testing.assert_close(out.sequence_ratios.double().cpu(), out_o["sequence_ratios"],
+                               rtol=1e-5, atol=1e-7)
+    rows = _sample_rows(B * T, mask, 8)
+    xf = x.detach().reshape(-1, V)
+    r_d = rows.to(device)
+    _check_rows(xf[r_d].cpu(), t.reshape(-1)[r_d].cpu(), lp.reshape(-1)[r_d].cpu(),
+                dl.reshape(-1, V)[r_d].cpu(), g[rows], f"c3 {objective}")
+    _row_sums_vanish(dl, f"c3 {objective}")
+    _masked_rows_zero(dl, mask, f"c3 {objective}")
+    del xd, x, dl, out, inp
+    _free()
+
+
+def test_config4_gae_sapo_inplace_fullsize(device):
+    print("[fullsize] config 4 GAE + whitening + SAPO, in place", flush=True)
+    cfg = bench.CONFIGS["c4"]
+    with torch.no_grad():
+        inp = bench.make_inputs(cfg, device, 1234)
+    B, T, V = inp["B"], inp["T"], inp["V"]
+    x, t, old, mask = inp["logits"], inp["actions"], inp["old"], inp["mask"]
+    rows = _sample_rows(B * T, mask, 9)
+    r_d = rows.to(device)
+    x_rows = x.reshape(-1, V)[r_d].cpu()  # kept before the logits are overwritten
+    # estimators against the oracle's sequential recurrences
+    adv, ret = R.generalized_advantage_estimation(inp["rewards"], inp["values"], gamma=1.0,
+                                                  gae_lambda=0.95, valid_mask=mask)
+    adv_o, ret_o = o.gae(inp["rewards"].double().cpu(), inp["values"].double().cpu(), gamma=1.0,
+                         gae_lambda=0.95, valid_mask=mask.cpu())
+    tol = 1e-5 * max(1.0, float(adv_o.abs().max()))
+    assert float((adv.double().cpu() - adv_o).abs().max()) <= tol
+    assert float((ret.double().cpu() - ret_o).abs().max()) <= tol
+    assert bool((adv.cpu()[~mask.cpu()] == 0).all())
+    w = R.masked_whiten(adv, mask)
+    sel = w.double()[mask]
+    assert abs(float(sel.mean())) < 1e-5 and abs(float(sel.std(unbiased=False)) - 1) < 1e-5
+    kw = cfg["kw"]
+    xd = x.requires_grad_()
+    out, lp = R.fused_policy_loss(xd, t, old, w, mask, objective="sapo", inplace=True,
+                                  return_logprobs=True, **kw)
+    out.loss.backward()
+    dl = xd.grad
+    assert dl.data_ptr() == x.data_ptr()  # written in place
+    out_o, g = _oracle_g("sapo", lp, old, w, mask, **kw)
+    scale = max(abs(float(out_o["loss"])), float(w.abs().mean()))
+    assert abs(float(out.loss) - float(out_o["loss"])) <= 1e-5 * scale
+    _check_rows(x_rows, t.reshape(-1)[r_d].cpu(), lp.reshape(-1)[r_d].cpu(),
+                dl.reshape(-1, V)[r_d].cpu(), g[rows], "c4")
+    _row_sums_vanish(dl, "c4")
+    _masked_rows_zero(dl, mask, "c4")
+    del xd, x, dl, out, inp
+    _free()
