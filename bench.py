@@ -17,6 +17,12 @@ backward to bf16 dlogits.  ``--path fused`` (default) runs it through
 ``clipped_policy_loss`` and autograd (two reads, one write).  Inputs are
 resident in HBM before the timed region.
 
+``--config c5`` is the fused LM-head step: hidden [256x1024, 1024] bf16 and
+an LM-head weight [151936, 1024] bf16 -> log-probs -> clipped objective ->
+d hidden and d weight, through ``fused_linear_policy_loss`` (``--path
+composed``: F.linear, gather_token_logprobs, clipped_policy_loss, autograd);
+its roofline is MFMA-bound (3 x 2*N*H*V flops per step).
+
 Prints one JSON line (rank 0): value = tokens/s over all B*T positions, plus
 ``roofline`` for the dominant kernel (HIP events around its entry point over
 the timed steps; algorithmic bytes N*(V*(2+2) + 21)) and ``cpu_baseline``, the
@@ -62,7 +68,14 @@ CONFIGS = {
                kw=dict(tau_positive=1.0, tau_negative=1.0),
                workload="C4: GAE(gamma 1, lambda 0.95) + masked whitening + SAPO fwd+bwd, "
                         "64x8192 tokens, V=151936 bf16, dlogits in place"),
+    "c5": dict(prompts=32, group=8, T=1024, V=151936, H=1024, dtype="bfloat16", sigma=1.0,
+               w_sigma=0.02, hot=0.0, noise=0.1, lengths=(64, 1024), rewards="uniform01",
+               objective="clipped", kw=dict(clip_low=0.2, clip_high=0.28), lm_head=True,
+               workload="C5: fused LM-head + logprob + GRPO PPO-clip fwd+bwd to dhidden and dW, "
+                        "256x1024 tokens, hidden 1024, V=151936 bf16"),
 }
+LM_HEAD_ROW_BLOCK = 16384
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -97,22 +110,37 @@ def make_inputs(cfg, device, seed):
     B = cfg["prompts"] * cfg["group"]
     T, V = cfg["T"], cfg["V"]
     dtype = getattr(torch, cfg["dtype"])
-    gens = [torch.Generator(device=device).manual_seed(seed + i) for i in range(8)]
-    logits = torch.randn(B, T, V, dtype=dtype, device=device, generator=gens[0])
-    logits.mul_(cfg["sigma"])
-    flat = logits.view(-1, V)
-    if cfg["hot"] > 0:
-        hot_rows = torch.nonzero(torch.rand(B * T, device=device, generator=gens[1]) < cfg["hot"])
-        hot_rows = hot_rows.reshape(-1)
-        hot_cols = torch.randint(0, V, (hot_rows.numel(),), device=device, generator=gens[2])
-        flat[hot_rows, hot_cols] = (flat[hot_rows, hot_cols].float() + 15.0).to(dtype)
+    gens = [torch.Generator(device=device).manual_seed(seed + i) for i in range(10)]
+    hidden = weight = logits = None
+    if cfg.get("lm_head"):
+        # Config 5: hidden ~ N(0, 1), LM-head weight ~ N(0, w_sigma); the
+        # logits exist only one row chunk at a time, as products of the two.
+        H = cfg["H"]
+        hidden = torch.randn(B, T, H, dtype=dtype, device=device, generator=gens[8])
+        hidden.mul_(cfg["sigma"])
+        weight = torch.randn(V, H, dtype=dtype, device=device, generator=gens[9])
+        weight.mul_(cfg["w_sigma"])
+        h2 = hidden.view(-1, H)
+        row_logits = lambda r0, r1: torch.mm(h2[r0:r1], weight.t())
+    else:
+        logits = torch.randn(B, T, V, dtype=dtype, device=device, generator=gens[0])
+        logits.mul_(cfg["sigma"])
+        flat = logits.view(-1, V)
+        if cfg["hot"] > 0:
+            hot_rows = torch.nonzero(torch.rand(B * T, device=device, generator=gens[1])
+                                     < cfg["hot"])
+            hot_rows = hot_rows.reshape(-1)
+            hot_cols = torch.randint(0, V, (hot_rows.numel(),), device=device,
+                                     generator=gens[2])
+            flat[hot_rows, hot_cols] = (flat[hot_rows, hot_cols].float() + 15.0).to(dtype)
+        row_logits = lambda r0, r1: flat[r0:r1]
     # Actions ~ softmax(logits) by Gumbel-max; reference log-probs by
     # log_softmax in float32, chunked so no [N, V] float32 tensor is built.
     actions = torch.empty(B * T, dtype=torch.int64, device=device)
     logp = torch.empty(B * T, dtype=torch.float32, device=device)
     chunk = max(1, (1 << 30) // (V * 4))
     for r0 in range(0, B * T, chunk):
-        xf = flat[r0:r0 + chunk].float()
+        xf = row_logits(r0, min(B * T, r0 + chunk)).float()
         u = torch.rand(xf.shape, device=device, generator=gens[3]).clamp_(min=1e-20)
         a = torch.argmax(xf - torch.log(-torch.log(u)), dim=-1)
         actions[r0:r0 + chunk] = a
@@ -135,8 +163,8 @@ def make_inputs(cfg, device, seed):
         rewards[torch.arange(B, device=device), lengths - 1] = torch.randn(
             B, device=device, generator=gens[5])
         values = 0.5 * torch.randn(B, T, device=device, generator=gens[7])
-    return dict(logits=logits, actions=actions, old=old, rewards=rewards, values=values,
-                mask=mask, B=B, T=T, V=V)
+    return dict(logits=logits, hidden=hidden, weight=weight, actions=actions, old=old,
+                rewards=rewards, values=values, mask=mask, B=B, T=T, V=V)
 
 
 def make_step(inp, cfg, path, objective, skip_masked=False):
@@ -144,10 +172,35 @@ def make_step(inp, cfg, path, objective, skip_masked=False):
 
     from rosellm_amd import roserlhf as R
 
-    logits = inp["logits"].requires_grad_()
     actions, old, rewards, mask = inp["actions"], inp["old"], inp["rewards"], inp["mask"]
     B, T = inp["B"], inp["T"]
     kw = cfg["kw"]
+
+    if cfg.get("lm_head"):
+        # Config 5: hidden -> LM head -> log-probs -> clipped objective ->
+        # d hidden, d weight.  "fused" never holds more than one row block of
+        # logits; "composed" is the reference's chain (F.linear, then
+        # gather_token_logprobs and clipped_policy_loss, autograd through all).
+        import torch.nn.functional as F
+
+        hidden = inp["hidden"].requires_grad_()
+        weight = inp["weight"].requires_grad_()
+
+        def step():
+            hidden.grad = None
+            weight.grad = None
+            a = R.group_standardized_advantages(rewards).reshape(-1)[:, None].expand(B, T)
+            if path == "fused":
+                out = R.fused_linear_policy_loss(hidden, weight, actions, old, a, mask,
+                                                 row_block=LM_HEAD_ROW_BLOCK, **kw)
+            else:
+                lp = R.gather_token_logprobs(F.linear(hidden, weight), actions)
+                out = R.clipped_policy_loss(lp, old, a, mask, **kw)
+            out.loss.backward()
+            return out
+        return step
+
+    logits = inp["logits"].requires_grad_()
 
     if objective == "sapo":
         # Config 4: GAE over the valid tokens, whitened, then SAPO.  dlogits
@@ -198,6 +251,8 @@ def cpu_baseline(inp, cfg, n_seq, runs):
     from oracle import roserlhf_oracle as o
 
     T = inp["T"]
+    if cfg.get("lm_head"):
+        return cpu_baseline_lm_head(inp, cfg, n_seq, runs)
     x = inp["logits"].detach()[:n_seq].cpu()
     t = inp["actions"][:n_seq].cpu()
     old = inp["old"][:n_seq].cpu()
@@ -231,6 +286,47 @@ def cpu_baseline(inp, cfg, n_seq, runs):
                    f"upcast, "
                    f"median of {runs} runs after 1 warm-up, torch threads={threads}, "
                    f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def cpu_baseline_lm_head(inp, cfg, n_seq, runs):
+    """Config 5 on the CPU: the reference chain (hidden @ W.T, log_softmax,
+    gather, clipped objective, autograd back through the linear map) in
+    float32 on the first n_seq sequences."""
+
+    import torch
+
+    from oracle import roserlhf_oracle as o
+
+    T = inp["T"]
+    h = inp["hidden"].detach()[:n_seq].cpu().float()
+    w = inp["weight"].detach().cpu().float()
+    t = inp["actions"][:n_seq].cpu()
+    old = inp["old"][:n_seq].cpu()
+    mask = inp["mask"][:n_seq].cpu()
+    seq_adv = o.group_standardize(inp["rewards"].cpu()).reshape(-1)[:n_seq]
+    adv = seq_adv[:, None].expand(n_seq, T)
+    threads = torch.get_num_threads()
+    times = []
+    for i in range(runs + 1):
+        t0 = time.perf_counter()
+        x = h @ w.t()
+        o.lm_head_step("ppo", h, w, x, t, old, adv, mask, **cfg["kw"])
+        dt = time.perf_counter() - t0
+        del x
+        if i > 0:
+            times.append(dt)
+        log(f"[bench] cpu oracle run {i}: {dt:.2f} s")
+    med = statistics.median(times)
+    return {
+        "value": round(n_seq * T / med, 1),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"first {n_seq} of {inp['B']} sequences ({n_seq * T} token rows, same "
+                   f"tensors), oracle hidden@W.T->log_softmax->gather->clip->autograd through "
+                   f"the LM head in float32, median of {runs} runs after 1 warm-up, torch "
+                   f"threads={threads}, os.cpu_count()={os.cpu_count()}"),
     }
 
 
@@ -297,7 +393,7 @@ def main():
     nat.time_calls()
     ms_step = elapsed * 1e3 / args.steps
     tok_s = N / (elapsed / args.steps)
-    in_b = inp["logits"].element_size()
+    in_b = (inp["hidden"] if cfg.get("lm_head") else inp["logits"]).element_size()
     # Algorithmic bytes per launch of each timed entry point.
     alg = {
         # read logits + write dlogits, 8 target + 4 old + 4 advantage + 1 mask + 4 logp
@@ -318,27 +414,59 @@ def main():
         + f"; loss {out.loss.item():.6g}")
     achieved = alg[kernel] / (k_avg * 1e-3) / 1e9
     workload_key = f"{args.config}-{path}" + (f"-{objective}" if args.config == "c3" else "")
-    roofline = {
-        "bound": "hbm",
-        "kernel": kernel,
-        "achieved": round(achieved, 1),
-        "peak": HBM_PEAK_GBS,
-        "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": traffic_from_profiles(kernel, workload_key),
-        "kernel_ms": round(k_avg, 4),
-        "alg_bytes_per_launch": alg[kernel],
-        "kernels_ms": {k: round(v, 4) for k, v in kstats.items()},
-        # whole step against the algorithmic minimum of one logits read and one
-        # dlogits write
-        "step_frac": round(N * (V * 2 * in_b + SIDE_BYTES) / (ms_step * 1e-3) / 1e9
-                           / HBM_PEAK_GBS, 4),
-    }
+    if cfg.get("lm_head"):
+        # Config 5 is bound by the three GEMMs (hidden x W^T, dlogits x W,
+        # dlogits^T x hidden): 3 x 2*N*H*V flops per step against the dense
+        # bf16 MFMA peak; the row kernel's share is reported beside it.
+        H = inp["hidden"].shape[-1]
+        flops = 3 * 2 * N * H * V
+        tflops = flops / (ms_step * 1e-3) / 1e12
+        per_step = len(timed[kernel]) / args.steps  # row-kernel launches per step
+        rows_launch = N / per_step
+        alg_launch = (rows_launch * (V * (in_b + in_b) + SIDE_BYTES) if kernel != "rrl_logprob_fwd"
+                      else rows_launch * (V * in_b + 16))
+        k_gbs = alg_launch / (k_avg * 1e-3) / 1e9
+        roofline = {
+            "bound": "mfma",
+            "kernel": "whole step (hipBLASLt GEMMs + " + kernel + ")",
+            "achieved": round(tflops, 1),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "alg_flops_per_step": flops,
+            "row_kernel": {"name": kernel, "launches_per_step": per_step,
+                           "kernel_ms": round(k_avg, 4),
+                           "ms_per_step": round(k_avg * per_step, 4),
+                           "alg_bytes_per_launch": alg_launch,
+                           "achieved_GBs": round(k_gbs, 1),
+                           "frac_hbm": round(k_gbs / HBM_PEAK_GBS, 4)},
+            "kernels_ms": {k: round(v, 4) for k, v in kstats.items()},
+            "blas": str(torch.backends.cuda.preferred_blas_library()),
+        }
+    else:
+        roofline = {
+            "bound": "hbm",
+            "kernel": kernel,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles(kernel, workload_key),
+            "kernel_ms": round(k_avg, 4),
+            "alg_bytes_per_launch": alg[kernel],
+            "kernels_ms": {k: round(v, 4) for k, v in kstats.items()},
+            # whole step against the algorithmic minimum of one logits read and
+            # one dlogits write
+            "step_frac": round(N * (V * 2 * in_b + SIDE_BYTES) / (ms_step * 1e-3) / 1e9
+                               / HBM_PEAK_GBS, 4),
+        }
 
     # The same step with skip_masked_rows=True (zero-weight rows are never
     # read); reported beside the exact-semantics headline, not as `value`.
     variants = {}
-    if path == "fused" and objective == "clipped" and not args.no_variants:
+    if (path == "fused" and objective == "clipped" and not args.no_variants
+            and not cfg.get("lm_head")):
         vstep = make_step(inp, cfg, path, objective, skip_masked=True)
         for _ in range(args.warmup):
             vstep()
@@ -405,6 +533,8 @@ def main():
             "sequences": inp["B"],
             "seq_len": inp["T"],
             "vocab": V,
+            **({"hidden": inp["hidden"].shape[-1], "row_block": LM_HEAD_ROW_BLOCK}
+               if cfg.get("lm_head") else {}),
             "tokens_per_step": N,
             "parallelism": "none (1 GPU)",
         },

@@ -377,6 +377,37 @@ def policy_step(kind: str, logits: Tensor, targets: Tensor, old: Tensor, adv: Te
     return out, lp.detach(), x.grad
 
 
+def lm_head_step(kind: str, hidden: Tensor, weight: Tensor, logits: Tensor, targets: Tensor,
+                 old: Tensor, adv: Tensor, mask: Tensor, *, exact: bool = False, **kw
+                 ) -> Tuple[Dict[str, Tensor], Tensor, Tensor, Tensor]:
+    """policy_step behind the LM head: logits = hidden @ weight.T with no bias
+    (rosetrainer/model.py:499,641; rosetrainer/qwen3.py:508,556), then the
+    objective, then the linear map's backward: d hidden = dlogits @ weight,
+    d weight = dlogits.T @ hidden (summed over every token).
+
+    ``logits`` are the rounded products the kernels under test consumed (the
+    product itself is the GEMM library's); pass the float64 product of
+    ``hidden`` and ``weight`` to run the whole chain exactly.  With 16-bit
+    logits the reference's autograd hands the linear map's backward a
+    gradient in the logits dtype, so dlogits are rounded to it (round to
+    nearest even) before the two products, as there.  Returns (objective
+    outputs with the dlogits so used under "dlogits", log-probs, d hidden,
+    d weight).
+    """
+
+    out, lp, dl = policy_step(kind, logits, targets, old, adv, mask, exact=exact, **kw)
+    wide = torch.float64 if exact else torch.float32
+    V, H = weight.shape
+    if logits.dtype in (torch.bfloat16, torch.float16):
+        dl = dl.to(logits.dtype)
+    out["dlogits"] = dl
+    d2 = dl.reshape(-1, V).to(wide)
+    h2 = hidden.reshape(-1, H).to(wide)
+    dh = (d2 @ weight.to(wide)).reshape(hidden.shape)
+    dw = d2.t() @ h2
+    return out, lp, dh, dw
+
+
 def clip_bounds(clip_low: float, clip_high: float) -> Tuple[float, float]:
     """Both log-ratio boundaries of the clip band (used by validators)."""
 

@@ -1,7 +1,8 @@
 """MI355X-native RoseRLHF hot path: same public names as ``rosellm.roserlhf``
 (rosellm/roserlhf/__init__.py:8-48), backed by gfx950 HIP kernels.
 
-``fused_policy_loss`` and ``masked_whiten`` are additions of this package;
+``fused_policy_loss``, ``fused_linear_policy_loss``, ``linear_token_logprobs``
+and ``masked_whiten`` are additions of this package;
 ``losses.masked_mean`` and ``losses.sequence_log_ratio`` stay module-level as
 in the reference.
 """
@@ -15,6 +16,7 @@ from .advantages import (
     masked_whiten,
     skip_observation_generalized_advantage_estimation,
 )
+from .linear import fused_linear_policy_loss, linear_token_logprobs
 from .losses import (
     GspoPolicyLossOutput,
     PolicyLossOutput,
@@ -39,11 +41,13 @@ __all__ = [
     "clipped_policy_loss",
     "discounted_returns",
     "direct_double_sided_mask",
+    "fused_linear_policy_loss",
     "fused_policy_loss",
     "gather_token_logprobs",
     "generalized_advantage_estimation",
     "group_standardized_advantages",
     "leave_one_out_advantages",
+    "linear_token_logprobs",
     "gspo_policy_loss",
     "gspo_token_policy_loss",
     "masked_whiten",

@@ -686,6 +686,60 @@ _OBJECTIVES = {
 }
 
 
+def _token_local_params(kind: int, prefix, old_logprobs: Tensor, advantages: Tensor,
+                       action_mask: Tensor, *, clip_low: float, clip_high: Optional[float],
+                       max_log_ratio: float, detach_ratio: bool, tau_positive: float,
+                       tau_negative: float) -> nat.RrlPolicyParams:
+    """Validate a token-local objective's arguments (the checks and messages of
+    clipped_policy_loss, sao_policy_loss and sapo_policy_loss) and pack its
+    kernel parameters."""
+
+    if kind == nat.OBJ_PPO:
+        if not (prefix == old_logprobs.shape == advantages.shape == action_mask.shape):
+            raise ValueError("all tensors must have the same shape")
+        clip_high = _check_clip_params(clip_low, clip_high, max_log_ratio)
+        p = _params(kind, clip_low=clip_low, clip_high=clip_high, max_log_ratio=max_log_ratio,
+                    mask_is_weight=True)
+    elif kind == nat.OBJ_SAO:
+        if clip_high is None:
+            raise TypeError("sao objective needs clip_high")
+        if not (prefix == old_logprobs.shape == advantages.shape == action_mask.shape):
+            raise ValueError("all tensors must have the same shape")
+        if max_log_ratio <= 0.0:
+            raise ValueError("max_log_ratio must be positive")
+        _check_clip_range(clip_low, clip_high, max_log_ratio)
+        p = _params(kind, clip_low=clip_low, clip_high=clip_high, max_log_ratio=max_log_ratio,
+                    detach_ratio=detach_ratio, mask_is_weight=False)
+    else:
+        if len(prefix) != 2:
+            raise ValueError("SAPO expects rank-2 [sequence, token] tensors")
+        if not (prefix == old_logprobs.shape == advantages.shape == action_mask.shape):
+            raise ValueError("all tensors must have the same shape")
+        _check_float(old_logprobs, advantages)
+        if tau_positive <= 0.0 or tau_negative <= 0.0:
+            raise ValueError("SAPO temperatures must be positive")
+        if max_log_ratio <= 0.0:
+            raise ValueError("max_log_ratio must be positive")
+        p = _params(kind, max_log_ratio=max_log_ratio, tau_positive=tau_positive,
+                    tau_negative=tau_negative, mask_is_weight=False)
+
+    return p
+
+
+def _token_local_output(kind: int, obj: Tensor, d1: Tensor, d2: Tensor, d3: Tensor,
+                        trusted: Tensor):
+    """The output record of the token-local objective ``kind``."""
+
+    if kind == nat.OBJ_PPO:
+        return PolicyLossOutput(loss=-obj, objective=obj, approximate_kl=d1, clip_fraction=d2,
+                                mean_ratio=d3)
+    if kind == nat.OBJ_SAO:
+        return SaoPolicyLossOutput(loss=-obj, objective=obj, approximate_kl=d1,
+                                   rejected_fraction=d2, mean_ratio=d3, trusted_mask=trusted)
+    return SapoPolicyLossOutput(loss=-obj, objective=obj, approximate_kl=d1, mean_ratio=d2,
+                                mean_gradient_gate=d3)
+
+
 class _FusedPolicy(torch.autograd.Function):
     """One sweep per logits row: log-prob, d(-objective)/d logp, dlogits.
 
@@ -887,49 +941,15 @@ def fused_policy_loss(
                  max_log_ratio=max_log_ratio)
         return (out, logp.detach()) if return_logprobs else out
 
-    prefix = logits.shape[:-1]
-    if kind == nat.OBJ_PPO:
-        if not (prefix == old_logprobs.shape == advantages.shape == action_mask.shape):
-            raise ValueError("all tensors must have the same shape")
-        clip_high = _check_clip_params(clip_low, clip_high, max_log_ratio)
-        p = _params(kind, clip_low=clip_low, clip_high=clip_high, max_log_ratio=max_log_ratio,
-                    mask_is_weight=True)
-    elif kind == nat.OBJ_SAO:
-        if clip_high is None:
-            raise TypeError("sao objective needs clip_high")
-        if not (prefix == old_logprobs.shape == advantages.shape == action_mask.shape):
-            raise ValueError("all tensors must have the same shape")
-        if max_log_ratio <= 0.0:
-            raise ValueError("max_log_ratio must be positive")
-        _check_clip_range(clip_low, clip_high, max_log_ratio)
-        p = _params(kind, clip_low=clip_low, clip_high=clip_high, max_log_ratio=max_log_ratio,
-                    detach_ratio=detach_ratio, mask_is_weight=False)
-    else:
-        if len(prefix) != 2:
-            raise ValueError("SAPO expects rank-2 [sequence, token] tensors")
-        if not (prefix == old_logprobs.shape == advantages.shape == action_mask.shape):
-            raise ValueError("all tensors must have the same shape")
-        _check_float(old_logprobs, advantages)
-        if tau_positive <= 0.0 or tau_negative <= 0.0:
-            raise ValueError("SAPO temperatures must be positive")
-        if max_log_ratio <= 0.0:
-            raise ValueError("max_log_ratio must be positive")
-        p = _params(kind, max_log_ratio=max_log_ratio, tau_positive=tau_positive,
-                    tau_negative=tau_negative, mask_is_weight=False)
-
+    p = _token_local_params(kind, logits.shape[:-1], old_logprobs, advantages, action_mask,
+                            clip_low=clip_low, clip_high=clip_high,
+                            max_log_ratio=max_log_ratio, detach_ratio=detach_ratio,
+                            tau_positive=tau_positive, tau_negative=tau_negative)
     if skip_masked_rows:
         p.flags |= nat.POLICY_SKIP_MASKED
     mask = _on_device(action_mask, logits)
     obj, d1, d2, d3, logp, trusted = _FusedPolicy.apply(p, bool(inplace), logits, target_ids,
                                                         old_logprobs, advantages, mask)
-    if kind == nat.OBJ_PPO:
-        out = PolicyLossOutput(loss=-obj, objective=obj, approximate_kl=d1, clip_fraction=d2,
-                               mean_ratio=d3)
-    elif kind == nat.OBJ_SAO:
-        out = SaoPolicyLossOutput(loss=-obj, objective=obj, approximate_kl=d1,
-                                  rejected_fraction=d2, mean_ratio=d3, trusted_mask=trusted)
-    else:
-        out = SapoPolicyLossOutput(loss=-obj, objective=obj, approximate_kl=d1, mean_ratio=d2,
-                                   mean_gradient_gate=d3)
+    out = _token_local_output(kind, obj, d1, d2, d3, trusted)
     return (out, logp) if return_logprobs else out
 

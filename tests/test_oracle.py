@@ -327,3 +327,40 @@ def test_planted_padding_as_terminal_is_caught():
     wrong = o.returns_to_go(torch.where(valid, r, torch.zeros_like(r)), terminated=~valid)
     assert not torch.allclose(good, wrong)
     np.testing.assert_allclose(good.numpy(), brute.returns(r.numpy(), valid=valid.numpy()))
+
+
+@pytest.mark.parametrize("kind", ["ppo", "sapo"])
+def test_lm_head_step_vs_finite_differences(kind):
+    """d hidden and d weight of the LM-head composition against central
+    differences of the float64 loss in a few coordinates of each."""
+
+    rng = _rng(11)
+    B, T, H, V = 2, 5, 7, 13
+    h = torch.tensor(rng.normal(0, 1.0, size=(B, T, H)))
+    w = torch.tensor(rng.normal(0, 0.7, size=(V, H)))
+    tgt = torch.tensor(rng.integers(0, V, size=(B, T)))
+    lp0 = o.token_logprobs(h @ w.t(), tgt, exact=True)
+    old = lp0 + torch.tensor(rng.normal(0, 0.1, size=(B, T)))
+    adv = torch.tensor(rng.normal(0, 1, size=(B, T)))
+    mask = torch.tensor(rng.random((B, T)) < 0.8)
+    mask[:, 0] = True
+    kw = dict(clip_low=0.2, clip_high=0.28) if kind == "ppo" else {}
+    out, _lp, dh, dw = o.lm_head_step(kind, h, w, h @ w.t(), tgt, old, adv, mask, exact=True,
+                                      **kw)
+
+    def loss(hh, ww):
+        o2, _, _ = o.policy_step(kind, hh @ ww.t(), tgt, old, adv, mask, exact=True, **kw)
+        return float(o2["loss"])
+
+    assert abs(loss(h, w) - float(out["loss"])) < 1e-14
+    eps = 1e-6
+    for idx in [(0, 0, 0), (1, 3, 6), (0, 4, 2)]:
+        e = torch.zeros_like(h)
+        e[idx] = eps
+        fd = (loss(h + e, w) - loss(h - e, w)) / (2 * eps)
+        assert abs(fd - float(dh[idx])) <= 1e-7 * max(1.0, abs(fd)), (idx, fd, float(dh[idx]))
+    for idx in [(0, 0), (int(tgt[0, 1]), 3), (12, 6)]:
+        e = torch.zeros_like(w)
+        e[idx] = eps
+        fd = (loss(h, w + e) - loss(h, w - e)) / (2 * eps)
+        assert abs(fd - float(dw[idx])) <= 1e-7 * max(1.0, abs(fd)), (idx, fd, float(dw[idx]))
