@@ -167,8 +167,16 @@ def make_inputs(cfg, device, seed):
                 rewards=rewards, values=values, mask=mask, B=B, T=T, V=V)
 
 
-def make_step(inp, cfg, path, objective, skip_masked=False):
-    """One timed step of the config's training-step hot path."""
+def _watch(lp, probe):
+    if probe is not None:
+        lp.register_hook(lambda g: probe.__setitem__("active", int((g != 0).sum().item())))
+
+
+def make_step(inp, cfg, path, objective, skip_masked=False, probe=None):
+    """One timed step of the config's training-step hot path.  With ``probe``
+    (a dict; composed path only, never in a timed step) the step also records
+    how many token rows receive a non-zero d loss / d logp: the backward
+    kernel reads the logits of those rows only."""
 
     from rosellm_amd import roserlhf as R
 
@@ -195,6 +203,7 @@ def make_step(inp, cfg, path, objective, skip_masked=False):
                                                  row_block=LM_HEAD_ROW_BLOCK, **kw)
             else:
                 lp = R.gather_token_logprobs(F.linear(hidden, weight), actions)
+                _watch(lp, probe)
                 out = R.clipped_policy_loss(lp, old, a, mask, **kw)
             out.loss.backward()
             return out
@@ -236,6 +245,7 @@ def make_step(inp, cfg, path, objective, skip_masked=False):
         def step():
             logits.grad = None
             lp = R.gather_token_logprobs(logits, actions)
+            _watch(lp, probe)
             out = fn(lp, old, advantages(), mask, **kw)
             out.loss.backward()
             return out
@@ -400,9 +410,20 @@ def main():
         "rrl_fused_logprob_policy": N * (V * (in_b + in_b) + SIDE_BYTES),
         # read logits, 8 target, write 4 logp + 4 lse
         "rrl_logprob_fwd": N * (V * in_b + 8 + 4 + 4),
-        # read logits + write dlogits, 8 target + 4 lse + 4 logp + 4 g
+        # read logits + write dlogits, 8 target + 4 lse + 4 logp + 4 g (the
+        # logits read is narrowed to the rows with a non-zero g below)
         "rrl_logprob_bwd": N * (V * (in_b + in_b) + 8 + 4 + 4 + 4),
     }
+    if path == "composed":
+        # Rows whose d loss / d logp is exactly zero (masked, clipped or
+        # zero-advantage tokens) are written as zeros without reading their
+        # logits: count them on one extra, untimed step.
+        probe = {}
+        make_step(inp, cfg, path, objective, probe=probe)()
+        torch.cuda.synchronize()
+        active = probe["active"]
+        alg["rrl_logprob_bwd"] = N * V * in_b + active * V * in_b + N * (8 + 4 + 4 + 4)
+        log(f"[bench] backward reads the logits of {active} of {N} rows")
     kstats = {}
     for k in kernels:
         kms = [s.elapsed_time(e) for s, e in timed[k]]
