@@ -23,6 +23,11 @@ d hidden and d weight, through ``fused_linear_policy_loss`` (``--path
 composed``: F.linear, gather_token_logprobs, clipped_policy_loss, autograd);
 its roofline is MFMA-bound (3 x 2*N*H*V flops per step).
 
+``--config sft`` is the supervised next-token cross-entropy of the model
+forwards (rosetrainer/model.py:643-649) on config 2's logits, labels = the
+sampled tokens: ``rosellm_amd.rosetrainer.causal_lm_loss`` (the same
+single-pass row kernel, objective NLL) -> backward to bf16 dlogits.
+
 Prints one JSON line (rank 0): value = tokens/s over all B*T positions, plus
 ``roofline`` for the dominant kernel (HIP events around its entry point over
 the timed steps; algorithmic bytes N*(V*(2+2) + 21)) and ``cpu_baseline``, the
@@ -74,6 +79,10 @@ CONFIGS = {
                workload="C5: fused LM-head + logprob + GRPO PPO-clip fwd+bwd to dhidden and dW, "
                         "256x1024 tokens, hidden 1024, V=151936 bf16"),
 }
+CONFIGS["sft"] = dict(CONFIGS["c2"], objective="nll", kw={}, sft=True,
+                      workload="SFT: next-token cross-entropy fwd+bwd (rosetrainer/model.py:"
+                               "643-649), 256x1024 tokens, V=151936 bf16")
+SFT_SIDE_BYTES = 12  # per row: 8 label + 4 logp out
 LM_HEAD_ROW_BLOCK = 16384
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 def log(msg: str) -> None:
@@ -211,6 +220,19 @@ def make_step(inp, cfg, path, objective, skip_masked=False, probe=None):
 
     logits = inp["logits"].requires_grad_()
 
+    if cfg.get("sft"):
+        # SFT loss of the model forwards: position t scores label t+1.
+        from types import SimpleNamespace
+
+        from rosellm_amd import rosetrainer as RT
+
+        def step():
+            logits.grad = None
+            loss = RT.causal_lm_loss(logits, actions)
+            loss.backward()
+            return SimpleNamespace(loss=loss)
+        return step
+
     if objective == "sapo":
         # Config 4: GAE over the valid tokens, whitened, then SAPO.  dlogits
         # overwrite the logits (logits + dlogits would need 318.6 GB), so each
@@ -265,6 +287,8 @@ def cpu_baseline(inp, cfg, n_seq, runs):
         return cpu_baseline_lm_head(inp, cfg, n_seq, runs)
     x = inp["logits"].detach()[:n_seq].cpu()
     t = inp["actions"][:n_seq].cpu()
+    if cfg.get("sft"):
+        return cpu_baseline_sft(x, t, inp, n_seq, runs)
     old = inp["old"][:n_seq].cpu()
     mask = inp["mask"][:n_seq].cpu()
     objective = cfg["objective"]
@@ -295,6 +319,37 @@ def cpu_baseline(inp, cfg, n_seq, runs):
                    f"tensors), oracle log_softmax->gather->{objective}->autograd on the fp32 "
                    f"upcast, "
                    f"median of {runs} runs after 1 warm-up, torch threads={threads}, "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def cpu_baseline_sft(x, t, inp, n_seq, runs):
+    """SFT loss on the CPU: the oracle's shift -> log_softmax -> gather ->
+    mean -> autograd on the float32 upcast of the first n_seq sequences."""
+
+    import torch
+
+    from oracle import roserlhf_oracle as o
+
+    T = inp["T"]
+    threads = torch.get_num_threads()
+    times = []
+    for i in range(runs + 1):
+        t0 = time.perf_counter()
+        o.sft_step(x, t, causal=True)
+        dt = time.perf_counter() - t0
+        if i > 0:
+            times.append(dt)
+        log(f"[bench] cpu oracle run {i}: {dt:.2f} s")
+    med = statistics.median(times)
+    return {
+        "value": round(n_seq * T / med, 1),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"first {n_seq} of {inp['B']} sequences ({n_seq * T} token rows, same "
+                   f"tensors), oracle shift->log_softmax->gather->mean->autograd on the fp32 "
+                   f"upcast, median of {runs} runs after 1 warm-up, torch threads={threads}, "
                    f"os.cpu_count()={os.cpu_count()}"),
     }
 
@@ -384,6 +439,8 @@ def main():
     # GSPO needs every token's log-prob before any gradient: its fused entry is
     # the two-kernel composition (forward sweep, backward sweep).
     path = args.path if objective in ("clipped", "sapo") else "composed"
+    if cfg.get("sft"):
+        path = "fused"
     step = make_step(inp, cfg, path, objective)
 
     for i in range(args.warmup):
@@ -404,10 +461,13 @@ def main():
     ms_step = elapsed * 1e3 / args.steps
     tok_s = N / (elapsed / args.steps)
     in_b = (inp["hidden"] if cfg.get("lm_head") else inp["logits"]).element_size()
+    # Rows one launch of the single-pass kernel processes, and their side data
+    # (the SFT loss scores the B*(T-1) positions that have a next token).
+    k_rows, side = (inp["B"] * (inp["T"] - 1), SFT_SIDE_BYTES) if cfg.get("sft") else (N, SIDE_BYTES)
     # Algorithmic bytes per launch of each timed entry point.
     alg = {
         # read logits + write dlogits, 8 target + 4 old + 4 advantage + 1 mask + 4 logp
-        "rrl_fused_logprob_policy": N * (V * (in_b + in_b) + SIDE_BYTES),
+        "rrl_fused_logprob_policy": k_rows * (V * (in_b + in_b) + side),
         # read logits, 8 target, write 4 logp + 4 lse
         "rrl_logprob_fwd": N * (V * in_b + 8 + 4 + 4),
         # read logits + write dlogits, 8 target + 4 lse + 4 logp + 4 g (the
@@ -479,7 +539,7 @@ def main():
             "kernels_ms": {k: round(v, 4) for k, v in kstats.items()},
             # whole step against the algorithmic minimum of one logits read and
             # one dlogits write
-            "step_frac": round(N * (V * 2 * in_b + SIDE_BYTES) / (ms_step * 1e-3) / 1e9
+            "step_frac": round(N * (V * 2 * in_b + side) / (ms_step * 1e-3) / 1e9
                                / HBM_PEAK_GBS, 4),
         }
 

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define RRL_ABI_VERSION 1
+#define RRL_ABI_VERSION 2
 
 #if defined(__GNUC__)
 #define RRL_API __attribute__((visibility("default")))
@@ -79,10 +79,11 @@ enum rrl_flag {
 /* rrl_policy_params.flags bits. */
 enum rrl_policy_flag {
   RRL_POLICY_GENERIC = 1,     /* rrl_fused_logprob_policy: use the generic row kernel only */
-  RRL_POLICY_SKIP_MASKED = 2  /* rrl_fused_logprob_policy: a token whose mask weight is exactly 0
+  RRL_POLICY_SKIP_MASKED = 2, /* rrl_fused_logprob_policy: a token whose mask weight is exactly 0
                                  is not read; its dlogits row is written as zeros and its logp /
                                  lse as 0 (equal to the reference for finite logits, where such a
                                  row contributes exactly 0; no reference counterpart) */
+  RRL_POLICY_SUM = 4          /* RRL_OBJ_NLL: reduction "sum" instead of "mean" */
 };
 
 /* Policy objectives (losses.py). */
@@ -91,7 +92,16 @@ enum rrl_objective {
   RRL_OBJ_SAO = 1,        /* sao_policy_loss          losses.py:127-203 */
   RRL_OBJ_GSPO = 2,       /* gspo_policy_loss         losses.py:206-273 */
   RRL_OBJ_GSPO_TOKEN = 3, /* gspo_token_policy_loss   losses.py:276-352 */
-  RRL_OBJ_SAPO = 4        /* sapo_policy_loss         losses.py:355-423 */
+  RRL_OBJ_SAPO = 4,       /* sapo_policy_loss         losses.py:355-423 */
+  RRL_OBJ_NLL = 5         /* SFT next-token cross-entropy: F.cross_entropy(logits, labels) with
+                             ignore_index and reduction "mean" (or "sum"), as called by
+                             rosetrainer/model.py:643-649 and rosetrainer/qwen3.py:558-564.
+                             The objective is sum(w * logp) / sum(w) (or sum(w * logp)), the loss
+                             its negative.  The `mask` operand is the target ids themselves (I32
+                             or I64): w = 1 where the id differs from ignore_index, else 0, and an
+                             ignored id is not range-checked.  An all-ignored batch gives a NaN
+                             "mean" objective and zero gradients, as F.cross_entropy does; no
+                             EMPTY_MASK flag is raised. */
 };
 
 /* Scalar outputs of rrl_policy_fwd, in this order (acc dtype):
@@ -100,6 +110,7 @@ enum rrl_objective {
  *   GSPO(/tok): objective, sequence_ratio_divergence, sequence_clip_fraction,
  *               mean_sequence_ratio
  *   SAPO:       objective, approximate_kl, mean_ratio, mean_gradient_gate
+ *   NLL:        objective, number of non-ignored tokens
  * Slots 4..7 are reserved.  rrl_policy_bwd takes upstream gradients in the
  * same slots (non-differentiable slots are ignored). */
 #define RRL_NSCALARS 8
@@ -122,6 +133,7 @@ typedef struct rrl_policy_params {
   double max_log_ratio;
   double tau_positive;   /* SAPO */
   double tau_negative;   /* SAPO */
+  int64_t ignore_index;  /* NLL: target id that carries no loss (F.cross_entropy's ignore_index) */
 } rrl_policy_params;
 
 RRL_API const char* rrl_last_error(void);
@@ -180,11 +192,11 @@ RRL_API int rrl_policy_bwd(const rrl_policy_params* params, int64_t B, int64_t T
                    void* grad_cur, void* stream);
 
 /* ---- single pass: log-prob + token-local objective gradient --------------
- * For PPO, SAO and SAPO, d loss / d logp is token-local once the mask
+ * For PPO, SAO, SAPO and NLL, d loss / d logp is token-local once the mask
  * denominators are known, so one sweep over each logits row produces logp,
  * lse and dlogits = d(-objective)/d logits.  rrl_policy_row_coef first writes
- * row_coef[b] (acc, [B]): 1/sum(mask weight) for PPO/SAO, 1/(B*L_b) for SAPO,
- * and flags EMPTY_MASK / EMPTY_ROW.  The objective scalars then come from
+ * row_coef[b] (acc, [B]): 1/sum(mask weight) for PPO/SAO/NLL (1 for NLL with
+ * RRL_POLICY_SUM), 1/(B*L_b) for SAPO, and flags EMPTY_MASK / EMPTY_ROW.  The objective scalars then come from
  * rrl_policy_fwd on the returned logp.
  * records: caller workspace of rrl_fused_records_bytes(B, T) bytes, where the
  * 16-bit fast path packs each token's target, old log-prob, advantage and

@@ -277,3 +277,39 @@ def whiten(values, mask, eps=1e-8):
 
 def gather_rows(seq: Sequence[float]) -> np.ndarray:
     return np.asarray(seq, dtype=np.float64)
+
+
+def nll_grad(labels, *, ignore_index=-100, reduction="mean") -> np.ndarray:
+    """d loss / d logp of the SFT cross-entropy per token: -1/n for each of the
+    n labels that differ from ignore_index ("mean"), -1 ("sum"), 0 for an
+    ignored label."""
+
+    y = np.asarray(labels).reshape(-1)
+    n = sum(1 for v in y if v != ignore_index)
+    out = np.zeros(y.shape[0])
+    for i, v in enumerate(y):
+        if v != ignore_index:
+            out[i] = -1.0 if reduction == "sum" else -1.0 / n
+    return out.reshape(np.asarray(labels).shape)
+
+
+def nll_loss(logits, labels, *, ignore_index=-100, reduction="mean") -> float:
+    """Scalar-loop SFT loss: -sum over kept tokens of log p(label) (/ n)."""
+
+    x = np.asarray(logits, dtype=np.float64)
+    flat = x.reshape(-1, x.shape[-1])
+    y = np.asarray(labels).reshape(-1)
+    total, n = 0.0, 0
+    for r in range(flat.shape[0]):
+        if y[r] == ignore_index:
+            continue
+        row = flat[r]
+        m = max(row)
+        s = 0.0
+        for v in row:
+            s += math.exp(v - m)
+        total += row[int(y[r])] - (m + math.log(s))
+        n += 1
+    if reduction == "sum":
+        return -total
+    return -total / n if n else float("nan")

@@ -10,7 +10,9 @@ upcast (the parity contract of the GPU kernels).
 Pinned by: the reference's known-answer tests (tests/golden), float64 brute
 force (oracle/brute.py), closed-form gradients, and invariants — see
 tests/test_oracle.py.  ``masked_whiten`` has no reference counterpart: parity
-unpinned (closed form and invariants only).
+unpinned (closed form and invariants only).  ``nll_loss`` / ``sft_step`` (the
+SFT loss of rosetrainer/model.py:643-649) are pinned by torch's own
+F.cross_entropy in float64 and by the scalar loops of oracle/brute.py.
 """
 
 from __future__ import annotations
@@ -406,6 +408,55 @@ def lm_head_step(kind: str, hidden: Tensor, weight: Tensor, logits: Tensor, targ
     dh = (d2 @ weight.to(wide)).reshape(hidden.shape)
     dw = d2.t() @ h2
     return out, lp, dh, dw
+
+
+# ---------------------------------------------------------------------------
+# SFT next-token cross-entropy (rosetrainer/model.py:643-649,
+# rosetrainer/qwen3.py:558-564)
+# ---------------------------------------------------------------------------
+
+
+def nll_loss(logits: Tensor, labels: Tensor, *, ignore_index: int = -100,
+             reduction: str = "mean", exact: bool = False) -> Tensor:
+    """F.cross_entropy(logits.view(-1, V), labels.view(-1)) restated from its
+    definition: the vocabulary log-softmax, a gather at each label, and the
+    negated mean (or sum) over the labels that differ from ``ignore_index``
+    (the class dimension is last).  An ignored label is never gathered; the
+    "mean" of no tokens is 0/0 = NaN.  Other ids outside [0, V) raise
+    IndexError, as F.cross_entropy does."""
+
+    V = logits.shape[-1]
+    x = logits.reshape(-1, V)
+    y = labels.reshape(-1).long()
+    keep = y != ignore_index
+    if bool(((y < 0) | (y >= V))[keep].any()):
+        raise IndexError("Target is out of bounds")
+    lp = token_logprobs(x, torch.where(keep, y, torch.zeros_like(y)), exact=exact)
+    total = torch.where(keep, lp, torch.zeros_like(lp)).sum()
+    if reduction == "sum":
+        return -total
+    return -(total / keep.sum().to(total.dtype))
+
+
+def sft_step(logits: Tensor, labels: Tensor, *, causal: bool = True, ignore_index: int = -100,
+             reduction: str = "mean", exact: bool = False) -> Tuple[Tensor, Tensor]:
+    """The reference's LM loss and its gradient: with ``causal`` the shift of
+    rosetrainer/model.py:644-645 (logits [B, T, V] at t score labels at t+1),
+    then nll_loss, then autograd.  Returns (loss, dlogits of the full logits'
+    shape; zero rows at the last position when causal).  16-bit logits are
+    evaluated on their float32 upcast (float64 with ``exact``)."""
+
+    x = logits.detach()
+    wide = torch.float64 if exact else (
+        torch.float32 if x.dtype in (torch.bfloat16, torch.float16) else x.dtype)
+    x = x.to(wide).requires_grad_()
+    if causal:
+        loss = nll_loss(x[:, :-1], labels[:, 1:], ignore_index=ignore_index,
+                        reduction=reduction)
+    else:
+        loss = nll_loss(x, labels, ignore_index=ignore_index, reduction=reduction)
+    loss.backward()
+    return loss.detach(), x.grad
 
 
 def clip_bounds(clip_low: float, clip_high: float) -> Tuple[float, float]:

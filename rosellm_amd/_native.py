@@ -43,9 +43,10 @@ FLAG_FAST_RANGE = 16
 # rrl_policy_flag
 POLICY_GENERIC = 1
 POLICY_SKIP_MASKED = 2
+POLICY_SUM = 4
 
 # rrl_objective
-OBJ_PPO, OBJ_SAO, OBJ_GSPO, OBJ_GSPO_TOKEN, OBJ_SAPO = range(5)
+OBJ_PPO, OBJ_SAO, OBJ_GSPO, OBJ_GSPO_TOKEN, OBJ_SAPO, OBJ_NLL = range(6)
 NSCALARS = 8
 
 
@@ -69,6 +70,7 @@ class RrlPolicyParams(ctypes.Structure):
         ("max_log_ratio", ctypes.c_double),
         ("tau_positive", ctypes.c_double),
         ("tau_negative", ctypes.c_double),
+        ("ignore_index", ctypes.c_int64),
     ]
 
 

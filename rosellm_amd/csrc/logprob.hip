@@ -35,7 +35,11 @@ __global__ __launch_bounds__(NT) void row_kernel(RowArgs a) {
     const int64_t tgt = load_index(a.tgt.ptr, a.tgt.dt, b * a.tgt.sr + t * a.tgt.sc);
     const bool tgt_ok = tgt >= 0 && tgt < a.V;
     const int64_t tgt_safe = tgt_ok ? tgt : 0;  // never address outside the row
-    const Acc xt = tgt_ok ? Tag::cvt(row[tgt_safe]) : M<Acc>::nan();
+    // A row without a valid target (NLL's ignored label; an out-of-range id,
+    // which is flagged) takes xt = -inf: e_t = 0, so the log-sum-exp stays the
+    // row's own and its gradient row is exact (zeros when g = 0); its log-prob
+    // is set to NaN below.
+    const Acc xt = tgt_ok ? Tag::cvt(row[tgt_safe]) : -M<Acc>::inf();
 
     Acc lse, g, logp;
     bool have_logp = true;
@@ -46,14 +50,15 @@ __global__ __launch_bounds__(NT) void row_kernel(RowArgs a) {
       logp = have_logp ? static_cast<const Acc*>(a.logp_in)[r] : Acc(0);
       if (threadIdx.x == 0 && !tgt_ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
     } else if (MODE == MODE_FUSED && (a.pp.flags & RRL_POLICY_SKIP_MASKED) &&
-               mask_weight<Acc>(PolicyConsts<Acc>::make(a.pp), a.mask, b, t) *
-                       static_cast<const Acc*>(a.row_coef)[b] == Acc(0)) {
+               weight_coef(mask_weight<Acc>(PolicyConsts<Acc>::make(a.pp), a.mask, b, t),
+                           static_cast<const Acc*>(a.row_coef)[b]) == Acc(0)) {
       // Zero-weight row under RRL_POLICY_SKIP_MASKED: never read.
       lse = Acc(0);
       logp = Acc(0);
       g = Acc(0);
       if (threadIdx.x == 0) {
-        if (!tgt_ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+        if (!tgt_ok && !target_ignored(PolicyConsts<Acc>::make(a.pp), tgt))
+          raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
         store_as<Acc>(a.logp, a.logp_dt, r, logp);
         static_cast<Acc*>(a.lse_out)[r] = lse;
       }
@@ -89,10 +94,11 @@ __global__ __launch_bounds__(NT) void row_kernel(RowArgs a) {
         const Acc w = mask_weight<Acc>(c, a.mask, b, t);
         const Acc coef = static_cast<const Acc*>(a.row_coef)[b];
         // loss = -objective, so dlogits carries d(-objective)/d logp.
-        g = -((w * coef) * token_local_grad<Acc>(c, logp, o, A));
+        g = -(weight_coef(w, coef) * token_local_grad<Acc>(c, logp, o, A));
       }
       if (threadIdx.x == 0) {
-        if (!tgt_ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+        if (!tgt_ok && !(MODE == MODE_FUSED && target_ignored(PolicyConsts<Acc>::make(a.pp), tgt)))
+          raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
         store_as<Acc>(a.logp, a.logp_dt, r, logp);
         static_cast<Acc*>(a.lse_out)[r] = lse;
       }
@@ -222,8 +228,9 @@ extern "C" int rrl_fused_logprob_policy(const rrl_policy_params* params, const v
   clear_error();
   RRL_REQUIRE(params != nullptr, RRL_EINVAL, "params is null");
   RRL_REQUIRE(params->kind == RRL_OBJ_PPO || params->kind == RRL_OBJ_SAO ||
-                  params->kind == RRL_OBJ_SAPO,
-              RRL_EINVAL, "single-pass path supports the token-local objectives PPO, SAO, SAPO");
+                  params->kind == RRL_OBJ_SAPO || params->kind == RRL_OBJ_NLL,
+              RRL_EINVAL,
+              "single-pass path supports the token-local objectives PPO, SAO, SAPO, NLL");
   int rc = validate_logits(logits, logits_dtype, B, T, V, targets);
   if (rc) return rc;
   RRL_REQUIRE(is_float_dtype(dl_dtype), RRL_EDTYPE, "dlogits dtype must be floating point");
@@ -233,6 +240,8 @@ extern "C" int rrl_fused_logprob_policy(const rrl_policy_params* params, const v
   RRL_REQUIRE(is_float_dtype(old.dtype) && is_float_dtype(adv.dtype), RRL_EDTYPE,
               "old log-probs and advantages must be floating point");
   RRL_REQUIRE(is_known_dtype(mask.dtype), RRL_EDTYPE, "unsupported mask dtype");
+  RRL_REQUIRE(params->kind != RRL_OBJ_NLL || mask.dtype == RRL_I32 || mask.dtype == RRL_I64,
+              RRL_EDTYPE, "NLL: the mask operand holds the target ids (int32 or int64)");
   RowArgs a{};
   a.logits = logits; a.B = B; a.T = T; a.V = V; a.ls_b = ls_b; a.ls_t = ls_t;
   a.tgt = to_view(targets);

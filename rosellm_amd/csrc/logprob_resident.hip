@@ -100,12 +100,12 @@ __global__ __launch_bounds__(256) void pack_records_kernel(RowArgs a) {
     const int64_t b = i / a.T, t = i - (i / a.T) * a.T;
     const int64_t tgt = load_index(a.tgt.ptr, a.tgt.dt, b * a.tgt.sr + t * a.tgt.sc);
     const bool ok = tgt >= 0 && tgt < a.V;
-    if (!ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+    if (!ok && !target_ignored(c, tgt)) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
     TokenRecord r;
     r.target = ok ? (int32_t)tgt : -1;
     r.old = a.old.get<float>(b, t);
     r.adv = a.adv.get<float>(b, t);
-    r.wcoef = mask_weight<float>(c, a.mask, b, t) * coef[b];
+    r.wcoef = weight_coef(mask_weight<float>(c, a.mask, b, t), coef[b]);
     rec[i] = r;
   }
 }
@@ -236,7 +236,9 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     if (!skip) {  // uniform over the workgroup
 #pragma unroll
       for (int k = 0; k < SL; ++k) fold(k);
-      if (!tgt_ok && tid == 0) sh_xt = __builtin_nanf("");
+      // No valid target: xt = -inf keeps the row's log-sum-exp finite (the
+      // log-prob is set to NaN below).
+      if (!tgt_ok && tid == 0) sh_xt = -__builtin_huge_valf();
       // Workgroup combine.  sh_xt is written before the first barrier and read
       // before the second, so the next row's write cannot overtake a read.
 #pragma unroll

@@ -56,13 +56,18 @@ __global__ __launch_bounds__(NT) void policy_rows_kernel(PolicyArgs a) {
   for (int64_t b = blockIdx.x; b < a.B; b += gridDim.x) {
     Acc v[7] = {Acc(0), Acc(0), Acc(0), Acc(0), Acc(0), Acc(0), Acc(0)};
     for (int64_t t = threadIdx.x; t < a.T; t += NT) {
-      const bool mt = a.mask.truth(b, t);
       const Acc w = mask_weight<Acc>(c, a.mask, b, t);
+      const bool mt = c.kind == RRL_OBJ_NLL ? w != Acc(0) : a.mask.truth(b, t);
       v[0] += mt ? Acc(1) : Acc(0);
       v[1] += w;
       if (STATS_ONLY) continue;
       const Acc l = a.cur.get<Acc>(b, t);
       const Acc o = a.old.get<Acc>(b, t);
+      if (c.kind == RRL_OBJ_NLL) {
+        // An ignored token's log-prob may be NaN (no target): select, not multiply.
+        v[3] += w != Acc(0) ? l * w : Acc(0);
+        continue;
+      }
       v[2] += (l - o) * w;
       if (c.kind == RRL_OBJ_PPO) {
         const Acc A = a.adv.get<Acc>(b, t);
@@ -133,7 +138,7 @@ __global__ __launch_bounds__(NT) void policy_finalize_kernel(PolicyArgs a) {
     const Acc* rs = ws.rows + b * RS;
     const Acc cnt = rs[0];
     if (per_seq) v[7] += (cnt == Acc(0)) ? Acc(1) : Acc(0);
-    if (c.kind == RRL_OBJ_PPO || c.kind == RRL_OBJ_SAO) {
+    if (c.kind == RRL_OBJ_PPO || c.kind == RRL_OBJ_SAO || c.kind == RRL_OBJ_NLL) {
       v[0] += rs[1];
       v[3] += rs[3];
       v[4] += rs[4];
@@ -162,7 +167,14 @@ __global__ __launch_bounds__(NT) void policy_finalize_kernel(PolicyArgs a) {
   if (threadIdx.x == 0) {
     Acc* out = static_cast<Acc*>(a.scalars);
     for (int k = 0; k < RRL_NSCALARS; ++k) out[k] = Acc(0);
-    if (c.kind == RRL_OBJ_PPO || c.kind == RRL_OBJ_SAO) {
+    if (c.kind == RRL_OBJ_NLL) {
+      // F.cross_entropy: "mean" divides by the number of non-ignored tokens
+      // (NaN when there is none, no error); "sum" does not divide.
+      const bool sum = (a.pp.flags & RRL_POLICY_SUM) != 0;
+      ws.glob[0] = sum ? Acc(1) : v[0];
+      out[0] = sum ? v[3] : v[3] / v[0];
+      out[1] = v[0];
+    } else if (c.kind == RRL_OBJ_PPO || c.kind == RRL_OBJ_SAO) {
       const Acc Mw = v[0];
       if (Mw == Acc(0)) raise_flag(a.status, RRL_FLAG_EMPTY_MASK);
       ws.glob[0] = Mw;
@@ -249,7 +261,9 @@ __global__ __launch_bounds__(NT) void policy_bwd_kernel(PolicyArgs a) {
     for (int64_t t = threadIdx.x; t < a.T; t += NT) {
       const Acc w = mask_weight<Acc>(c, a.mask, b, t);
       Acc gr = Acc(0);
-      if (c.kind == RRL_OBJ_PPO) {
+      if (c.kind == RRL_OBJ_NLL) {
+        gr = w != Acc(0) ? (w / ws.glob[0]) * G0 : Acc(0);
+      } else if (c.kind == RRL_OBJ_PPO) {
         const Acc l = a.cur.get<Acc>(b, t), o = a.old.get<Acc>(b, t), A = a.adv.get<Acc>(b, t);
         Acc rho, safe, d;
         (void)ppo_token(c, l, o, A, rho, safe, d);
@@ -297,14 +311,16 @@ __global__ __launch_bounds__(NT) void row_coef_kernel(PolicyArgs a) {
   }
   block_sum<NT, 2, Acc>(v, sh);
   const bool per_seq = a.pp.kind == RRL_OBJ_SAPO;
+  const bool nll = a.pp.kind == RRL_OBJ_NLL;
   if (threadIdx.x == 0) {
-    if (!per_seq && v[0] == Acc(0)) raise_flag(a.status, RRL_FLAG_EMPTY_MASK);
+    if (!per_seq && !nll && v[0] == Acc(0)) raise_flag(a.status, RRL_FLAG_EMPTY_MASK);
     if (per_seq && v[1] != Acc(0)) raise_flag(a.status, RRL_FLAG_EMPTY_ROW);
   }
   Acc* coef = static_cast<Acc*>(a.row_coef);
   const Acc Bf = (Acc)a.B;
+  const Acc flat = (nll && (a.pp.flags & RRL_POLICY_SUM)) ? Acc(1) : Acc(1) / v[0];
   for (int64_t b = threadIdx.x; b < a.B; b += NT) {
-    coef[b] = per_seq ? (Acc(1) / ws.rows[b * RS + 0]) / Bf : Acc(1) / v[0];
+    coef[b] = per_seq ? (Acc(1) / ws.rows[b * RS + 0]) / Bf : flat;
   }
 }
 
@@ -329,7 +345,7 @@ int run_policy_fwd(const PolicyArgs& a, hipStream_t st) {
 
 int validate_policy(const rrl_policy_params* p, int64_t B, int64_t T, int acc) {
   RRL_REQUIRE(p != nullptr, RRL_EINVAL, "params is null");
-  RRL_REQUIRE(p->kind >= RRL_OBJ_PPO && p->kind <= RRL_OBJ_SAPO, RRL_EINVAL, "unknown objective kind");
+  RRL_REQUIRE(p->kind >= RRL_OBJ_PPO && p->kind <= RRL_OBJ_NLL, RRL_EINVAL, "unknown objective kind");
   RRL_REQUIRE(B >= 0 && T >= 0, RRL_EINVAL, "negative size");
   RRL_REQUIRE(acc == RRL_F32 || acc == RRL_F64, RRL_EDTYPE, "acc dtype must be float32 or float64");
   return RRL_OK;
@@ -358,6 +374,8 @@ extern "C" int rrl_policy_fwd(const rrl_policy_params* params, int64_t B, int64_
   RRL_REQUIRE(is_float_dtype(cur.dtype) && is_float_dtype(old.dtype) && is_float_dtype(adv.dtype),
               RRL_EDTYPE, "log-probabilities and advantages must be floating point");
   RRL_REQUIRE(is_known_dtype(mask.dtype), RRL_EDTYPE, "unsupported mask dtype");
+  RRL_REQUIRE(params->kind != RRL_OBJ_NLL || mask.dtype == RRL_I32 || mask.dtype == RRL_I64,
+              RRL_EDTYPE, "NLL: the mask operand holds the target ids (int32 or int64)");
   PolicyArgs a{};
   a.pp = *params; a.B = B; a.T = T;
   a.cur = to_view(cur); a.old = to_view(old); a.adv = to_view(adv); a.mask = to_view(mask);
@@ -396,10 +414,12 @@ extern "C" int rrl_policy_row_coef(const rrl_policy_params* params, int64_t B, i
   clear_error();
   if (int rc = validate_policy(params, B, T, acc_dtype)) return rc;
   RRL_REQUIRE(params->kind == RRL_OBJ_PPO || params->kind == RRL_OBJ_SAO ||
-                  params->kind == RRL_OBJ_SAPO,
+                  params->kind == RRL_OBJ_SAPO || params->kind == RRL_OBJ_NLL,
               RRL_EINVAL, "row coefficients exist for the token-local objectives only");
   RRL_REQUIRE(workspace && (B == 0 || (row_coef && mask.ptr)), RRL_EINVAL, "null pointer argument");
   RRL_REQUIRE(is_known_dtype(mask.dtype), RRL_EDTYPE, "unsupported mask dtype");
+  RRL_REQUIRE(params->kind != RRL_OBJ_NLL || mask.dtype == RRL_I32 || mask.dtype == RRL_I64,
+              RRL_EDTYPE, "NLL: the mask operand holds the target ids (int32 or int64)");
   PolicyArgs a{};
   a.pp = *params; a.B = B; a.T = T; a.mask = to_view(mask);
   a.ws = workspace; a.row_coef = row_coef; a.status = status;

@@ -15,6 +15,7 @@ struct PolicyConsts {
   bool detach;
   int kind;
   bool mask_is_weight;
+  int64_t ignore_index;  // NLL only
   __host__ __device__ static PolicyConsts make(const rrl_policy_params& p) {
     PolicyConsts c;
     c.lo = (Acc)(1.0 - p.clip_low);
@@ -25,6 +26,7 @@ struct PolicyConsts {
     c.detach = p.detach_ratio != 0;
     c.kind = p.kind;
     c.mask_is_weight = p.mask_is_weight != 0;
+    c.ignore_index = p.ignore_index;
     return c;
   }
 };
@@ -88,9 +90,10 @@ __device__ __forceinline__ Acc sapo_token(const PolicyConsts<Acc>& c, Acc l, Acc
 }
 
 // d(token term)/d logp used by the single-pass kernel for the token-local
-// objectives (PPO, SAO, SAPO).
+// objectives (PPO, SAO, SAPO, and NLL, whose term is logp itself).
 template <typename Acc>
 __device__ __forceinline__ Acc token_local_grad(const PolicyConsts<Acc>& c, Acc l, Acc o, Acc A) {
+  if (c.kind == RRL_OBJ_NLL) return Acc(1);
   Acc rho, safe;
   if (c.kind == RRL_OBJ_PPO) {
     Acc d;
@@ -109,10 +112,29 @@ __device__ __forceinline__ Acc token_local_grad(const PolicyConsts<Acc>& c, Acc 
 }
 
 // Weight of token (b, t) in the objective's sum (mask semantics per function).
+// For NLL the mask operand holds the target ids: weight 1 unless the id is
+// F.cross_entropy's ignore_index.
 template <typename Acc>
 __device__ __forceinline__ Acc mask_weight(const PolicyConsts<Acc>& c, const View& mask,
                                            int64_t b, int64_t t) {
+  if (c.kind == RRL_OBJ_NLL)
+    return load_index(mask.ptr, mask.dt, b * mask.sr + t * mask.sc) != c.ignore_index ? Acc(1)
+                                                                                     : Acc(0);
   return c.mask_is_weight ? mask.get<Acc>(b, t) : (mask.truth(b, t) ? Acc(1) : Acc(0));
+}
+
+// Whether target id `tgt` is exempt from the [0, V) range check: NLL's ignored
+// ids, which carry no loss (F.cross_entropy skips them).
+template <typename Acc>
+__device__ __forceinline__ bool target_ignored(const PolicyConsts<Acc>& c, int64_t tgt) {
+  return c.kind == RRL_OBJ_NLL && tgt == c.ignore_index;
+}
+
+// Mask weight times the row coefficient, exactly 0 for a zero weight even when
+// the coefficient is infinite (NLL's "mean" over an all-ignored batch, 1/0).
+template <typename Acc>
+__device__ __forceinline__ Acc weight_coef(Acc w, Acc coef) {
+  return w == Acc(0) ? Acc(0) : w * coef;
 }
 
 }  // namespace rrl

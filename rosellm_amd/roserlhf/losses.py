@@ -243,7 +243,12 @@ _PER_ROW = (nat.OBJ_GSPO, nat.OBJ_GSPO_TOKEN, nat.OBJ_SAPO)
 
 def _raise_flags(flags: int, kind: int) -> None:
     if flags & nat.FLAG_TARGET_RANGE:
+        if kind == nat.OBJ_NLL:  # F.cross_entropy's error type
+            raise IndexError("Target is out of bounds: every label other than ignore_index "
+                             "must lie in [0, vocabulary)")
         _raise_target_range()
+    if kind == nat.OBJ_NLL:
+        return
     if kind in _PER_ROW and flags & nat.FLAG_EMPTY_ROW:
         raise ValueError("every sequence needs at least one action token")
     if kind not in _PER_ROW and flags & nat.FLAG_EMPTY_MASK:
