@@ -70,10 +70,12 @@ enum rrl_flag {
   RRL_FLAG_EMPTY_ROW = 2,        /* some row has no action token          (losses.py:250-251) */
   RRL_FLAG_TARGET_RANGE = 4,     /* target id outside [0, V)              (gather, losses.py:36) */
   RRL_FLAG_INVALID_TURN = 8,     /* unmasked token with invalid turn id   (advantages.py:284-286) */
-  RRL_FLAG_FAST_RANGE = 16       /* rrl_fused_logprob_policy's 16-bit register-resident kernel met a
+  RRL_FLAG_FAST_RANGE = 16,      /* rrl_fused_logprob_policy's 16-bit register-resident kernel met a
                                     row with finite |log-sum-exp| > 2e38, outside its exponent range;
                                     that call's outputs are undefined: rerun it with
                                     RRL_POLICY_GENERIC set (no reference counterpart) */
+  RRL_FLAG_BAD_PROBS = 32        /* rrl_sample_logprobs: a row holds NaN or +inf logits (torch.multinomial
+                                    rejects such probabilities, roseinfer/engine.py:1155,1169) */
 };
 
 /* rrl_policy_params.flags bits. */
@@ -278,6 +280,40 @@ RRL_API int rrl_broadcast_turn(int64_t B, int64_t K, int64_t T, rrl_view turn_ad
 RRL_API int rrl_masked_whiten(int64_t B, int64_t T, rrl_view x, rrl_view mask, double eps,
                       int32_t shift_mean, int32_t acc_dtype, void* workspace, void* out,
                       int32_t out_dtype, int32_t* status, void* stream);
+
+/* ---- rollout side: next-token sampling with behaviour log-probs -------------
+ * Replaces the token choice of roseinfer/engine.py:1103-1171
+ * (InferenceEngine._sample_next_token_batch, its PyTorch path) and adds the
+ * log-probabilities that rosellm/roserlhf/trajectory.py:15,27-28 requires per
+ * sampled token.  logits: [B, V] rows of F32, BF16 or F16, row r at
+ * logits + r*row_stride elements.  Per row:
+ *   - greedy (do_sample == 0 or temperature <= 0): the lowest index of the
+ *     maximum (torch.argmax);
+ *   - else x/temperature; candidates = the top_k largest when 0 < top_k < V
+ *     (ties at the k-th value kept lowest index first), else the whole row;
+ *     p = softmax over the candidates; when 0 < top_p < 1, a candidate is
+ *     kept iff its inclusive cumulative p in descending order (ties lowest
+ *     index first) is <= top_p, the first always; q = max(p * kept, 1e-9) over
+ *     the candidates (the reference's masked_fill + clamp_min(1e-9)), 0
+ *     elsewhere; the token is the first index, in vocabulary order, whose
+ *     inclusive cumulative q exceeds u * sum(q), with one uniform
+ *     u = (r >> 8) * 2^-24 per row from Philox4x32-10 (Salmon et al., SC'11)
+ *     of counter {row, row >> 32, offset, offset >> 32} and key {seed, seed >> 32}
+ *     (r = its first output word).
+ * Outputs (contiguous [B]): token_out (int64); logp_out (float32) the token's
+ * log_softmax(x / T) over the whole row, T = 1 when greedy, formed as the
+ * training kernels form log-probs; logq_out (float32, may be NULL) log(q/sum q),
+ * the log-probability of the sampling distribution (0 when greedy).
+ * status gets BAD_PROBS.  The arithmetic is float32 on the exact upcast of
+ * the logits (the reference divides and normalises in the logits dtype). */
+RRL_API int rrl_sample_logprobs(const void* logits, int32_t logits_dtype, int64_t B, int64_t V,
+                        int64_t row_stride, double temperature, int64_t top_k, double top_p,
+                        int32_t do_sample, uint64_t seed, uint64_t offset, int64_t* token_out,
+                        float* logp_out, float* logq_out, int32_t* status, void* stream);
+
+/* Philox4x32-10 on the host (the generator rrl_sample_logprobs draws from):
+ * ctr[4] is replaced by the 4 output words. */
+RRL_API void rrl_philox4x32_10(uint32_t ctr[4], const uint32_t key[2]);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,7 @@ FLAG_EMPTY_ROW = 2
 FLAG_TARGET_RANGE = 4
 FLAG_INVALID_TURN = 8
 FLAG_FAST_RANGE = 16
+FLAG_BAD_PROBS = 32
 
 # rrl_policy_flag
 POLICY_GENERIC = 1
@@ -107,6 +108,9 @@ SIGNATURES = {
     "rrl_leave_one_out": (ctypes.c_int, [_I64, _I64, _V, _P, _I32, _P]),
     "rrl_broadcast_turn": (ctypes.c_int, [_I64, _I64, _I64, _V, _V, _V, _P, _I32, _P, _P]),
     "rrl_masked_whiten": (ctypes.c_int, [_I64, _I64, _V, _V, _D, _I32, _I32, _P, _P, _I32, _P, _P]),
+    "rrl_sample_logprobs": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _D, _I64, _D, _I32,
+                                           ctypes.c_uint64, ctypes.c_uint64, _P, _P, _P, _P, _P]),
+    "rrl_philox4x32_10": (None, [ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32)]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

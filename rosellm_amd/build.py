@@ -27,6 +27,7 @@ SOURCES = [
     "logprob_resident.hip",
     "objectives.hip",
     "estimators.hip",
+    "sampler.hip",
 ]
 
 ARCH = os.environ.get("ROSELLM_AMD_ARCH", "gfx950")

@@ -1,0 +1,107 @@
+"""Next-token sampling with behaviour log-probs in one launch.
+
+The reference picks the next token in ``InferenceEngine._sample_next_token_batch``
+(roseinfer/engine.py:1103-1171): greedy argmax, or ``logits / temperature``
+restricted to the ``top_k`` largest and/or the ``top_p`` nucleus, then
+``torch.multinomial`` over ``softmax(...).clamp_min(1e-9)``.  It returns the
+token only, while every rollout token needs its behaviour log-probability
+(``PolicyAction.old_logprobs``, roserlhf/trajectory.py:15,27-28), which the
+trainer later compares with its own recomputation (the train/inference
+mismatch of docs/agentic-rl/systems.md:252-274).
+
+``sample_next_token_batch`` runs ``rrl_sample_logprobs``: one workgroup per
+row chooses the token by inverse CDF with a counter-based uniform (Philox4x32-10
+of row, ``offset`` and ``seed``: reproducible, no generator state on the
+device) and returns, with it,
+
+* ``logprobs``: ``log_softmax(logits / T)[token]`` over the whole row (T = 1
+  when greedy), formed as the training row kernels form log-probs — at T = 1
+  it is the value ``gather_token_logprobs`` recomputes;
+* ``sampling_logprobs``: ``log q(token)`` of the distribution actually
+  sampled (after top-k / top-p and the 1e-9 floor; 0 when greedy).
+
+The distribution is the reference's on the float32 upcast of the logits (the
+reference divides by T and normalises in the logits dtype); ties at a top-k or
+top-p threshold are kept lowest index first (torch.topk leaves their order
+unspecified).  Rows with NaN or +inf logits raise, as ``torch.multinomial``
+does.
+"""
+
+from __future__ import annotations
+
+from typing import NamedTuple, Optional
+
+import torch
+from torch import Tensor
+
+from .. import _native as nat
+
+__all__ = ["SampleOutput", "sample_next_token", "sample_next_token_batch"]
+
+
+class SampleOutput(NamedTuple):
+    token_ids: Tensor          # [B] int64
+    logprobs: Tensor           # [B] float32, log_softmax(logits / T)[token]
+    sampling_logprobs: Tensor  # [B] float32, log q(token) of the sampled distribution
+
+
+def _draw_seed(generator: Optional[torch.Generator]) -> int:
+    """A 63-bit seed from a host generator (no device sync)."""
+
+    return int(torch.randint(0, 2 ** 63 - 1, (1,), generator=generator, dtype=torch.int64).item())
+
+
+def sample_next_token_batch(
+    logits: Tensor,
+    temperature: float,
+    top_k: int,
+    top_p: float,
+    do_sample: bool,
+    *,
+    seed: Optional[int] = None,
+    offset: int = 0,
+    generator: Optional[torch.Generator] = None,
+) -> SampleOutput:
+    """Sample one token per row of ``logits`` [B, V] with the reference's
+    argument meaning (roseinfer/engine.py:1103-1171) and return its
+    log-probabilities.
+
+    ``seed`` and ``offset`` fix the uniforms (row r of a call uses counter
+    (r, offset)); with ``seed=None`` a seed is drawn from ``generator`` (a CPU
+    ``torch.Generator``, default: torch's global one).  A decode loop can keep
+    one seed and advance ``offset`` per step.
+    """
+
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be 2D [B, V], got shape={tuple(logits.shape)}")
+    if logits.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise TypeError("logits must be float32, bfloat16 or float16")
+    dev = nat.require_device(logits)
+    x = logits if logits.stride(-1) == 1 else logits.contiguous()
+    B, V = x.shape
+    if V == 0:
+        raise ValueError("logits need at least one vocabulary entry")
+    if seed is None:
+        seed = _draw_seed(generator)
+    tokens = torch.empty(B, dtype=torch.int64, device=dev)
+    logp = torch.empty(B, dtype=torch.float32, device=dev)
+    logq = torch.empty(B, dtype=torch.float32, device=dev)
+    status = nat.new_status(dev)
+    nat.call("rrl_sample_logprobs", x.data_ptr(), nat.dtype_code(x.dtype), B, V,
+             x.stride(0) if B > 1 else V, float(temperature), int(top_k), float(top_p),
+             int(bool(do_sample)), int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 64 - 1),
+             tokens.data_ptr(), logp.data_ptr(), logq.data_ptr(), status.data_ptr(),
+             nat.stream_ptr(dev))
+    if B and nat.read_status(status) & nat.FLAG_BAD_PROBS:
+        raise RuntimeError("probability tensor contains either `inf`, `nan` or element < 0")
+    return SampleOutput(tokens, logp, logq)
+
+
+def sample_next_token(logits: Tensor, temperature: float, top_k: int, top_p: float,
+                      do_sample: bool, **kw) -> int:
+    """The single-sequence form (roseinfer/engine.py:1088-1101): ``logits``
+    [..., V] are viewed as rows and the first row's token is returned."""
+
+    rows = logits.reshape(-1, int(logits.size(-1)))
+    return int(sample_next_token_batch(rows, temperature, top_k, top_p, do_sample,
+                                       **kw).token_ids[0].item())

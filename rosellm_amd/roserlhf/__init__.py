@@ -1,8 +1,10 @@
 """MI355X-native RoseRLHF hot path: same public names as ``rosellm.roserlhf``
 (rosellm/roserlhf/__init__.py:8-48), backed by gfx950 HIP kernels.
 
-``fused_policy_loss``, ``fused_linear_policy_loss``, ``linear_token_logprobs``
-and ``masked_whiten`` are additions of this package;
+``fused_policy_loss``, ``fused_linear_policy_loss``, ``linear_token_logprobs``,
+``masked_whiten`` and ``pack_trajectories`` are additions of this package;
+the record types live in ``rosellm_amd.roserlhf.trajectory`` as in the
+reference (rosellm/roserlhf/trajectory.py);
 ``losses.masked_mean`` and ``losses.sequence_log_ratio`` stay module-level as
 in the reference.
 """
@@ -17,6 +19,7 @@ from .advantages import (
     skip_observation_generalized_advantage_estimation,
 )
 from .linear import fused_linear_policy_loss, linear_token_logprobs
+from .packing import PackedTrajectories, pack_trajectories
 from .losses import (
     GspoPolicyLossOutput,
     PolicyLossOutput,
@@ -34,6 +37,7 @@ from .losses import (
 
 __all__ = [
     "GspoPolicyLossOutput",
+    "PackedTrajectories",
     "PolicyLossOutput",
     "SapoPolicyLossOutput",
     "SaoPolicyLossOutput",
@@ -51,6 +55,7 @@ __all__ = [
     "gspo_policy_loss",
     "gspo_token_policy_loss",
     "masked_whiten",
+    "pack_trajectories",
     "sapo_policy_loss",
     "sao_policy_loss",
     "skip_observation_generalized_advantage_estimation",

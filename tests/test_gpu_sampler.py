@@ -1,0 +1,139 @@
+"""Next-token sampling kernel (rrl_sample_logprobs) vs the CPU oracle on the
+same logits and the same Philox uniforms (MI355X).
+
+Bars: the sampled token equals the oracle's on every row whose uniform lies
+farther than 1e-5 of sum(q) from a cumulative boundary (the kernel's float32
+partial sums against the oracle's float64 ones); ``logprobs`` within 1e-5
+relative (+1e-6) of the float64 log_softmax(x/T) and, at T = 1, of the
+training path's own gather_token_logprobs; ``sampling_logprobs`` within 1e-5
+relative (+1e-6) of log(q/sum q).  Ties at top-k / top-p thresholds (bf16
+logits tie often) resolve lowest index first on both sides.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampler_oracle as so
+from rosellm_amd import roseinfer as RI
+from rosellm_amd import roserlhf as R
+
+pytestmark = pytest.mark.gpu
+
+MARGIN = 1e-5
+
+
+def _check(logits, out, *, temperature, top_k, top_p, do_sample, seed, offset, what):
+    x = logits.float().cpu().numpy()
+    want = so.sample_rows(x, temperature=temperature, top_k=top_k, top_p=top_p,
+                          do_sample=do_sample, seed=seed, offset=offset)
+    tok = out.token_ids.cpu().numpy()
+    sure = want["margin"] > MARGIN
+    diff = (tok != want["token"]) & sure
+    print(f"{what}: {int(sure.sum())}/{len(tok)} rows decided, {int((~sure).sum())} within "
+          f"{MARGIN} of a boundary", flush=True)
+    assert not diff.any(), (what, np.nonzero(diff)[0][:5], tok[diff][:5], want["token"][diff][:5])
+    same = tok == want["token"]
+    lp = out.logprobs.cpu().double().numpy()
+    err = np.abs(lp - want["logp"])[same]
+    assert (err <= 1e-5 * np.abs(want["logp"][same]) + 1e-6).all(), (what, err.max())
+    lq = out.sampling_logprobs.cpu().double().numpy()
+    errq = np.abs(lq - want["logq"])[same]
+    assert (errq <= 1e-5 * np.abs(want["logq"][same]) + 1e-6).all(), (what, errq.max())
+    return tok
+
+
+CONFIGS = [
+    dict(temperature=1.0, top_k=0, top_p=1.0),     # the reference's defaults
+    dict(temperature=0.7, top_k=50, top_p=1.0),
+    dict(temperature=1.0, top_k=0, top_p=0.9),
+    dict(temperature=1.2, top_k=200, top_p=0.8),
+    dict(temperature=1.0, top_k=0, top_p=1e-6),    # first token only (+ floor mass)
+]
+
+
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 151936), (torch.float32, 50257),
+                                     (torch.float16, 32000)])
+@pytest.mark.parametrize("cfg", CONFIGS, ids=lambda c: f"T{c['temperature']}-k{c['top_k']}-p{c['top_p']}")
+def test_sampler_matches_oracle(device, dtype, V, cfg):
+    print(f"[sampler] dtype={dtype} V={V} cfg={cfg}", flush=True)
+    g = torch.Generator().manual_seed(21)
+    B = 48
+    x = torch.randn(B, V, generator=g) * 3.0
+    hot = torch.randint(0, V, (B,), generator=g)
+    x[torch.arange(0, B, 5), hot[::5]] += 15.0  # dominant rows, as config 2
+    x = x.to(dtype)
+    xd = x.to(device)
+    out = RI.sample_next_token_batch(xd, do_sample=True, seed=1234, offset=3, **cfg)
+    assert out.token_ids.dtype == torch.int64 and out.logprobs.dtype == torch.float32
+    tok = _check(x, out, do_sample=True, seed=1234, offset=3, what=f"{dtype} V={V}", **cfg)
+    if cfg["temperature"] == 1.0:
+        # the trainer's own recomputation of the same token's log-prob
+        lp = R.gather_token_logprobs(xd, out.token_ids).cpu().double()
+        got = out.logprobs.cpu().double()
+        assert torch.allclose(got, lp, rtol=1e-6, atol=1e-6), (got - lp).abs().max()
+    assert (tok >= 0).all() and (tok < V).all()
+
+
+def test_sampler_ties_at_thresholds(device):
+    """bf16 logits on a coarse grid: the top-k and top-p thresholds cut
+    through groups of equal logits; eight offsets per row."""
+
+    g = torch.Generator().manual_seed(22)
+    B, V = 32, 4096
+    x = (torch.round(torch.randn(B, V, generator=g) * 2.0) / 2.0).to(torch.bfloat16)
+    xd = x.to(device)
+    for cfg in (dict(temperature=1.0, top_k=37, top_p=1.0),
+                dict(temperature=1.0, top_k=0, top_p=0.3),
+                dict(temperature=0.9, top_k=300, top_p=0.6)):
+        for off in range(8):
+            out = RI.sample_next_token_batch(xd, do_sample=True, seed=77, offset=off, **cfg)
+            _check(x, out, do_sample=True, seed=77, offset=off, what=f"ties {cfg} off={off}", **cfg)
+
+
+def test_greedy_and_temperature_zero(device):
+    g = torch.Generator().manual_seed(23)
+    x = (torch.randn(16, 151936, generator=g) * 3.0).to(torch.bfloat16)
+    x[3, 10] = x[3].max()  # a tie at the maximum: lowest index wins
+    xd = x.to(device)
+    for kw in (dict(do_sample=False, temperature=1.0), dict(do_sample=True, temperature=0.0)):
+        out = RI.sample_next_token_batch(xd, top_k=5, top_p=0.5, **kw)
+        assert torch.equal(out.token_ids.cpu(), torch.argmax(x.float(), dim=-1))
+        assert (out.sampling_logprobs == 0).all()
+        lp = R.gather_token_logprobs(xd, out.token_ids).cpu()
+        assert torch.allclose(out.logprobs.cpu(), lp, rtol=1e-6, atol=1e-6)
+    assert RI.sample_next_token(xd[:1], 1.0, 0, 1.0, False) == int(torch.argmax(x[0].float()))
+
+
+def test_draws_follow_the_distribution(device):
+    """8192 draws from one row (rows of a stride-0 view take distinct counters)."""
+
+    V, B = 64, 8192
+    g = torch.Generator().manual_seed(24)
+    row = torch.randn(V, generator=g) * 1.5
+    xd = row.to(device)[None].expand(B, V)
+    out = RI.sample_next_token_batch(xd, 1.0, 0, 0.95, True, seed=5)
+    q, _ = so.sampling_distribution(row.double().numpy(), 1.0, 0, 0.95)
+    counts = np.bincount(out.token_ids.cpu().numpy(), minlength=V)
+    expect = q / q.sum() * B
+    big = expect > 5
+    chi2 = float((((counts[big] - expect[big]) ** 2) / expect[big]).sum())
+    dof = int(big.sum()) - 1
+    assert chi2 < dof + 6 * np.sqrt(2 * dof), (chi2, dof)
+    assert counts[~big].sum() <= max(10, 5 * expect[~big].sum())
+
+
+def test_bad_rows_and_shapes(device):
+    x = torch.randn(4, 100, device=device)
+    x[2, 7] = float("nan")
+    with pytest.raises(RuntimeError, match="inf"):
+        RI.sample_next_token_batch(x, 1.0, 0, 1.0, True, seed=1)
+    x[2, 7] = float("inf")
+    with pytest.raises(RuntimeError, match="inf"):
+        RI.sample_next_token_batch(x, 1.0, 0, 1.0, True, seed=1)
+    with pytest.raises(ValueError, match="2D"):
+        RI.sample_next_token_batch(x[0], 1.0, 0, 1.0, True)
+    empty = RI.sample_next_token_batch(torch.randn(0, 100, device=device), 1.0, 0, 1.0, True)
+    assert empty.token_ids.numel() == 0

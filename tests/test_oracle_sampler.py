@@ -1,0 +1,122 @@
+"""The sampling oracle (roseinfer/engine.py:1103-1171) pinned on the CPU.
+
+* Philox4x32-10 against the known-answer vectors published with the Random123
+  library (the generator the kernel draws its uniforms from), for the oracle
+  and for the library's own host copy of the generator;
+* the sampling distribution against a direct restatement of the reference's
+  torch op chain (topk / softmax / cumsum / masked_fill / clamp_min) in
+  float64 on tie-free logits;
+* the inverse-CDF draw against the distribution by a chi-square test, and the
+  uniforms by their first two moments and a Kolmogorov-Smirnov bound.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampler_oracle as so
+
+KAT = [
+    ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF,) * 4, (0xFFFFFFFF, 0xFFFFFFFF), (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+]
+
+
+@pytest.mark.parametrize("ctr,key,want", KAT)
+def test_philox_known_answers(ctr, key, want):
+    assert so.philox4x32_10(ctr, key) == want
+
+
+@pytest.mark.parametrize("ctr,key,want", KAT)
+def test_library_philox_known_answers(ctr, key, want):
+    from rosellm_amd import _native as nat
+
+    lib = nat.load()
+    c = (ctypes.c_uint32 * 4)(*ctr)
+    k = (ctypes.c_uint32 * 2)(*key)
+    lib.rrl_philox4x32_10(c, k)
+    assert tuple(c) == want
+
+
+def _reference_chain(x: torch.Tensor, T: float, top_k: int, top_p: float) -> torch.Tensor:
+    """engine.py:1141-1171's PyTorch path, restated on float64: the unnormalised
+    probabilities torch.multinomial receives, scattered back to vocabulary ids."""
+
+    V = x.numel()
+    scaled = (x / T)[None]
+    q = torch.zeros(V, dtype=torch.float64)
+    if top_p <= 0.0 or top_p >= 1.0:
+        if top_k <= 0 or top_k >= V:
+            return torch.softmax(scaled, dim=-1).clamp_min(1e-9)[0]
+        vals, idx = torch.topk(scaled, min(top_k, V), dim=-1)
+        q[idx[0]] = torch.softmax(vals, dim=-1).clamp_min(1e-9)[0]
+        return q
+    k = V if top_k <= 0 else min(top_k, V)
+    sorted_logits, sorted_idx = torch.topk(scaled, k, dim=-1)
+    probs = torch.softmax(sorted_logits, dim=-1)
+    cum = torch.cumsum(probs, dim=-1)
+    mask = cum > float(top_p)
+    mask[..., 0] = False
+    probs = probs.masked_fill(mask, 0.0).clamp_min(1e-9)
+    q[sorted_idx[0]] = probs[0]
+    return q
+
+
+CASES = [(1.0, 0, 1.0), (0.7, 50, 1.0), (1.3, 0, 0.9), (1.0, 20, 0.5), (1.0, 0, 0.05),
+         (2.0, 4000, 0.95), (0.5, 1, 1.0), (1.0, 5000, 1.0)]
+
+
+@pytest.mark.parametrize("T,top_k,top_p", CASES)
+def test_distribution_matches_reference_chain(T, top_k, top_p):
+    g = torch.Generator().manual_seed(17)
+    for _ in range(3):
+        x = torch.randn(5000, generator=g, dtype=torch.float64) * 2.5
+        want = _reference_chain(x, T, top_k, top_p)
+        got, cand = so.sampling_distribution(x.numpy(), T, top_k, top_p)
+        np.testing.assert_allclose(got, want.numpy(), rtol=1e-12, atol=1e-20)
+        assert cand.sum() == (top_k if 0 < top_k < 5000 else 5000)
+
+
+def test_inverse_cdf_draws_follow_the_distribution():
+    V, B = 24, 40000
+    x = np.random.default_rng(3).normal(size=V) * 1.5
+    q, _ = so.sampling_distribution(x, 1.0, 0, 1.0)
+    rows = np.broadcast_to(x, (B, V))
+    out = so.sample_rows(rows, temperature=1.0, top_k=0, top_p=1.0, do_sample=True,
+                         seed=99, offset=5)
+    counts = np.bincount(out["token"], minlength=V)
+    expect = q / q.sum() * B
+    chi2 = float((((counts - expect) ** 2) / expect).sum())
+    # chi-square with 23 degrees of freedom: P(chi2 > 60) ~ 3e-5
+    assert chi2 < 60.0, chi2
+    np.testing.assert_allclose(out["logq"], np.log(q[out["token"]] / q.sum()), rtol=1e-12)
+
+
+def test_uniforms():
+    u = np.array([so.row_uniform(1234, 7, r) for r in range(50000)])
+    assert abs(u.mean() - 0.5) < 0.005 and abs(u.var() - 1 / 12) < 0.002
+    ks = np.max(np.abs(np.sort(u) - (np.arange(u.size) + 0.5) / u.size))
+    assert ks < 1.63 / math.sqrt(u.size)  # 1% critical value
+    # different offsets / seeds give different streams
+    assert so.row_uniform(1234, 8, 0) != so.row_uniform(1234, 7, 0)
+    assert so.row_uniform(1235, 7, 0) != so.row_uniform(1234, 7, 0)
+
+
+def test_greedy_and_first_token_rules():
+    x = np.array([[0.5, 2.0, 2.0, -1.0]])
+    out = so.sample_rows(x, temperature=0.0, top_k=0, top_p=1.0, do_sample=True, seed=1, offset=0)
+    assert out["token"][0] == 1 and out["logq"][0] == 0.0
+    # top_p below the largest probability keeps only the first token (plus
+    # the 1e-9 floor on the others)
+    q, _ = so.sampling_distribution(np.array([3.0, 0.0, -1.0]), 1.0, 0, 1e-6)
+    assert q[1] == q[2] == 1e-9 and q[0] > 0.9
+    # top-k ties: lowest index first
+    _, cand = so.sampling_distribution(np.array([1.0, 5.0, 1.0, 1.0, 0.0]), 1.0, 3, 1.0)
+    assert cand.tolist() == [True, True, True, False, False]
