@@ -23,6 +23,11 @@ d hidden and d weight, through ``fused_linear_policy_loss`` (``--path
 composed``: F.linear, gather_token_logprobs, clipped_policy_loss, autograd);
 its roofline is MFMA-bound (3 x 2*N*H*V flops per step).
 
+``--config sample`` is the rollout side: one decode step of 256 rows x
+151936 bf16 logits -> next token + behaviour log-probs
+(``rosellm_amd.roseinfer.sample_next_token_batch``, roseinfer/engine.py:
+1103-1171 defaults T = 1, top_k = 0, top_p = 1; a top-k/top-p variant beside it).
+
 ``--config sft`` is the supervised next-token cross-entropy of the model
 forwards (rosetrainer/model.py:643-649) on config 2's logits, labels = the
 sampled tokens: ``rosellm_amd.rosetrainer.causal_lm_loss`` (the same
@@ -94,7 +99,7 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=2)
-    p.add_argument("--config", choices=sorted(CONFIGS), default="c2")
+    p.add_argument("--config", choices=sorted(CONFIGS) + ["sample"], default="c2")
     p.add_argument("--path", choices=["fused", "composed"], default="fused")
     p.add_argument("--objective", choices=["gspo", "gspo_token"], default=None,
                    help="config c3 only: GSPO (default) or GSPO-token")
@@ -409,6 +414,92 @@ def traffic_from_profiles(kernel_key, workload_key):
         return None
 
 
+SAMPLE_ROWS = 256
+SAMPLE_VARIANTS = {"default": dict(temperature=1.0, top_k=0, top_p=1.0),
+                   "topk50_topp0.9_T0.7": dict(temperature=0.7, top_k=50, top_p=0.9)}
+
+
+def bench_sample(args):
+    """Rollout sampling: tokens/s of sample_next_token_batch over 256 rows of
+    151936 bf16 logits (config 2's distribution), one call per step."""
+
+    import numpy as np
+    import torch
+
+    from oracle import sampler_oracle as so
+    from rosellm_amd import _native as nat
+    from rosellm_amd.roseinfer import sample_next_token_batch
+
+    device = torch.device("cuda", 0)
+    B, V = SAMPLE_ROWS, 151936
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    x = torch.randn(B, V, dtype=torch.bfloat16, device=device, generator=g).mul_(3.0)
+    hot = torch.randint(0, V, (B,), device=device, generator=g)
+    rows = torch.arange(0, B, 20, device=device)
+    x[rows, hot[rows]] = (x[rows, hot[rows]].float() + 15.0).to(torch.bfloat16)
+    results = {}
+    for name, kw in SAMPLE_VARIANTS.items():
+        for i in range(args.warmup):
+            sample_next_token_batch(x, do_sample=True, seed=args.seed, offset=i, **kw)
+        torch.cuda.synchronize()
+        timed = nat.time_calls("rrl_sample_logprobs")
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            out = sample_next_token_batch(x, do_sample=True, seed=args.seed, offset=100 + i, **kw)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        nat.time_calls()
+        kms = [s.elapsed_time(e) for s, e in timed["rrl_sample_logprobs"]]
+        results[name] = dict(ms=el * 1e3 / args.steps, kernel_ms=sum(kms) / len(kms),
+                             tokens=out.token_ids)
+        log(f"[bench] sample {name}: {el * 1e3 / args.steps:.4f} ms/step, kernel "
+            f"{results[name]['kernel_ms']:.4f} ms")
+    head = results["default"]
+    alg = B * (V * 2 + 8 + 4 + 4)  # one read of the logits; token + two log-probs out
+    achieved = alg / (head["kernel_ms"] * 1e-3) / 1e9
+    cpu = None
+    if not args.skip_cpu:
+        n = 16
+        xc = x[:n].float().cpu().numpy()
+        times = []
+        for i in range(args.cpu_runs + 1):
+            t0 = time.perf_counter()
+            so.sample_rows(xc, temperature=1.0, top_k=0, top_p=1.0, do_sample=True,
+                           seed=args.seed, offset=0)
+            if i:
+                times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        cpu = {"value": round(n / med, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"first {n} of {B} rows, oracle inverse-CDF sampler in float64 NumPy "
+                         f"(one thread), median of {args.cpu_runs} runs after 1 warm-up"}
+    result = {
+        "metric": "tokens/sec sampled with behaviour log-probs @151936 vocab (rollout side)",
+        "value": round(B / (head["ms"] * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (config 2's logits distribution, generated on the GPU)",
+        "config": {"workload": "Rollout sampling: 256 rows x V=151936 bf16 -> token + behaviour "
+                               "log-probs (roseinfer/engine.py:1103-1171 defaults)",
+                   "rows": B, "vocab": V, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": "rrl_sample_logprobs",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel_ms": round(head["kernel_ms"], 4), "alg_bytes_per_launch": alg},
+        "cpu_baseline": cpu,
+        "variants": {k: {"ms_per_step": round(v["ms"], 4), "kernel_ms": round(v["kernel_ms"], 4),
+                         "value": round(B / (v["ms"] * 1e-3), 1)}
+                     for k, v in results.items() if k != "default"},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -416,6 +507,9 @@ def main():
               "shards by whole GRPO groups with one scalar all-reduce (see DESIGN.md), which "
               "is not run here.", file=sys.stderr)
         sys.exit(2)
+    if args.config == "sample":
+        bench_sample(args)
+        return
 
     import torch
 

@@ -137,11 +137,51 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Butterfly steps inside a row of 16 lanes: DPP quad_perm [1,0,3,2] and
+// [2,3,0,1] exchange with lanes i^1 and i^2; once quads agree, the half-row
+// and row mirrors pair each half with the other (i^4, i^8 for a reduction).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+__device__ __forceinline__ float lane_read(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Wave64 max / sum, the same value in every lane: DPP within rows of 16,
+// then the four row results through readlane (scalar operands).
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)), fmaxf(lane_read(v, 32), lane_read(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f<kDppXor1>(v);
+  v += dpp_f<kDppXor2>(v);
+  v += dpp_f<kDppHalfMirror>(v);
+  v += dpp_f<kDppMirror>(v);
+  return (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
+}
+
+// s * exp(m - M) for the combine: exact s when m == M (also for M = -inf or
+// +inf, where m - M is NaN), 0 for m = -inf below a finite M.
+__device__ __forceinline__ float rescale(float s, float m, float M) {
+  return m == M ? s : s * exp2_hw((m - M) * kLog2e);
+}
+
 template <class Tag, int SL>
 __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t nvec) {
-  __shared__ float sh_m[RNT / 64];
-  __shared__ float sh_s[RNT / 64];
-  __shared__ float sh_xt;
+  // Double-buffered by combine parity: a wave can run at most one combine
+  // ahead of the slowest (each combine has one barrier), so the buffer it
+  // writes is never the one another wave is still reading.
+  __shared__ float sh_m[2][RNT / 64];
+  __shared__ float sh_s[2][RNT / 64];
+  __shared__ float sh_xt[2];
+  int buf = 0;
 
   const int tid = threadIdx.x;
   const int64_t rows = a.B * a.T;
@@ -226,7 +266,7 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
             so += (i == ti) ? 0.0f : e[i];
           }
           s8 = so;
-          sh_xt = xt;
+          sh_xt[buf] = xt;
         }
         s = __builtin_fmaf(s, exp2_hw((m - mg) * kLog2e), s8);
         m = mn;
@@ -238,26 +278,33 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
       for (int k = 0; k < SL; ++k) fold(k);
       // No valid target: xt = -inf keeps the row's log-sum-exp finite (the
       // log-prob is set to NaN below).
-      if (!tgt_ok && tid == 0) sh_xt = -__builtin_huge_valf();
-      // Workgroup combine.  sh_xt is written before the first barrier and read
-      // before the second, so the next row's write cannot overtake a read.
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const float m2 = __shfl_xor(m, off, 64);
-        const float s2 = __shfl_xor(s, off, 64);
-        online_merge(m, s, m2, s2);
-      }
+      if (!tgt_ok && tid == 0) sh_xt[buf] = -__builtin_huge_valf();
+      // Workgroup combine, kept short: the next row's loads are not issued
+      // until it ends.  Wave max, then the rescaled sum (one exponential per
+      // lane), then the 16 wave pairs through LDS with one barrier.
+      const float Mw = wave_max_dpp(m);
+      const float Sw = wave_sum_dpp(rescale(s, m, Mw));
       if ((tid & 63) == 0) {
-        sh_m[tid >> 6] = m;
-        sh_s[tid >> 6] = s;
+        sh_m[buf][tid >> 6] = Mw;
+        sh_s[buf][tid >> 6] = Sw;
       }
       lds_barrier();
-      m = sh_m[0];
-      s = sh_s[0];
+      float mw[RNT / 64];
 #pragma unroll
-      for (int i = 1; i < RNT / 64; ++i) online_merge(m, s, sh_m[i], sh_s[i]);
-      xt = sh_xt;
-      lds_barrier();
+      for (int i = 0; i < RNT / 64; ++i) mw[i] = sh_m[buf][i];
+      m = mw[0];
+#pragma unroll
+      for (int i = 1; i < RNT / 64; ++i) m = fmaxf(m, mw[i]);
+      float sp[RNT / 64];
+#pragma unroll
+      for (int i = 0; i < RNT / 64; ++i) sp[i] = rescale(sh_s[buf][i], mw[i], m);
+#pragma unroll
+      for (int w = RNT / 128; w > 0; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) sp[i] += sp[i + w];
+      s = sp[0];
+      xt = sh_xt[buf];
+      buf ^= 1;
     }
     // Past the last row (or for a skipped next row) the descriptor covers 0
     // bytes: the refills return zeros without touching memory.
