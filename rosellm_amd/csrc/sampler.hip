@@ -88,33 +88,61 @@ template <> struct Bits<TagF32> {
   static __device__ __forceinline__ float val(uint32_t u) { return __uint_as_float(u); }
 };
 
-// The raw bits of lane `tid`'s elements of slab k (0 past the row's end).
+// Lane `tid`'s 16 bytes of slab k as stored (zeros past the row's end); a
+// row that is not 16-byte aligned, or the row's last partial vector, is read
+// element by element.
 template <class Tag>
-__device__ __forceinline__ void load_bits(const typename Tag::S* row, int64_t V, bool al16, int k,
-                                          int tid, uint32_t (&u)[Tag::VEC]) {
+__device__ __forceinline__ uint4 load_raw(const typename Tag::S* row, int64_t V, bool al16, int k,
+                                          int tid) {
   constexpr int VEC = Tag::VEC;
   const int64_t e0 = ((int64_t)k * SNT + tid) * VEC;
-  if (al16 && e0 + VEC <= V) {
-    const uint4 w = *reinterpret_cast<const uint4*>(row + e0);
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    if (VEC == 8) {
+  if (al16 && e0 + VEC <= V) return *reinterpret_cast<const uint4*>(row + e0);
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) u[i] = (ws[i >> 1] >> (16 * (i & 1))) & 0xffffu;
-    } else {
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) u[i] = ws[i & 3];
+  for (int i = 0; i < VEC; ++i) {
+    if (e0 + i < V) {
+      if (VEC == 8)
+        w[i >> 1] |= (uint32_t)reinterpret_cast<const uint16_t*>(row)[e0 + i] << (16 * (i & 1));
+      else
+        w[i] = reinterpret_cast<const uint32_t*>(row)[e0 + i];
     }
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <class Tag>
+__device__ __forceinline__ void unpack_raw(const uint4& v, uint32_t (&u)[Tag::VEC]) {
+  const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
+  if (Tag::VEC == 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = (ws[i >> 1] >> (16 * (i & 1))) & 0xffffu;
   } else {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      uint32_t b = 0;
-      if (e0 + i < V) {
-        if (sizeof(typename Tag::S) == 2)
-          b = reinterpret_cast<const uint16_t*>(row)[e0 + i];
-        else
-          b = reinterpret_cast<const uint32_t*>(row)[e0 + i];
+    for (int i = 0; i < 4; ++i) u[i] = ws[i];
+  }
+}
+
+// f(k, e0, u) over the slabs of this lane, ten slab loads in flight at a
+// time: a pass re-reads the row from memory, and each batch costs one memory
+// latency, so a 19-slab bf16 row of 151936 entries takes two per pass.
+template <class Tag, class F>
+__device__ __forceinline__ void for_slabs(const typename Tag::S* row, int64_t V, bool al16,
+                                          int nslab, F&& f) {
+  constexpr int VEC = Tag::VEC;
+  constexpr int UNR = 10;
+  const int tid = threadIdx.x;
+  for (int k0 = 0; k0 < nslab; k0 += UNR) {
+    uint4 w[UNR];
+#pragma unroll
+    for (int j = 0; j < UNR; ++j)
+      w[j] = (k0 + j < nslab) ? load_raw<Tag>(row, V, al16, k0 + j, tid) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < UNR; ++j) {
+      if (k0 + j < nslab) {
+        uint32_t u[VEC];
+        unpack_raw<Tag>(w[j], u);
+        f(k0 + j, ((long long)(k0 + j) * SNT + tid) * VEC, u);
       }
-      u[i] = b;
     }
   }
 }
@@ -130,10 +158,14 @@ struct SearchShared {
   double wave_slab[SWAVES][MAX_SLABS];
   double slab_tot[MAX_SLABS];
   double wave_tot[SWAVES];
+  float wave_e[SWAVES][MAX_SLABS];
+  float slab_e[MAX_SLABS];
+  float wave_f[SWAVES];
   int wave_i[SWAVES];
   long long wave_l[SWAVES];
   long long sel;
-  int last_lane;
+  float other;
+  int other_ok;
 };
 
 // Lowest-index maximum over the workgroup: (value, index) pairs, NaN never wins.
@@ -144,45 +176,65 @@ __device__ __forceinline__ void argmax_merge(float& bx, long long& bi, float ox,
   }
 }
 
+// A weight and, for the log-prob, the element's exp(x/T - max).
+struct WE {
+  float w, e;
+};
+
 // First element, in vocabulary order, whose inclusive prefix of the weights
-// exceeds target(total of the weights).  w(e, bits) >= 0 (float) must be a pure
-// function of its arguments (it is evaluated twice per element); the prefix
-// sums run in float64, so ~1e5 floor weights of 1e-9 next to a weight near 1
-// keep their share of the total.  When
-// rounding leaves the target at or past the last partial sum, the last
-// element with a positive weight is returned; -1 when every weight is 0.
-template <class Tag, class WFn, class TFn>
-__device__ long long vocab_search(const typename Tag::S* row, int64_t V, bool al16, int nslab,
-                                  WFn wfn, TFn tfn, SearchShared& sh) {
+// exceeds target(total of the weights).  wfn(e, bits).w >= 0 must be a pure
+// function of its arguments (it is evaluated twice per element).  Each lane
+// adds its 8 (or 4) weights in float32 and the groups in float64, so ~1e5
+// floor weights of 1e-9 next to a weight near 1 keep their share of the
+// total.  When rounding leaves the target at or past the last partial sum,
+// the last element with a positive weight is returned; -1 when every weight
+// is 0.
+//
+// OTHER: also sums wfn(...).e over every element but the one returned, into
+// sh.other (sh.other_ok = 0 on the rounding fallback): per-slab totals from
+// the first sweep plus the chosen slab re-summed without the element, so no
+// total is ever reduced by subtraction.
+template <class Tag, bool OTHER, class WFn, class TFn>
+__device__ __forceinline__ long long vocab_search(const typename Tag::S* row, int64_t V, bool al16,
+                                                  int nslab, WFn wfn, TFn tfn, SearchShared& sh) {
   constexpr int VEC = Tag::VEC;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   long long last_pos = -1;
-  for (int k = 0; k < nslab; ++k) {
-    uint32_t u[VEC];
-    load_bits<Tag>(row, V, al16, k, tid, u);
-    const long long e0 = ((long long)k * SNT + tid) * VEC;
-    double acc = 0.0;
+  for_slabs<Tag>(row, V, al16, nslab, [&](int k, long long e0, const uint32_t (&u)[VEC]) {
+    float facc = 0.0f, eacc = 0.0f;
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
-      float wi = (e0 + i < V) ? wfn(e0 + i, u[i]) : 0.0f;
-      asm volatile("" : "+v"(wi));  // the same rounding in both evaluations
-      if (wi > 0.0f) last_pos = e0 + i;
-      acc += (double)wi;
+      WE we = {0.0f, 0.0f};
+      if (e0 + i < V) we = wfn(e0 + i, u[i]);
+      asm volatile("" : "+v"(we.w));  // the same rounding in both evaluations
+      if (we.w > 0.0f) last_pos = e0 + i;
+      facc += we.w;
+      if (OTHER) eacc += we.e;
     }
-    acc = wave_sum(acc);
+    double acc = wave_sum((double)facc);
     if (lane == 0) sh.wave_slab[wave][k] = acc;
-  }
+    if (OTHER) {
+      eacc = wave_sum(eacc);
+      if (lane == 0) sh.wave_e[wave][k] = eacc;
+    }
+  });
   // last positive element over the workgroup
   for (int o = 32; o > 0; o >>= 1) {
     const long long t = __shfl_xor(last_pos, o, 64);
     last_pos = t > last_pos ? t : last_pos;
   }
   if (lane == 0) sh.wave_l[wave] = last_pos;
+  if (tid == 0) sh.other_ok = 0;
   __syncthreads();
   if (tid < nslab) {
     double s = 0.0;
-    for (int w = 0; w < SWAVES; ++w) s += sh.wave_slab[w][tid];
+    float se = 0.0f;
+    for (int w = 0; w < SWAVES; ++w) {
+      s += sh.wave_slab[w][tid];
+      if (OTHER) se += sh.wave_e[w][tid];
+    }
     sh.slab_tot[tid] = s;
+    if (OTHER) sh.slab_e[tid] = se;
   }
   last_pos = sh.wave_l[0];
   for (int w = 1; w < SWAVES; ++w) last_pos = sh.wave_l[w] > last_pos ? sh.wave_l[w] : last_pos;
@@ -200,21 +252,24 @@ __device__ long long vocab_search(const typename Tag::S* row, int64_t V, bool al
     }
     run += t;
   }
-  if (ks < 0) return last_pos;  // uniform over the workgroup
+  if (ks < 0) return last_pos;  // uniform over the workgroup; sh.other_ok stays 0
 
   // Lane scan inside slab ks.
   uint32_t u[VEC];
-  load_bits<Tag>(row, V, al16, ks, tid, u);
+  unpack_raw<Tag>(load_raw<Tag>(row, V, al16, ks, tid), u);
   const long long e0 = ((long long)ks * SNT + tid) * VEC;
-  float w8[VEC];
-  double lw = 0.0;
+  float w8[VEC], e8[VEC];
+  float flw = 0.0f;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) {
-    float wi = (e0 + i < V) ? wfn(e0 + i, u[i]) : 0.0f;
-    asm volatile("" : "+v"(wi));
-    w8[i] = wi;
-    lw += (double)wi;
+    WE we = {0.0f, 0.0f};
+    if (e0 + i < V) we = wfn(e0 + i, u[i]);
+    asm volatile("" : "+v"(we.w));
+    w8[i] = we.w;
+    e8[i] = we.e;
+    flw += we.w;
   }
+  const double lw = (double)flw;
   double incl = lw;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -259,6 +314,25 @@ __device__ long long vocab_search(const typename Tag::S* row, int64_t V, bool al
   }
   __syncthreads();
   const long long sel = sh.sel;
+  if (OTHER) {
+    // slab ks without the chosen element, plus every other slab's total
+    float es = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i)
+      if (e0 + i != sel) es += e8[i];
+    es = wave_sum(es);
+    if (lane == 0) sh.wave_f[wave] = es;
+    __syncthreads();
+    if (tid == 0) {
+      float o = 0.0f;
+      for (int w = 0; w < SWAVES; ++w) o += sh.wave_f[w];
+      for (int k = 0; k < nslab; ++k)
+        if (k != ks) o += sh.slab_e[k];
+      sh.other = o;
+      sh.other_ok = (sel >= e0 - (long long)tid * VEC &&
+                     sel < e0 - (long long)tid * VEC + (long long)SNT * VEC) ? 1 : 0;
+    }
+  }
   __syncthreads();
   return sel;
 }
@@ -274,7 +348,6 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   __shared__ float sh_m[SWAVES], sh_s[SWAVES];
   __shared__ float sh_x[SWAVES];
   __shared__ long long sh_e[SWAVES];
-  __shared__ int sh_bad;
   __shared__ uint32_t sh_digit;
   __shared__ int sh_found;
   __shared__ unsigned long long sh_above;
@@ -286,33 +359,36 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   const bool al16 = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
   const int nslab = (int)((V + (int64_t)SNT * VEC - 1) / ((int64_t)SNT * VEC));
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const float T = a.temp;
+  // x / T as x * (1/T): within an ulp of the division, and one multiply in
+  // the per-element work (the sampler is bound by its VALU issue rate).
+  const float iT = 1.0f / a.temp;
 
-  // 1. row max with its lowest index; NaN / +inf check.
+  // 1. row max with its lowest index and the online (max, sum exp) of x / T
+  // over the whole row.  A lane walks its elements in increasing index
+  // order, so a strict > keeps the first of equal maxima.  NaN and +inf
+  // reach the online sum (exp(NaN), exp(inf - inf)) and are caught there.
   float bx = -__builtin_huge_valf();
-  long long bi = 0x7fffffffffffffffLL;
-  bool bad = false;
-  for (int k = 0; k < nslab; ++k) {
-    uint32_t u[VEC];
-    load_bits<Tag>(row, V, al16, k, tid, u);
-    const long long e0 = ((long long)k * SNT + tid) * VEC;
+  int bi32 = 0x7fffffff;
+  float om = -__builtin_huge_valf(), os = 0.0f;
+  for_slabs<Tag>(row, V, al16, nslab, [&](int, long long e0, const uint32_t (&u)[VEC]) {
+    float v[VEC];
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
-      if (e0 + i < V) {
-        const float x = Bits<Tag>::val(u[i]);
-        bad |= (x != x) || (x == __builtin_huge_valf());
-        argmax_merge(bx, bi, x, e0 + i);
-      }
+      const bool ok = e0 + i < V;
+      const float x = ok ? Bits<Tag>::val(u[i]) : -__builtin_huge_valf();
+      const bool up = x > bx;
+      bx = up ? x : bx;
+      bi32 = up ? (int)(e0 + i) : bi32;
+      v[i] = x * iT;
     }
-  }
+    online_update<float, VEC>(om, os, v, -1);
+  });
+  long long bi = bi32;
   for (int o = 32; o > 0; o >>= 1) {
     const float ox = __shfl_xor(bx, o, 64);
     const long long oi = __shfl_xor(bi, o, 64);
     argmax_merge(bx, bi, ox, oi);
   }
-  if (tid == 0) sh_bad = 0;
-  __syncthreads();
-  if (bad) sh_bad = 1;
   if (lane == 0) {
     sh_x[wave] = bx;
     sh_e[wave] = bi;
@@ -321,8 +397,10 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   bx = sh_x[0];
   bi = sh_e[0];
   for (int w = 1; w < SWAVES; ++w) argmax_merge(bx, bi, sh_x[w], sh_e[w]);
-  const bool row_bad = sh_bad != 0 || bx == -__builtin_huge_valf();
   __syncthreads();
+  block_online_combine<SNT, float>(om, os, sh_m, sh_s);
+  const bool row_bad = bx == -__builtin_huge_valf() || bi >= V || os != os ||
+                       om == __builtin_huge_valf();
   if (row_bad) {
     if (tid == 0) {
       raise_flag(a.status, RRL_FLAG_BAD_PROBS);
@@ -332,10 +410,12 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
     }
     return;
   }
-  const float m = bx / T;  // max of x / T (division by T > 0 is monotone)
+  const float m = bx * iT;  // max of x / T (scaling by 1/T > 0 is monotone)
 
   long long tok = bi;
   float logq = 0.0f;
+  bool have_other = false;
+  float s_other = 0.0f;
   if (!a.greedy) {
     // 2. top-k candidates: the k-th largest key by an MSB-first radix select.
     const bool use_k = a.top_k > 0 && a.top_k < V;
@@ -348,16 +428,13 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
       for (int shift = KB - 8; shift >= 0; shift -= 8) {
         for (int i = tid; i < 256; i += SNT) hist[i] = 0;
         __syncthreads();
-        for (int k = 0; k < nslab; ++k) {
-          uint32_t u[VEC];
-          load_bits<Tag>(row, V, al16, k, tid, u);
-          const long long e0 = ((long long)k * SNT + tid) * VEC;
+        for_slabs<Tag>(row, V, al16, nslab, [&](int, long long e0, const uint32_t (&u)[VEC]) {
 #pragma unroll
           for (int i = 0; i < VEC; ++i) {
             const uint32_t key = float_key<KB>(u[i]);
             if (e0 + i < V && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
           }
-        }
+        });
         __syncthreads();
         if (wave == 0) {
           // lane l owns bins 4l..4l+3; counts above a bin = suffix sums.
@@ -390,9 +467,9 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
       need_k = kk;  // 1 <= need_k <= cnt_k tokens at the threshold are kept
       if (need_k < cnt_k) {
         const double nth = (double)(need_k - 1);
-        cut_k = vocab_search<Tag>(
+        cut_k = vocab_search<Tag, false>(
             row, V, al16, nslab,
-            [&](long long, uint32_t b) { return float_key<KB>(b) == kth ? 1.0f : 0.0f; },
+            [&](long long, uint32_t b) { return WE{float_key<KB>(b) == kth ? 1.0f : 0.0f, 0.0f}; },
             [&](double) { return nth; }, sh);
       }
     }
@@ -400,29 +477,28 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
       return !use_k || key > kth || (key == kth && (need_k >= cnt_k || e <= cut_k));
     };
 
-    // 3. Z over the candidates.
-    float zs = 0.0f;
-    for (int k = 0; k < nslab; ++k) {
-      uint32_t u[VEC];
-      load_bits<Tag>(row, V, al16, k, tid, u);
-      const long long e0 = ((long long)k * SNT + tid) * VEC;
+    // 3. Z over the candidates (the whole row's online sum without top-k).
+    float zs = os * expf(om - m);  // om == m: the same maximum
+    if (use_k) {
+      zs = 0.0f;
+      for_slabs<Tag>(row, V, al16, nslab, [&](int, long long e0, const uint32_t (&u)[VEC]) {
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        if (e0 + i < V && cand(e0 + i, float_key<KB>(u[i])))
-          zs += expf(Bits<Tag>::val(u[i]) / T - m);
-      }
-    }
-    {
+        for (int i = 0; i < VEC; ++i) {
+          if (e0 + i < V && cand(e0 + i, float_key<KB>(u[i])))
+            zs += expf(Bits<Tag>::val(u[i]) * iT - m);
+        }
+      });
       float v1[1] = {zs};
       block_sum<SNT, 1, float>(v1, sh_s);
       zs = v1[0];
     }
     const float inv_z = 1.0f / zs;
-    auto prob = [&](uint32_t b) {
-      float e = expf(Bits<Tag>::val(b) / T - m);
+    auto ex = [&](uint32_t b) {
+      float e = expf(Bits<Tag>::val(b) * iT - m);
       asm volatile("" : "+v"(e));
-      return e * inv_z;
+      return e;
     };
+    auto prob = [&](uint32_t b) { return ex(b) * inv_z; };
 
     // 4. top-p: radix select over fixed-point mass in descending key order.
     const bool use_p = a.top_p > 0.0 && a.top_p < 1.0;
@@ -442,10 +518,7 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
         }
         if (tid == 0) sh_found = 0;
         __syncthreads();
-        for (int k = 0; k < nslab; ++k) {
-          uint32_t u[VEC];
-          load_bits<Tag>(row, V, al16, k, tid, u);
-          const long long e0 = ((long long)k * SNT + tid) * VEC;
+        for_slabs<Tag>(row, V, al16, nslab, [&](int, long long e0, const uint32_t (&u)[VEC]) {
 #pragma unroll
           for (int i = 0; i < VEC; ++i) {
             const uint32_t key = float_key<KB>(u[i]);
@@ -456,7 +529,7 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
               atomicAdd(&histm[(key >> shift) & 255u], fx);
             }
           }
-        }
+        });
         __syncthreads();
         if (wave == 0) {
           unsigned long long c[4];
@@ -492,7 +565,7 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
         prefix |= d << shift;
         pmask |= 255u << shift;
         cnt_p = binc;
-        if (shift == 0 || KB == 8) {
+        if (shift == 0) {
           const unsigned long long each = binm / binc;  // equal keys, equal mass
           n_keep = each > 0 ? (P - A) / each : binc;
         }
@@ -503,11 +576,11 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
         if (pth == float_key<KB>(load_one<Tag>(row, bi)) && n_keep == 0) n_keep = 1;
         if (n_keep > 0 && n_keep < cnt_p) {
           const double nth = (double)(n_keep - 1);
-          cut_p = vocab_search<Tag>(
+          cut_p = vocab_search<Tag, false>(
               row, V, al16, nslab,
               [&](long long e, uint32_t b) {
                 const uint32_t key = float_key<KB>(b);
-                return (key == pth && cand(e, key)) ? 1.0f : 0.0f;
+                return WE{(key == pth && cand(e, key)) ? 1.0f : 0.0f, 0.0f};
               },
               [&](double) { return nth; }, sh);
         }
@@ -517,47 +590,59 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
       return !p_found || key > pth ||
              (key == pth && (n_keep >= cnt_p || (n_keep > 0 && e <= cut_p)));
     };
-    auto qw = [&](long long e, uint32_t b) {
+    // q weight with the element's exp(x/T - m) for the log-prob's S_other
+    auto qwe = [&](long long e, uint32_t b) {
       const uint32_t key = float_key<KB>(b);
-      if (!cand(e, key)) return 0.0f;
-      const float p = kept(e, key) ? prob(b) : 0.0f;
-      return fmaxf(p, 1e-9f);
+      const float ev = ex(b);
+      WE r;
+      r.e = ev;
+      r.w = cand(e, key) ? fmaxf(kept(e, key) ? ev * inv_z : 0.0f, 1e-9f) : 0.0f;
+      return r;
     };
 
-    // 5. inverse CDF with this row's uniform.
+    // 5. inverse CDF with this row's uniform; the same sweep sums exp(x/T - m)
+    // over every column but the token (the log-prob's S_other).
     uint32_t c[4] = {(uint32_t)r, (uint32_t)((uint64_t)r >> 32), (uint32_t)a.offset,
                      (uint32_t)(a.offset >> 32)};
     philox4x32_10(c, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
     const double u01 = (double)(c[0] >> 8) * 5.9604644775390625e-8;  // 2^-24
     __shared__ double sh_total;
-    tok = vocab_search<Tag>(
-        row, V, al16, nslab, qw,
+    tok = vocab_search<Tag, true>(
+        row, V, al16, nslab, qwe,
         [&](double total) {
           if (tid == 0) sh_total = total;
           return u01 * total;
         },
         sh);
-    __syncthreads();
     const double qtot = sh_total;
-    if (tok < 0 || tok >= V) tok = bi;  // no positive weight: cannot happen, q >= 1e-9
-    if (tid == 0) logq = (float)(log((double)qw(tok, load_one<Tag>(row, tok))) - log(qtot));
+    have_other = sh.other_ok != 0;
+    s_other = sh.other;
+    __syncthreads();
+    if (tok < 0 || tok >= V) {  // no positive weight: cannot happen, q >= 1e-9
+      tok = bi;
+      have_other = false;
+    }
+    if (tid == 0) logq = (float)(log((double)qwe(tok, load_one<Tag>(row, tok)).w) - log(qtot));
   }
 
-  // 6. log_softmax(x / T) at the token, as the training row kernels form it.
-  const float xt = Bits<Tag>::val(load_one<Tag>(row, tok)) / T;
-  float mm = -__builtin_huge_valf(), ss = 0.0f;
-  for (int k = 0; k < nslab; ++k) {
-    uint32_t u[VEC];
-    load_bits<Tag>(row, V, al16, k, tid, u);
-    const long long e0 = ((long long)k * SNT + tid) * VEC;
-    float v[VEC];
+  // 6. log_softmax(x / T) at the token, as the training row kernels form it:
+  // finish_row of the maximum, the sum over the other columns and the
+  // token's own value.
+  const float xt = Bits<Tag>::val(load_one<Tag>(row, tok)) * iT;
+  float mm = m, ss = s_other;
+  if (!have_other) {
+    mm = -__builtin_huge_valf();
+    ss = 0.0f;
+    for_slabs<Tag>(row, V, al16, nslab, [&](int, long long e0, const uint32_t (&u)[VEC]) {
+      float v[VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i)
-      v[i] = e0 + i < V ? Bits<Tag>::val(u[i]) / T : -__builtin_huge_valf();
-    const long long rel = tok - e0;
-    online_update<float, VEC>(mm, ss, v, (rel >= 0 && rel < VEC) ? (int)rel : -1);
+      for (int i = 0; i < VEC; ++i)
+        v[i] = e0 + i < V ? Bits<Tag>::val(u[i]) * iT : -__builtin_huge_valf();
+      const long long rel = tok - e0;
+      online_update<float, VEC>(mm, ss, v, (rel >= 0 && rel < VEC) ? (int)rel : -1);
+    });
+    block_online_combine<SNT, float>(mm, ss, sh_m, sh_s);
   }
-  block_online_combine<SNT, float>(mm, ss, sh_m, sh_s);
   if (tid == 0) {
     const RowLogprob<float> fr = finish_row<float>(mm, ss, xt);
     a.token[r] = tok;
