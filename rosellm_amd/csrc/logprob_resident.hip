@@ -1,7 +1,8 @@
-// Register-resident 16-bit row kernel: the fast path of
+// Register-resident 16-bit row kernels: the fast path of
 // rrl_fused_logprob_policy (log-prob + token-local objective gradient in one
 // read of the logits, losses.py:14-38 composed with :426-486 / :127-203 /
-// :355-423).
+// :355-423), and of rrl_logprob_bwd (resident_bwd_kernel, the backward of
+// losses.py:34-38 given the forward's lse and log-probs).
 //
 // Layout and schedule (gfx950, wave64):
 //   * A persistent grid of one 1024-lane workgroup per CU walks rows
@@ -378,10 +379,143 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
   }
 }
 
-// Variants by slab count; a row needs ceil(nvec / 1024) slabs.
-template <class Tag>
-int launch_resident(const RowArgs& a, int32_t nvec, hipStream_t stream) {
-  const int need = (nvec + RNT - 1) / RNT;
+// Per-row inputs of the backward (rrl_logprob_bwd): target id, log-sum-exp,
+// upstream gradient g = d loss / d logp and the forward's log-prob, each a
+// uniform load through the scalar data cache (read-only in this kernel).
+struct BwdRow {
+  int64_t target;
+  float lse, g, logp;
+};
+
+__device__ __forceinline__ BwdRow load_bwd_row(const RowArgs& a, uint32_t r, uint32_t T32) {
+  typedef __attribute__((address_space(4))) const float CF;
+  typedef __attribute__((address_space(4))) const int32_t CI32;
+  typedef __attribute__((address_space(4))) const int64_t CI64;
+  const uint32_t b = r / T32, t = r - b * T32;
+  const int64_t off = (int64_t)b * a.tgt.sr + (int64_t)t * a.tgt.sc;
+  const uintptr_t tp = reinterpret_cast<uintptr_t>(a.tgt.ptr);
+  BwdRow q;
+  q.target = a.tgt.dt == RRL_I32 ? (int64_t)reinterpret_cast<CI32*>(tp)[off]
+                                 : reinterpret_cast<CI64*>(tp)[off];
+  q.lse = reinterpret_cast<CF*>(reinterpret_cast<uintptr_t>(a.lse))[r];
+  q.g = reinterpret_cast<CF*>(reinterpret_cast<uintptr_t>(a.g))[r];
+  q.logp = reinterpret_cast<CF*>(reinterpret_cast<uintptr_t>(a.logp_in))[r];
+  return q;
+}
+
+// A row whose gradient is exactly zero and whose log-sum-exp is finite has
+// all-zero dlogits: its logits are never read.
+__device__ __forceinline__ bool bwd_zero_row(const BwdRow& q) {
+  return q.g == 0.0f && q.lse - q.lse == 0.0f;
+}
+
+// rrl_logprob_bwd for 16-bit rows (losses.py:34-38 backward):
+// dlogits = g * (onehot(target) - exp(x - lse)) with lse, g and log-prob given,
+// so there is no reduction and no exchange between lanes.  The schedule is the
+// fused kernel's sweep 2: the row sits in VGPRs as SL slabs of 16 bytes per
+// lane, is written back as one burst of stores and the registers are refilled
+// with the workgroup's next row as one burst of loads.  The waves never
+// synchronise.
+template <class Tag, int SL>
+__global__ __launch_bounds__(RNT) void resident_bwd_kernel(RowArgs a) {
+  const int tid = threadIdx.x;
+  const uint32_t rows32 = (uint32_t)(a.B * a.T);
+  const uint32_t T32 = (uint32_t)a.T;
+  const uint32_t row_bytes = (uint32_t)(a.V * 2);
+  const int voff = tid * 16;
+  const uint16_t* logits = static_cast<const uint16_t*>(a.logits);
+  uint16_t* dl = static_cast<uint16_t*>(a.dl);
+  uint32_t r = blockIdx.x;
+  if (r >= rows32) return;
+
+  auto row_src = [&](uint32_t rr, bool zero) {
+    const uint32_t bb = rr / T32, tt = rr - bb * T32;
+    return zero ? row_rsrc(logits, 0u)
+                : row_rsrc(logits + (int64_t)bb * a.ls_b + (int64_t)tt * a.ls_t, row_bytes);
+  };
+  BwdRow next = load_bwd_row(a, r, T32);
+  u32x4 x[SL];
+  {
+    const __amdgpu_buffer_rsrc_t src = row_src(r, bwd_zero_row(next));
+#pragma unroll
+    for (int k = 0; k < SL; ++k) {
+      x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // The zero rows' store data: a register quad of its own, opaque so that it
+  // is not rematerialised into a slab register whose load is still pending
+  // (that would make the zero stores wait on vmcnt, which on gfx9 also waits
+  // for every older store to be acknowledged).
+  u32x4 zv = {0u, 0u, 0u, 0u};
+  asm volatile("" : "+v"(zv));
+
+  for (; r < rows32; r += gridDim.x) {
+    const uint32_t b = r / T32, t = r - b * T32;
+    int lane = tid;
+    asm volatile("" : "+v"(lane));
+    const BwdRow cur = next;
+    const uint32_t rn = r + gridDim.x;
+    const bool has_next = rn < rows32;
+    if (has_next) next = load_bwd_row(a, rn, T32);
+    // A target outside [0, V) has no column: every element takes the
+    // exp(x - lse) term, as in the generic kernel.
+    const bool tgt_ok = cur.target >= 0 && cur.target < a.V;
+    const int32_t tgt = tgt_ok ? (int32_t)cur.target : 0;
+    const int rel = tgt_ok ? (tgt >> 3) - lane : -1;
+    const int ti = tgt & 7;
+    const bool zero = bwd_zero_row(cur);
+    const float g = cur.g, lse = cur.lse;
+    // -g * exp(x - lse) = -sign(g) * exp2((x - lse) * log2e + log2|g|): the
+    // difference is formed first, so no finite lse overflows.
+    const float lg = __log2f(fabsf(g));
+    const bool flip = g > 0.0f;
+    const uint32_t sgn = flip ? 0x80008000u : 0u;
+    const float tgt_d = zero ? 0.0f : target_grad<float>(g, cur.logp, true, 0.0f, lse);
+    const float tgt_pre = flip ? -tgt_d : tgt_d;  // the XOR restores tgt_d
+    const __amdgpu_buffer_rsrc_t src =
+        has_next ? row_src(rn, bwd_zero_row(next)) : row_rsrc(logits, 0u);
+    const __amdgpu_buffer_rsrc_t dst =
+        row_rsrc(dl + (int64_t)b * a.ds_b + (int64_t)t * a.ds_t, row_bytes);
+    if (zero) {  // uniform over the workgroup
+      // Stores only, with no dependence on the (never read) slabs: a run of
+      // zero rows (a clipped GSPO sequence, masked prompt tokens) streams its
+      // stores without waiting for earlier ones.  Measured on config 3 (72%
+      // zero rows): backward 16.8-18.4 ms against 18.6-20.0 ms when the zero
+      // rows went through the arithmetic below.
+#pragma unroll
+      for (int k = 0; k < SL; ++k) {
+        __builtin_amdgcn_raw_buffer_store_b128(zv, dst, voff, k * RNT * 16, kAuxStoreNT);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < SL; ++k) {
+        float d[8];
+        float v[8];
+        Pack16<Tag>::unpack(x[k], v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d[i] = exp2_hw(__builtin_fmaf(v[i] - lse, kLog2e, lg));
+        if (rel == k * RNT) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) d[i] = (i == ti) ? tgt_pre : d[i];
+        }
+        u32x4 o = Pack16<Tag>::pack(d);
+        o.x ^= sgn; o.y ^= sgn; o.z ^= sgn; o.w ^= sgn;
+        __builtin_amdgcn_raw_buffer_store_b128(o, dst, voff, k * RNT * 16, kAuxStoreNT);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < SL; ++k) {
+      x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+int cu_count_of_current_device(int* n_out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return check_launch("hipGetDevice");
   static int cu_count[64] = {0};
@@ -392,11 +526,21 @@ int launch_resident(const RowArgs& a, int32_t nvec, hipStream_t stream) {
       n = 256;
     cu_count[dev] = n;
   }
+  *n_out = cu_count[dev];
+  return RRL_OK;
+}
+
+// Variants by slab count; a row needs ceil(nvec / 1024) slabs.
+template <class Tag>
+int launch_resident(const RowArgs& a, int32_t nvec, hipStream_t stream) {
+  const int need = (nvec + RNT - 1) / RNT;
+  int cus = 0;
+  if (int rc = cu_count_of_current_device(&cus)) return rc;
   const int64_t rows = a.B * a.T;
   const unsigned pgrid = (unsigned)((rows + 255) / 256 < 65536 ? (rows + 255) / 256 : 65536);
   hipLaunchKernelGGL(pack_records_kernel, dim3(pgrid), dim3(256), 0, stream, a);
   if (int rc = check_launch("pack_records_kernel")) return rc;
-  const unsigned grid = (unsigned)(rows < cu_count[dev] ? rows : cu_count[dev]);
+  const unsigned grid = (unsigned)(rows < cus ? rows : cus);
 #define RRL_RESIDENT_CASE(SLV)                                                                \
   if (need <= SLV) {                                                                          \
     hipLaunchKernelGGL((resident_fused_kernel<Tag, SLV>), dim3(grid), dim3(RNT), 0, stream,   \
@@ -413,28 +557,61 @@ int launch_resident(const RowArgs& a, int32_t nvec, hipStream_t stream) {
   return RRL_EINVAL;
 }
 
+template <class Tag>
+int launch_resident_bwd(const RowArgs& a, int32_t nvec, hipStream_t stream) {
+  const int need = (nvec + RNT - 1) / RNT;
+  int cus = 0;
+  if (int rc = cu_count_of_current_device(&cus)) return rc;
+  const int64_t rows = a.B * a.T;
+  const unsigned grid = (unsigned)(rows < cus ? rows : cus);
+#define RRL_RESIDENT_CASE(SLV)                                                                \
+  if (need <= SLV) {                                                                          \
+    hipLaunchKernelGGL((resident_bwd_kernel<Tag, SLV>), dim3(grid), dim3(RNT), 0, stream, a); \
+    return check_launch("resident_bwd_kernel");                                               \
+  }
+  RRL_RESIDENT_CASE(4)
+  RRL_RESIDENT_CASE(8)
+  RRL_RESIDENT_CASE(12)
+  RRL_RESIDENT_CASE(16)
+  RRL_RESIDENT_CASE(20)
+#undef RRL_RESIDENT_CASE
+  set_error("resident_bwd_kernel: row too long");
+  return RRL_EINVAL;
+}
+
 constexpr int64_t kMaxResidentVec = 20 * RNT;  // SL = 20 fits 128 VGPRs without spills
 
 }  // namespace
 
-// Takes the fused single-pass call when the row fits the register budget and
-// every row of logits and dlogits is 16-byte aligned; otherwise leaves
-// *launched false so the caller runs the generic row kernel.
+// Takes the register-resident kernel (mode 2: the fused single pass; mode 1:
+// rrl_logprob_bwd with the forward's log-probs given) when the row fits the
+// register budget and every row of logits and dlogits is 16-byte aligned;
+// otherwise leaves *launched false so the caller runs the generic row kernel.
 int maybe_launch_resident(const RowArgs& a, int mode, int logits_dtype, hipStream_t stream,
                           bool* launched) {
   *launched = false;
-  if (mode != 2 || (a.pp.flags & RRL_POLICY_GENERIC)) return RRL_OK;
+  if (mode == 2 && (a.pp.flags & RRL_POLICY_GENERIC)) return RRL_OK;
+  if (mode != 1 && mode != 2) return RRL_OK;
   if (logits_dtype != RRL_BF16 && logits_dtype != RRL_F16) return RRL_OK;
   if (a.dl_dt != logits_dtype || a.accumulate) return RRL_OK;
   if (a.B * a.T == 0 || a.V % 8 != 0 || a.V / 8 > kMaxResidentVec) return RRL_OK;
   const auto al16 = [](int64_t elems) { return ((elems * 2) % 16) == 0; };
   if (((uintptr_t)a.logits % 16) || ((uintptr_t)a.dl % 16)) return RRL_OK;
   if (!al16(a.ls_b) || !al16(a.ls_t) || !al16(a.ds_b) || !al16(a.ds_t)) return RRL_OK;
+  if (a.B * a.T >= ((int64_t)1 << 31) || a.T >= ((int64_t)1 << 31)) return RRL_OK;
+  const int32_t nvec = (int32_t)(a.V / 8);
+  if (mode == 1) {
+    // Scalar loads need 4-byte aligned operands.
+    if (a.logp_in == nullptr || a.tgt.ptr == nullptr) return RRL_OK;
+    if (((uintptr_t)a.lse | (uintptr_t)a.g | (uintptr_t)a.logp_in) % 4) return RRL_OK;
+    if ((uintptr_t)a.tgt.ptr % (a.tgt.dt == RRL_I32 ? 4 : 8)) return RRL_OK;
+    *launched = true;
+    return logits_dtype == RRL_BF16 ? launch_resident_bwd<TagBF16>(a, nvec, stream)
+                                    : launch_resident_bwd<TagF16>(a, nvec, stream);
+  }
   if (a.logp_dt != RRL_F32 || a.records == nullptr) return RRL_OK;
   if ((uintptr_t)a.records % 16) return RRL_OK;
-  if (a.B * a.T >= ((int64_t)1 << 31) || a.T >= ((int64_t)1 << 31)) return RRL_OK;
   *launched = true;
-  const int32_t nvec = (int32_t)(a.V / 8);
   return logits_dtype == RRL_BF16 ? launch_resident<TagBF16>(a, nvec, stream)
                                   : launch_resident<TagF16>(a, nvec, stream);
 }
