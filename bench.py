@@ -97,7 +97,8 @@ def log(msg: str) -> None:
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--steps", type=int, default=None,
+                   help="timed steps (default 10; 200 for config c1, whose step is under 1 ms)")
     p.add_argument("--warmup", type=int, default=2)
     p.add_argument("--config", choices=sorted(CONFIGS) + ["sample"], default="c2")
     p.add_argument("--path", choices=["fused", "composed"], default="fused")
@@ -507,6 +508,8 @@ def main():
               "shards by whole GRPO groups with one scalar all-reduce (see DESIGN.md), which "
               "is not run here.", file=sys.stderr)
         sys.exit(2)
+    if args.steps is None:
+        args.steps = 200 if args.config == "c1" else 10
     if args.config == "sample":
         bench_sample(args)
         return
@@ -640,9 +643,11 @@ def main():
     # The same step with skip_masked_rows=True (zero-weight rows are never
     # read); reported beside the exact-semantics headline, not as `value`.
     variants = {}
-    if (path == "fused" and objective == "clipped" and not args.no_variants
-            and not cfg.get("lm_head")):
-        vstep = make_step(inp, cfg, path, objective, skip_masked=True)
+
+    def time_variant(vstep):
+        """Warm-up, then the timed steps of a variant: (seconds, average
+        duration of the dominant entry point in ms, last output)."""
+
         for _ in range(args.warmup):
             vstep()
         vt = nat.time_calls(kernels[0])
@@ -653,9 +658,13 @@ def main():
         torch.cuda.synchronize()
         v_el = time.perf_counter() - t0
         nat.time_calls()
-        assert vout.loss.item() == out.loss.item(), "skip_masked_rows changed the loss"
         v_ms = [s.elapsed_time(e) for s, e in vt[kernels[0]]]
-        v_k = sum(v_ms) / len(v_ms)
+        return v_el, sum(v_ms) / len(v_ms), vout
+
+    if (path == "fused" and objective == "clipped" and not args.no_variants
+            and not cfg.get("lm_head")):
+        v_el, v_k, vout = time_variant(make_step(inp, cfg, path, objective, skip_masked=True))
+        assert vout.loss.item() == out.loss.item(), "skip_masked_rows changed the loss"
         n_active = int(inp["mask"].sum().item())
         v_alg = n_active * V * in_b + N * V * in_b + N * SIDE_BYTES
         variants["skip_masked_rows"] = {
@@ -669,6 +678,24 @@ def main():
         }
         log(f"[bench] skip_masked_rows: {v_el * 1e3 / args.steps:.3f} ms/step, "
             f"{N / (v_el / args.steps) / 1e6:.3f} M tok/s, kernel {v_k:.3f} ms")
+
+    if objective == "sapo" and not args.no_variants:
+        # Config 4 is specified with tau_negative = 1.0; the reference's
+        # default (tau_positive 1.0, tau_negative 1.05) is reported beside it.
+        # Same bytes per step: the taus change only the per-token arithmetic.
+        ref_kw = dict(tau_positive=1.0, tau_negative=1.05)
+        v_el, v_k, _ = time_variant(make_step(inp, dict(cfg, kw=ref_kw), path, objective))
+        v_alg = alg[kernels[0]]
+        variants["reference_default_taus"] = {
+            "kw": ref_kw,
+            "value": round(N / (v_el / args.steps), 1),
+            "ms_per_step": round(v_el * 1e3 / args.steps, 4),
+            "kernel_ms": round(v_k, 4),
+            "achieved": round(v_alg / (v_k * 1e-3) / 1e9, 1),
+            "frac": round(v_alg / (v_k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        log(f"[bench] SAPO with the reference's default taus: {v_el * 1e3 / args.steps:.3f} "
+            f"ms/step, {N / (v_el / args.steps) / 1e6:.3f} M tok/s, kernel {v_k:.3f} ms")
 
     if args.calibrate_copy:
         # Calibration kernel of known traffic for the HBM counters: a bf16 ->

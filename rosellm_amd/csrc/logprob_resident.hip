@@ -49,8 +49,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, uin
 constexpr int kAuxLoad = 0;
 constexpr int kAuxStoreNT = 2;
 
+// Element access of one 16-byte vector per tag: EPV elements, their float
+// values, the packed form written back (round to nearest even for 16-bit),
+// the sign bit of every element of a dword, and the single-element loads and
+// non-temporal stores of a row's unaligned head and tail.
 template <class Tag> struct Pack16;
 template <> struct Pack16<TagBF16> {
+  static constexpr int EPV = 8, LOG2_EPV = 3;
+  static constexpr uint32_t SGN2 = 0x80008000u, SGN1 = 0x8000u;
   static __device__ __forceinline__ void unpack(const u32x4& u, float (&x)[8]) {
     x[0] = __uint_as_float(u.x << 16); x[1] = __uint_as_float(u.x & 0xffff0000u);
     x[2] = __uint_as_float(u.y << 16); x[3] = __uint_as_float(u.y & 0xffff0000u);
@@ -65,8 +71,18 @@ template <> struct Pack16<TagBF16> {
     o.w = f32x2_to_bf16x2_bits(d[6], d[7]);
     return o;
   }
+  static __device__ __forceinline__ float one(uint32_t b) { return __uint_as_float(b << 16); }
+  static __device__ __forceinline__ uint32_t pack_one(float d) { return f32_to_bf16_bits(d); }
+  static __device__ __forceinline__ uint32_t load_one(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  }
+  static __device__ __forceinline__ void store_one(uint32_t b, __amdgpu_buffer_rsrc_t r, int off) {
+    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)b, r, off, 0, kAuxStoreNT);
+  }
 };
 template <> struct Pack16<TagF16> {
+  static constexpr int EPV = 8, LOG2_EPV = 3;
+  static constexpr uint32_t SGN2 = 0x80008000u, SGN1 = 0x8000u;
   static __device__ __forceinline__ void unpack(const u32x4& u, float (&x)[8]) {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -84,7 +100,78 @@ template <> struct Pack16<TagF16> {
     o.x = w[0]; o.y = w[1]; o.z = w[2]; o.w = w[3];
     return o;
   }
+  static __device__ __forceinline__ float one(uint32_t b) {
+    return f16_bits_to_f32((uint16_t)(b & 0xffffu));
+  }
+  static __device__ __forceinline__ uint32_t pack_one(float d) { return f32_to_f16_bits(d); }
+  static __device__ __forceinline__ uint32_t load_one(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  }
+  static __device__ __forceinline__ void store_one(uint32_t b, __amdgpu_buffer_rsrc_t r, int off) {
+    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)b, r, off, 0, kAuxStoreNT);
+  }
 };
+template <> struct Pack16<TagF32> {
+  static constexpr int EPV = 4, LOG2_EPV = 2;
+  static constexpr uint32_t SGN2 = 0x80000000u, SGN1 = 0x80000000u;
+  static __device__ __forceinline__ void unpack(const u32x4& u, float (&x)[4]) {
+    x[0] = __uint_as_float(u.x); x[1] = __uint_as_float(u.y);
+    x[2] = __uint_as_float(u.z); x[3] = __uint_as_float(u.w);
+  }
+  static __device__ __forceinline__ u32x4 pack(const float (&d)[4]) {
+    u32x4 o;
+    o.x = __float_as_uint(d[0]); o.y = __float_as_uint(d[1]);
+    o.z = __float_as_uint(d[2]); o.w = __float_as_uint(d[3]);
+    return o;
+  }
+  static __device__ __forceinline__ float one(uint32_t b) { return __uint_as_float(b); }
+  static __device__ __forceinline__ uint32_t pack_one(float d) { return __float_as_uint(d); }
+  static __device__ __forceinline__ uint32_t load_one(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  }
+  static __device__ __forceinline__ void store_one(uint32_t b, __amdgpu_buffer_rsrc_t r, int off) {
+    __builtin_amdgcn_raw_buffer_store_b32(b, r, off, 0, kAuxStoreNT);
+  }
+};
+
+// A row as the resident kernels hold it: `head` single elements up to the
+// first 16-byte boundary, `nbody` aligned 16-byte vectors (the register
+// slabs), then `tail` single elements.  head <= EPV - 1 and tail <= EPV - 1,
+// so lanes 0-7 carry the head and lanes 8-15 the tail in one extra register.
+// Without EXTRAS every row is 16-byte aligned with V % EPV == 0: head = tail
+// = 0 and nbody is the same for every row.
+struct RowGeo {
+  uint32_t head, nbody, tail;
+};
+
+template <class Tag, bool EXTRAS>
+__device__ __forceinline__ RowGeo row_geo(const void* row, uint32_t V, int32_t nvec) {
+  constexpr uint32_t EPV = Pack16<Tag>::EPV, ESZ = 16 / EPV;
+  RowGeo g;
+  if constexpr (EXTRAS) {
+    const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(row) & 15u);
+    uint32_t h = mis ? (16u - mis) / ESZ : 0u;
+    h = h < V ? h : V;
+    const uint32_t rem = V - h;
+    g.head = h;
+    g.nbody = rem / EPV;
+    g.tail = rem - g.nbody * EPV;
+  } else {
+    g.head = 0;
+    g.nbody = (uint32_t)nvec;
+    g.tail = 0;
+  }
+  return g;
+}
+
+// Vocabulary index of the extra element lane `tid` carries, or -1.
+template <class Tag>
+__device__ __forceinline__ int32_t extra_index(const RowGeo& g, int tid) {
+  constexpr int EPV = Pack16<Tag>::EPV;
+  if (tid < 8) return tid < (int)g.head ? tid : -1;
+  if (tid < 16) return tid - 8 < (int)g.tail ? (int)(g.head + g.nbody * EPV) + tid - 8 : -1;
+  return -1;
+}
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -173,8 +260,44 @@ __device__ __forceinline__ float rescale(float s, float m, float M) {
   return m == M ? s : s * exp2_hw((m - M) * kLog2e);
 }
 
-template <class Tag, int SL>
+// Balanced max / sum of the EPV values of one vector.
+template <int N>
+__device__ __forceinline__ float vmax(const float (&v)[N]) {
+  if constexpr (N == 8)
+    return fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])),
+                 fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
+  else
+    return fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+}
+template <int N>
+__device__ __forceinline__ float vsum(const float (&e)[N]) {
+  if constexpr (N == 8)
+    return ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+  else
+    return (e[0] + e[1]) + (e[2] + e[3]);
+}
+
+// exp2 exponent of -g * exp(x - lse) without the sign: x*log2e + (log2|g| -
+// lse*log2e) for 16-bit logits (one FMA per element; |lse| > 2e38 is flagged
+// and rerun by the host), (x - lse)*log2e + log2|g| for float32 logits (a
+// subtract more, and exact for every finite lse).
+struct ExpArg {
+  float cg, lg, lse;
+};
+template <class Tag>
+__device__ __forceinline__ float exp_arg(float x, const ExpArg& q) {
+  if constexpr (Pack16<Tag>::EPV == 4)
+    return __builtin_fmaf(x - q.lse, kLog2e, q.lg);
+  else
+    return __builtin_fmaf(x, kLog2e, q.cg);
+}
+
+template <class Tag, int SL, bool EXTRAS>
 __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t nvec) {
+  using P = Pack16<Tag>;
+  using S = typename Tag::S;
+  constexpr int EPV = P::EPV;
+  constexpr int ESZ = (int)sizeof(S);
   // Double-buffered by combine parity: a wave can run at most one combine
   // ahead of the slowest (each combine has one barrier), so the buffer it
   // writes is never the one another wave is still reading.
@@ -185,10 +308,10 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
 
   const int tid = threadIdx.x;
   const int64_t rows = a.B * a.T;
-  const uint32_t row_bytes = (uint32_t)(a.V * 2);
+  const uint32_t V32 = (uint32_t)a.V;
   const int voff = tid * 16;
-  const uint16_t* logits = static_cast<const uint16_t*>(a.logits);
-  uint16_t* dl = static_cast<uint16_t*>(a.dl);
+  const S* logits = static_cast<const S*>(a.logits);
+  S* dl = static_cast<S*>(a.dl);
   const PolicyConsts<float> c = PolicyConsts<float>::make(a.pp);
   // Row indices fit in 32 bits (checked on the host); 32-bit division keeps the
   // per-row address arithmetic short.
@@ -197,9 +320,15 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
   uint32_t r = blockIdx.x;
   if (r >= rows32) return;
 
-  auto row_src = [&](uint32_t rr) {
+  auto row_ptr = [&](uint32_t rr) {
     const uint32_t bb = rr / T32, tt = rr - bb * T32;
-    return row_rsrc(logits + (int64_t)bb * a.ls_b + (int64_t)tt * a.ls_t, row_bytes);
+    return logits + (int64_t)bb * a.ls_b + (int64_t)tt * a.ls_t;
+  };
+  // The extra element of this lane (EXTRAS): its byte offset in the row, or
+  // the row's end (out of range: loads return 0, stores are dropped).
+  auto extra_off = [&](const RowGeo& g) {
+    const int32_t ei = extra_index<Tag>(g, tid);
+    return ei >= 0 ? ei * ESZ : (int)(V32 * ESZ);
   };
   // RRL_POLICY_SKIP_MASKED: rows whose weight is exactly 0 are never read
   // (their loads use a 0-byte descriptor: no memory traffic) and get zero
@@ -207,9 +336,12 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
   const bool skip_masked = (a.pp.flags & RRL_POLICY_SKIP_MASKED) != 0;
   TokenRecord rec_next = load_record(a.records, r);
   u32x4 x[SL];
+  uint32_t xe = 0;  // EXTRAS: the lane's head or tail element, as stored
   {
     const bool skip0 = skip_masked && rec_next.wcoef == 0.0f;
-    const __amdgpu_buffer_rsrc_t src = skip0 ? row_rsrc(logits, 0u) : row_src(r);
+    const S* p0 = row_ptr(r);
+    const RowGeo g0 = row_geo<Tag, EXTRAS>(p0, V32, nvec);
+    const __amdgpu_buffer_rsrc_t src = skip0 ? row_rsrc(logits, 0u) : row_rsrc(p0 + g0.head, g0.nbody * 16);
     // Issue in slab order, the order sweep 2 refills them: with one order on
     // both paths into the row loop, sweep 1 waits for slab k only (older
     // loads), not for the whole row.
@@ -217,6 +349,10 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     for (int k = 0; k < SL; ++k) {
       x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
       __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (EXTRAS) {
+      const __amdgpu_buffer_rsrc_t esrc = skip0 ? row_rsrc(logits, 0u) : row_rsrc(p0, V32 * ESZ);
+      xe = P::load_one(esrc, extra_off(g0));
     }
   }
 
@@ -227,6 +363,8 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     // loop-invariant masks.
     int lane = tid;
     asm volatile("" : "+v"(lane));
+    const RowGeo g = row_geo<Tag, EXTRAS>(row_ptr(r), V32, nvec);
+    const int32_t ei = EXTRAS ? extra_index<Tag>(g, tid) : -1;
     // Per-row scalars: one scalar-cache load, issued a row ahead.
     const TokenRecord rec = rec_next;
     const bool skip = skip_masked && rec.wcoef == 0.0f;
@@ -235,9 +373,13 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     if (has_next) rec_next = load_record(a.records, rn);
     const int32_t tgt = rec.target;
     const bool tgt_ok = tgt >= 0;
-    // Slab k of this lane holds the target iff rel == k * RNT.
-    const int rel = tgt_ok ? (tgt >> 3) - lane : -1;
-    const int ti = tgt & 7;
+    // Slab k of this lane holds the target iff rel == k * RNT; a target in
+    // the head or tail is the extra element of lane ei == tgt.
+    const int32_t bt = tgt - (int32_t)g.head;
+    const bool in_body = tgt_ok && (!EXTRAS || (bt >= 0 && bt < (int32_t)(g.nbody * EPV)));
+    const int rel = in_body ? (bt >> P::LOG2_EPV) - lane : -1;
+    const int ti = bt & (EPV - 1);
+    const bool ex_tgt = EXTRAS && tgt_ok && ei == tgt;
 
     // Sweep 1: per-lane online (max, sum exp) over the slabs.  The running max
     // starts at -inf; `mg` (the max as an exponent offset) is kept finite so
@@ -247,28 +389,26 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     // and slab that hold it.
     float m = -__builtin_huge_valf(), s = 0.0f;
     auto fold = [&](int k) {
-      if (lane < nvec - k * RNT) {
-        float v[8];
-        Pack16<Tag>::unpack(x[k], v);
-        const float mc = fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])),
-                               fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
-        const float mn = fmaxf(m, mc);
+      if (lane < (int)g.nbody - k * RNT) {
+        float v[EPV];
+        P::unpack(x[k], v);
+        const float mn = fmaxf(m, vmax(v));
         const float mg = fmaxf(mn, -__FLT_MAX__);
-        float e[8];
+        float e[EPV];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) e[i] = exp2_hw((v[i] - mg) * kLog2e);
-        float s8 = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+        for (int i = 0; i < EPV; ++i) e[i] = exp2_hw((v[i] - mg) * kLog2e);
+        float se = vsum(e);
         if (rel == k * RNT) {
-          float xt = v[0], so = 0.0f;
+          float xv = v[0], so = 0.0f;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            xt = (i == ti) ? v[i] : xt;
+          for (int i = 0; i < EPV; ++i) {
+            xv = (i == ti) ? v[i] : xv;
             so += (i == ti) ? 0.0f : e[i];
           }
-          s8 = so;
-          sh_xt[buf] = xt;
+          se = so;
+          sh_xt[buf] = xv;
         }
-        s = __builtin_fmaf(s, exp2_hw((m - mg) * kLog2e), s8);
+        s = __builtin_fmaf(s, exp2_hw((m - mg) * kLog2e), se);
         m = mn;
       }
     };
@@ -276,6 +416,19 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     if (!skip) {  // uniform over the workgroup
 #pragma unroll
       for (int k = 0; k < SL; ++k) fold(k);
+      if constexpr (EXTRAS) {
+        // As in a slab: the element joins the max, and the sum unless it is
+        // the target.
+        if (ei >= 0) {
+          const float v = P::one(xe);
+          const float mn = fmaxf(m, v);
+          const float mg = fmaxf(mn, -__FLT_MAX__);
+          const float ev = ex_tgt ? 0.0f : exp2_hw((v - mg) * kLog2e);
+          if (ex_tgt) sh_xt[buf] = v;
+          s = __builtin_fmaf(s, exp2_hw((m - mg) * kLog2e), ev);
+          m = mn;
+        }
+      }
       // No valid target: xt = -inf keeps the row's log-sum-exp finite (the
       // log-prob is set to NaN below).
       if (!tgt_ok && tid == 0) sh_xt[buf] = -__builtin_huge_valf();
@@ -309,62 +462,75 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     // Past the last row (or for a skipped next row) the descriptor covers 0
     // bytes: the refills return zeros without touching memory.
     const bool skip_next = skip_masked && rec_next.wcoef == 0.0f;
+    const bool load_next = has_next && !skip_next;
+    const S* pn = row_ptr(load_next ? rn : r);
+    const RowGeo gn = row_geo<Tag, EXTRAS>(pn, V32, nvec);
     const __amdgpu_buffer_rsrc_t src =
-        (has_next && !skip_next) ? row_src(rn) : row_rsrc(logits, 0u);
+        load_next ? row_rsrc(pn + gn.head, gn.nbody * 16) : row_rsrc(logits, 0u);
 
     // Opaque to the optimiser: sweep 2 re-expands the packed slabs instead of
     // keeping sweep 1's widened copies live (twice the registers).
 #pragma unroll
     for (int k = 0; k < SL; ++k) asm volatile("" : "+v"(x[k]));
+    if constexpr (EXTRAS) asm volatile("" : "+v"(xe));
 
     const RowLogprob<float> fr = finish_row<float>(m, s, xt);
     const float lse = skip ? 0.0f : fr.lse;
     const float logp = skip ? 0.0f : (tgt_ok ? fr.logp : __builtin_nanf(""));
-    const float g =
+    const float gr =
         skip ? 0.0f : -(rec.wcoef * token_local_grad<float>(c, logp, rec.old, rec.adv));
-    const float tgt_d = target_grad<float>(g, logp, true, xt, lse);
+    const float tgt_d = target_grad<float>(gr, logp, true, xt, lse);
     if (tid == 0) {
       store_as<float>(a.logp, a.logp_dt, r, logp);
       static_cast<float*>(a.lse_out)[r] = lse;
     }
 
     // Sweep 2: dlogits, then refill the register slabs with the next row.
-    const __amdgpu_buffer_rsrc_t dst =
-        row_rsrc(dl + (int64_t)b * a.ds_b + (int64_t)t * a.ds_t, row_bytes);
+    const S* drow = dl + (int64_t)b * a.ds_b + (int64_t)t * a.ds_t;
+    const __amdgpu_buffer_rsrc_t dst = row_rsrc(drow + g.head, g.nbody * 16);
     // lse * log2e overflows for finite |lse| > 2.3e38 (logits near the 16-bit
     // maximum): such a row is flagged and the host reruns the call on the
     // generic kernel.  Non-finite lse needs no care: NaN propagates as in
-    // log_softmax.
-    if (tid == 0 && fabsf(lse) > 2e38f && fabsf(lse) != __builtin_huge_valf())
+    // log_softmax.  Float32 logits use the x - lse form, which has no limit.
+    if (EPV == 8 && tid == 0 && fabsf(lse) > 2e38f && fabsf(lse) != __builtin_huge_valf())
       raise_flag(a.status, RRL_FLAG_FAST_RANGE);
     // -g * exp(x - lse) = -sign(g) * exp2(x*log2e + (log2|g| - lse*log2e)):
     // one FMA and one v_exp_f32 per element; the sign is applied to the packed
-    // 16-bit words with one XOR per two elements.
-    const float cg = __log2f(fabsf(g)) - lse * kLog2e;
-    const bool flip = g > 0.0f;
-    const uint32_t sgn = flip ? 0x80008000u : 0u;
+    // words with one XOR per dword.
+    ExpArg q;
+    q.lg = __log2f(fabsf(gr));
+    q.cg = q.lg - lse * kLog2e;
+    q.lse = lse;
+    const bool flip = gr > 0.0f;
+    const uint32_t sgn = flip ? P::SGN2 : 0u;
     const float tgt_pre = flip ? -tgt_d : tgt_d;  // the XOR restores tgt_d
     // Every element goes through the same arithmetic, also for a zero-weight
-    // row: there cg = -inf and exp2(-inf) = 0 for every finite or -inf logit
-    // (a +inf or NaN logit makes lse non-finite and the row NaN, as in
+    // row: there log2|g| = -inf and exp2(-inf) = 0 for every finite or -inf
+    // logit (a +inf or NaN logit makes lse non-finite and the row NaN, as in
     // log_softmax).  A uniform branch around the arithmetic with
     // zero-initialised registers was tried with the store-then-load order
     // below: on gfx950 it stored the zero initialiser instead of the computed
     // first dword of odd slabs in waves 4-15, so it is not used.
 #pragma unroll
     for (int k = 0; k < SL; ++k) {
-      float d[8];
-      float v[8];
-      Pack16<Tag>::unpack(x[k], v);
+      float d[EPV];
+      float v[EPV];
+      P::unpack(x[k], v);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) d[i] = exp2_hw(__builtin_fmaf(v[i], kLog2e, cg));
+      for (int i = 0; i < EPV; ++i) d[i] = exp2_hw(exp_arg<Tag>(v[i], q));
       if (rel == k * RNT) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) d[i] = (i == ti) ? tgt_pre : d[i];
+        for (int i = 0; i < EPV; ++i) d[i] = (i == ti) ? tgt_pre : d[i];
       }
-      u32x4 o = Pack16<Tag>::pack(d);
+      u32x4 o = P::pack(d);
       o.x ^= sgn; o.y ^= sgn; o.z ^= sgn; o.w ^= sgn;
       __builtin_amdgcn_raw_buffer_store_b128(o, dst, voff, k * RNT * 16, kAuxStoreNT);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (EXTRAS) {
+      const float dv = ex_tgt ? tgt_pre : exp2_hw(exp_arg<Tag>(P::one(xe), q));
+      P::store_one(P::pack_one(dv) ^ (flip ? P::SGN1 : 0u), row_rsrc(drow, V32 * ESZ),
+                   extra_off(g));
       __builtin_amdgcn_sched_barrier(0);
     }
     // Then the next row's loads into the same registers: each CU issues its
@@ -375,6 +541,10 @@ __global__ __launch_bounds__(RNT) void resident_fused_kernel(RowArgs a, int32_t 
     for (int k = 0; k < SL; ++k) {
       x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
       __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (EXTRAS) {
+      const __amdgpu_buffer_rsrc_t esrc = load_next ? row_rsrc(pn, V32 * ESZ) : row_rsrc(logits, 0u);
+      xe = P::load_one(esrc, extra_off(gn));
     }
   }
 }
@@ -409,39 +579,52 @@ __device__ __forceinline__ bool bwd_zero_row(const BwdRow& q) {
   return q.g == 0.0f && q.lse - q.lse == 0.0f;
 }
 
-// rrl_logprob_bwd for 16-bit rows (losses.py:34-38 backward):
+// rrl_logprob_bwd for 16-bit and float32 rows (losses.py:34-38 backward):
 // dlogits = g * (onehot(target) - exp(x - lse)) with lse, g and log-prob given,
 // so there is no reduction and no exchange between lanes.  The schedule is the
 // fused kernel's sweep 2: the row sits in VGPRs as SL slabs of 16 bytes per
-// lane, is written back as one burst of stores and the registers are refilled
-// with the workgroup's next row as one burst of loads.  The waves never
-// synchronise.
-template <class Tag, int SL>
-__global__ __launch_bounds__(RNT) void resident_bwd_kernel(RowArgs a) {
+// lane (plus the head and tail elements with EXTRAS), is written back as one
+// burst of stores and the registers are refilled with the workgroup's next
+// row as one burst of loads.  The waves never synchronise.
+template <class Tag, int SL, bool EXTRAS>
+__global__ __launch_bounds__(RNT) void resident_bwd_kernel(RowArgs a, int32_t nvec) {
+  using P = Pack16<Tag>;
+  using S = typename Tag::S;
+  constexpr int EPV = P::EPV;
+  constexpr int ESZ = (int)sizeof(S);
   const int tid = threadIdx.x;
   const uint32_t rows32 = (uint32_t)(a.B * a.T);
   const uint32_t T32 = (uint32_t)a.T;
-  const uint32_t row_bytes = (uint32_t)(a.V * 2);
+  const uint32_t V32 = (uint32_t)a.V;
   const int voff = tid * 16;
-  const uint16_t* logits = static_cast<const uint16_t*>(a.logits);
-  uint16_t* dl = static_cast<uint16_t*>(a.dl);
+  const S* logits = static_cast<const S*>(a.logits);
+  S* dl = static_cast<S*>(a.dl);
   uint32_t r = blockIdx.x;
   if (r >= rows32) return;
 
-  auto row_src = [&](uint32_t rr, bool zero) {
+  auto row_ptr = [&](uint32_t rr) {
     const uint32_t bb = rr / T32, tt = rr - bb * T32;
-    return zero ? row_rsrc(logits, 0u)
-                : row_rsrc(logits + (int64_t)bb * a.ls_b + (int64_t)tt * a.ls_t, row_bytes);
+    return logits + (int64_t)bb * a.ls_b + (int64_t)tt * a.ls_t;
+  };
+  auto extra_off = [&](const RowGeo& g) {
+    const int32_t ei = extra_index<Tag>(g, tid);
+    return ei >= 0 ? ei * ESZ : (int)(V32 * ESZ);
   };
   BwdRow next = load_bwd_row(a, r, T32);
   u32x4 x[SL];
+  uint32_t xe = 0;
   {
-    const __amdgpu_buffer_rsrc_t src = row_src(r, bwd_zero_row(next));
+    const bool z0 = bwd_zero_row(next);
+    const S* p0 = row_ptr(r);
+    const RowGeo g0 = row_geo<Tag, EXTRAS>(p0, V32, nvec);
+    const __amdgpu_buffer_rsrc_t src = z0 ? row_rsrc(logits, 0u) : row_rsrc(p0 + g0.head, g0.nbody * 16);
 #pragma unroll
     for (int k = 0; k < SL; ++k) {
       x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (EXTRAS)
+      xe = P::load_one(z0 ? row_rsrc(logits, 0u) : row_rsrc(p0, V32 * ESZ), extra_off(g0));
   }
 
   // The zero rows' store data: a register quad of its own, opaque so that it
@@ -455,6 +638,8 @@ __global__ __launch_bounds__(RNT) void resident_bwd_kernel(RowArgs a) {
     const uint32_t b = r / T32, t = r - b * T32;
     int lane = tid;
     asm volatile("" : "+v"(lane));
+    const RowGeo g = row_geo<Tag, EXTRAS>(row_ptr(r), V32, nvec);
+    const int32_t ei = EXTRAS ? extra_index<Tag>(g, tid) : -1;
     const BwdRow cur = next;
     const uint32_t rn = r + gridDim.x;
     const bool has_next = rn < rows32;
@@ -463,21 +648,27 @@ __global__ __launch_bounds__(RNT) void resident_bwd_kernel(RowArgs a) {
     // exp(x - lse) term, as in the generic kernel.
     const bool tgt_ok = cur.target >= 0 && cur.target < a.V;
     const int32_t tgt = tgt_ok ? (int32_t)cur.target : 0;
-    const int rel = tgt_ok ? (tgt >> 3) - lane : -1;
-    const int ti = tgt & 7;
+    const int32_t bt = tgt - (int32_t)g.head;
+    const bool in_body = tgt_ok && (!EXTRAS || (bt >= 0 && bt < (int32_t)(g.nbody * EPV)));
+    const int rel = in_body ? (bt >> P::LOG2_EPV) - lane : -1;
+    const int ti = bt & (EPV - 1);
+    const bool ex_tgt = EXTRAS && tgt_ok && ei == tgt;
     const bool zero = bwd_zero_row(cur);
-    const float g = cur.g, lse = cur.lse;
+    const float gr = cur.g, lse = cur.lse;
     // -g * exp(x - lse) = -sign(g) * exp2((x - lse) * log2e + log2|g|): the
     // difference is formed first, so no finite lse overflows.
-    const float lg = __log2f(fabsf(g));
-    const bool flip = g > 0.0f;
-    const uint32_t sgn = flip ? 0x80008000u : 0u;
-    const float tgt_d = zero ? 0.0f : target_grad<float>(g, cur.logp, true, 0.0f, lse);
+    const float lg = __log2f(fabsf(gr));
+    const bool flip = gr > 0.0f;
+    const uint32_t sgn = flip ? P::SGN2 : 0u;
+    const float tgt_d = zero ? 0.0f : target_grad<float>(gr, cur.logp, true, 0.0f, lse);
     const float tgt_pre = flip ? -tgt_d : tgt_d;  // the XOR restores tgt_d
+    const bool load_next = has_next && !bwd_zero_row(next);
+    const S* pn = row_ptr(load_next ? rn : r);
+    const RowGeo gn = row_geo<Tag, EXTRAS>(pn, V32, nvec);
     const __amdgpu_buffer_rsrc_t src =
-        has_next ? row_src(rn, bwd_zero_row(next)) : row_rsrc(logits, 0u);
-    const __amdgpu_buffer_rsrc_t dst =
-        row_rsrc(dl + (int64_t)b * a.ds_b + (int64_t)t * a.ds_t, row_bytes);
+        load_next ? row_rsrc(pn + gn.head, gn.nbody * 16) : row_rsrc(logits, 0u);
+    const S* drow = dl + (int64_t)b * a.ds_b + (int64_t)t * a.ds_t;
+    const __amdgpu_buffer_rsrc_t dst = row_rsrc(drow + g.head, g.nbody * 16);
     if (zero) {  // uniform over the workgroup
       // Stores only, with no dependence on the (never read) slabs: a run of
       // zero rows (a clipped GSPO sequence, masked prompt tokens) streams its
@@ -489,21 +680,32 @@ __global__ __launch_bounds__(RNT) void resident_bwd_kernel(RowArgs a) {
         __builtin_amdgcn_raw_buffer_store_b128(zv, dst, voff, k * RNT * 16, kAuxStoreNT);
         __builtin_amdgcn_sched_barrier(0);
       }
+      if constexpr (EXTRAS) {
+        P::store_one(zv.x, row_rsrc(drow, V32 * ESZ), extra_off(g));
+        __builtin_amdgcn_sched_barrier(0);
+      }
     } else {
 #pragma unroll
       for (int k = 0; k < SL; ++k) {
-        float d[8];
-        float v[8];
-        Pack16<Tag>::unpack(x[k], v);
+        float d[EPV];
+        float v[EPV];
+        P::unpack(x[k], v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) d[i] = exp2_hw(__builtin_fmaf(v[i] - lse, kLog2e, lg));
+        for (int i = 0; i < EPV; ++i) d[i] = exp2_hw(__builtin_fmaf(v[i] - lse, kLog2e, lg));
         if (rel == k * RNT) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) d[i] = (i == ti) ? tgt_pre : d[i];
+          for (int i = 0; i < EPV; ++i) d[i] = (i == ti) ? tgt_pre : d[i];
         }
-        u32x4 o = Pack16<Tag>::pack(d);
+        u32x4 o = P::pack(d);
         o.x ^= sgn; o.y ^= sgn; o.z ^= sgn; o.w ^= sgn;
         __builtin_amdgcn_raw_buffer_store_b128(o, dst, voff, k * RNT * 16, kAuxStoreNT);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (EXTRAS) {
+        const float dv =
+            ex_tgt ? tgt_pre : exp2_hw(__builtin_fmaf(P::one(xe) - lse, kLog2e, lg));
+        P::store_one(P::pack_one(dv) ^ (flip ? P::SGN1 : 0u), row_rsrc(drow, V32 * ESZ),
+                     extra_off(g));
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -512,6 +714,8 @@ __global__ __launch_bounds__(RNT) void resident_bwd_kernel(RowArgs a) {
       x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, voff, k * RNT * 16, kAuxLoad);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (EXTRAS)
+      xe = P::load_one(load_next ? row_rsrc(pn, V32 * ESZ) : row_rsrc(logits, 0u), extra_off(gn));
   }
 }
 
@@ -531,7 +735,7 @@ int cu_count_of_current_device(int* n_out) {
 }
 
 // Variants by slab count; a row needs ceil(nvec / 1024) slabs.
-template <class Tag>
+template <class Tag, bool EXTRAS>
 int launch_resident(const RowArgs& a, int32_t nvec, hipStream_t stream) {
   const int need = (nvec + RNT - 1) / RNT;
   int cus = 0;
@@ -543,8 +747,8 @@ int launch_resident(const RowArgs& a, int32_t nvec, hipStream_t stream) {
   const unsigned grid = (unsigned)(rows < cus ? rows : cus);
 #define RRL_RESIDENT_CASE(SLV)                                                                \
   if (need <= SLV) {                                                                          \
-    hipLaunchKernelGGL((resident_fused_kernel<Tag, SLV>), dim3(grid), dim3(RNT), 0, stream,   \
-                       a, nvec);                                                             \
+    hipLaunchKernelGGL((resident_fused_kernel<Tag, SLV, EXTRAS>), dim3(grid), dim3(RNT), 0,   \
+                       stream, a, nvec);                                                     \
     return check_launch("resident_fused_kernel");                                             \
   }
   RRL_RESIDENT_CASE(4)
@@ -557,7 +761,7 @@ int launch_resident(const RowArgs& a, int32_t nvec, hipStream_t stream) {
   return RRL_EINVAL;
 }
 
-template <class Tag>
+template <class Tag, bool EXTRAS>
 int launch_resident_bwd(const RowArgs& a, int32_t nvec, hipStream_t stream) {
   const int need = (nvec + RNT - 1) / RNT;
   int cus = 0;
@@ -566,7 +770,8 @@ int launch_resident_bwd(const RowArgs& a, int32_t nvec, hipStream_t stream) {
   const unsigned grid = (unsigned)(rows < cus ? rows : cus);
 #define RRL_RESIDENT_CASE(SLV)                                                                \
   if (need <= SLV) {                                                                          \
-    hipLaunchKernelGGL((resident_bwd_kernel<Tag, SLV>), dim3(grid), dim3(RNT), 0, stream, a); \
+    hipLaunchKernelGGL((resident_bwd_kernel<Tag, SLV, EXTRAS>), dim3(grid), dim3(RNT), 0,     \
+                       stream, a, nvec);                                                     \
     return check_launch("resident_bwd_kernel");                                               \
   }
   RRL_RESIDENT_CASE(4)
@@ -579,41 +784,62 @@ int launch_resident_bwd(const RowArgs& a, int32_t nvec, hipStream_t stream) {
   return RRL_EINVAL;
 }
 
+template <class Tag>
+int dispatch_resident(int mode, bool extras, const RowArgs& a, int32_t nvec, hipStream_t st) {
+  if (mode == 1)
+    return extras ? launch_resident_bwd<Tag, true>(a, nvec, st)
+                  : launch_resident_bwd<Tag, false>(a, nvec, st);
+  return extras ? launch_resident<Tag, true>(a, nvec, st) : launch_resident<Tag, false>(a, nvec, st);
+}
+
 constexpr int64_t kMaxResidentVec = 20 * RNT;  // SL = 20 fits 128 VGPRs without spills
 
 }  // namespace
 
 // Takes the register-resident kernel (mode 2: the fused single pass; mode 1:
-// rrl_logprob_bwd with the forward's log-probs given) when the row fits the
-// register budget and every row of logits and dlogits is 16-byte aligned;
-// otherwise leaves *launched false so the caller runs the generic row kernel.
+// rrl_logprob_bwd with the forward's log-probs given) for 16-bit and float32
+// logits when the row's 16-byte vectors fit the register budget (V <= 163840
+// 16-bit or 81920 float32 entries).  Rows that are 16-byte aligned with
+// V % (16 / element size) == 0 take the plain variant; any other row takes the
+// variant with head and tail elements, provided every dlogits row sits at its
+// logits row's offset from a 16-byte boundary (same strides mod 16 bytes, as
+// for contiguous tensors or in place).  Otherwise *launched stays false and
+// the caller runs the generic row kernel.
 int maybe_launch_resident(const RowArgs& a, int mode, int logits_dtype, hipStream_t stream,
                           bool* launched) {
   *launched = false;
   if (mode == 2 && (a.pp.flags & RRL_POLICY_GENERIC)) return RRL_OK;
   if (mode != 1 && mode != 2) return RRL_OK;
-  if (logits_dtype != RRL_BF16 && logits_dtype != RRL_F16) return RRL_OK;
+  if (logits_dtype != RRL_BF16 && logits_dtype != RRL_F16 && logits_dtype != RRL_F32)
+    return RRL_OK;
   if (a.dl_dt != logits_dtype || a.accumulate) return RRL_OK;
-  if (a.B * a.T == 0 || a.V % 8 != 0 || a.V / 8 > kMaxResidentVec) return RRL_OK;
-  const auto al16 = [](int64_t elems) { return ((elems * 2) % 16) == 0; };
-  if (((uintptr_t)a.logits % 16) || ((uintptr_t)a.dl % 16)) return RRL_OK;
-  if (!al16(a.ls_b) || !al16(a.ls_t) || !al16(a.ds_b) || !al16(a.ds_t)) return RRL_OK;
+  const int64_t esz = logits_dtype == RRL_F32 ? 4 : 2;
+  const int64_t epv = 16 / esz;
+  if (a.B * a.T == 0 || a.V / epv > kMaxResidentVec) return RRL_OK;
   if (a.B * a.T >= ((int64_t)1 << 31) || a.T >= ((int64_t)1 << 31)) return RRL_OK;
-  const int32_t nvec = (int32_t)(a.V / 8);
+  const auto al16 = [&](int64_t elems) { return ((elems * esz) % 16) == 0; };
+  const bool aligned = a.V % epv == 0 && (uintptr_t)a.logits % 16 == 0 &&
+                       (uintptr_t)a.dl % 16 == 0 && al16(a.ls_b) && al16(a.ls_t) &&
+                       al16(a.ds_b) && al16(a.ds_t);
+  const bool same_offset = ((uintptr_t)a.dl - (uintptr_t)a.logits) % 16 == 0 &&
+                           al16(a.ds_b - a.ls_b) && al16(a.ds_t - a.ls_t);
+  if (!aligned && !same_offset) return RRL_OK;
+  const int32_t nvec = (int32_t)(a.V / epv);
   if (mode == 1) {
     // Scalar loads need 4-byte aligned operands.
     if (a.logp_in == nullptr || a.tgt.ptr == nullptr) return RRL_OK;
     if (((uintptr_t)a.lse | (uintptr_t)a.g | (uintptr_t)a.logp_in) % 4) return RRL_OK;
     if ((uintptr_t)a.tgt.ptr % (a.tgt.dt == RRL_I32 ? 4 : 8)) return RRL_OK;
-    *launched = true;
-    return logits_dtype == RRL_BF16 ? launch_resident_bwd<TagBF16>(a, nvec, stream)
-                                    : launch_resident_bwd<TagF16>(a, nvec, stream);
+  } else {
+    if (a.logp_dt != RRL_F32 || a.records == nullptr) return RRL_OK;
+    if ((uintptr_t)a.records % 16) return RRL_OK;
   }
-  if (a.logp_dt != RRL_F32 || a.records == nullptr) return RRL_OK;
-  if ((uintptr_t)a.records % 16) return RRL_OK;
   *launched = true;
-  return logits_dtype == RRL_BF16 ? launch_resident<TagBF16>(a, nvec, stream)
-                                  : launch_resident<TagF16>(a, nvec, stream);
+  switch (logits_dtype) {
+    case RRL_BF16: return dispatch_resident<TagBF16>(mode, !aligned, a, nvec, stream);
+    case RRL_F16: return dispatch_resident<TagF16>(mode, !aligned, a, nvec, stream);
+    default: return dispatch_resident<TagF32>(mode, !aligned, a, nvec, stream);
+  }
 }
 
 }  // namespace rrl

@@ -711,3 +711,59 @@ def test_fused_skip_masked_rows_bit_identical(device, dtype, V, objective):
     with pytest.raises(ValueError, match="return_logprobs"):
         R.fused_policy_loss(d(x), d(t), d(old), d(adv), d(mask), objective=objective,
                             skip_masked_rows=True, return_logprobs=True, **kw)
+
+
+@pytest.mark.parametrize(
+    "dtype,V,B,T",
+    [
+        (torch.float32, 50257, 4, 68),  # config 1's vocabulary, 272 rows: every head offset
+        (torch.float32, 81923, 4, 1),  # 20 slabs of float32 vectors
+        (torch.float32, 7, 4, 5),  # head and tail elements only
+        (torch.float32, 1, 4, 5),  # the target is the row's only element, a head or tail one
+        (torch.bfloat16, 1, 4, 5),
+        (torch.bfloat16, 50257, 4, 68),
+        (torch.float16, 4099, 4, 7),
+        (torch.bfloat16, 163843, 4, 1),  # 20 full slabs and a tail
+        (torch.bfloat16, 3, 4, 3),
+    ],
+)
+@pytest.mark.parametrize("objective", ["clipped", "sapo"])
+def test_fused_resident_head_tail_rows(device, dtype, V, B, T, objective):
+    """Rows that do not start on a 16-byte boundary or whose length is not a
+    whole number of 16-byte vectors: the register-resident kernel carries the
+    head and tail elements beside its aligned slabs.  Held against the
+    float64 oracle and against the generic row kernel, reached through a
+    logits view whose rows sit at a different offset from the dlogits rows."""
+
+    print(f"[fused-headtail] objective={objective} dtype={dtype} V={V} B={B} T={T}", flush=True)
+    x, t, old, adv, mask = _fused_inputs(40 + V % 97, B, T, V, dtype)
+    kw = (dict(clip_low=0.2, clip_high=0.28) if objective == "clipped"
+          else dict(tau_positive=1.0, tau_negative=1.05))
+    d = lambda z: z.to(device)  # noqa: E731
+    xd = d(x).requires_grad_()
+    out, lp = R.fused_policy_loss(xd, d(t), d(old), d(adv), d(mask), objective=objective,
+                                  return_logprobs=True, **kw)
+    out.loss.backward()
+    kind = {"clipped": "ppo"}.get(objective, objective)
+    out_o, lpo, dlo = o.policy_step(kind, x, t, old, adv, mask, exact=True, **kw)
+    _close(lp, lpo, F32_RTOL, 1e-7, "logp")
+    scale = max(abs(out_o["loss"].item()), adv.abs().mean().item())
+    rt = F32_RTOL if dtype == torch.float32 else 2e-3
+    assert abs(out.loss.item() - out_o["loss"].item()) <= rt * scale
+    if dtype == torch.float32:
+        _close_rows_by_g(xd.grad, dlo, out_o["dloss_dlogp"], F32_RTOL, "dlogits")
+    else:
+        assert _ulp16(xd.grad, dlo, "dlogits") > 0.98
+        _rownorm16(xd.grad, dlo, 2e-3, "dlogits")
+    # generic kernel: logits rows one element off the dlogits rows' offset
+    wide = torch.empty(B, T, V + 1, dtype=dtype, device=device)
+    wide[..., 1:] = d(x)
+    xg = wide[..., 1:].requires_grad_()
+    out_g, lp_g = R.fused_policy_loss(xg, d(t), d(old), d(adv), d(mask), objective=objective,
+                                      return_logprobs=True, **kw)
+    out_g.loss.backward()
+    _close(lp, lp_g, F32_RTOL, 1e-7, "logp resident vs generic")
+    if dtype == torch.float32:
+        _close_rows_by_g(xd.grad, xg.grad, out_o["dloss_dlogp"], F32_RTOL, "resident vs generic")
+    else:
+        _ulp16(xd.grad, xg.grad.float(), "resident vs generic")
