@@ -416,8 +416,10 @@ def traffic_from_profiles(kernel_key, workload_key):
 
 
 SAMPLE_ROWS = 256
-SAMPLE_VARIANTS = {"default": dict(temperature=1.0, top_k=0, top_p=1.0),
-                   "topk50_topp0.9_T0.7": dict(temperature=0.7, top_k=50, top_p=0.9)}
+SAMPLE_VARIANTS = {"default": dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=True),
+                   "topk50_topp0.9_T0.7": dict(temperature=0.7, top_k=50, top_p=0.9,
+                                               do_sample=True),
+                   "greedy": dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=False)}
 
 
 def bench_sample(args):
@@ -441,12 +443,12 @@ def bench_sample(args):
     results = {}
     for name, kw in SAMPLE_VARIANTS.items():
         for i in range(args.warmup):
-            sample_next_token_batch(x, do_sample=True, seed=args.seed, offset=i, **kw)
+            sample_next_token_batch(x, seed=args.seed, offset=i, **kw)
         torch.cuda.synchronize()
-        timed = nat.time_calls("rrl_sample_logprobs")
+        timed = nat.time_calls("rrl_sample_logprobs", capacity=args.steps)
         t0 = time.perf_counter()
         for i in range(args.steps):
-            out = sample_next_token_batch(x, do_sample=True, seed=args.seed, offset=100 + i, **kw)
+            out = sample_next_token_batch(x, seed=args.seed, offset=100 + i, **kw)
         torch.cuda.synchronize()
         el = time.perf_counter() - t0
         nat.time_calls()
@@ -547,7 +549,7 @@ def main():
 
     kernels = (["rrl_fused_logprob_policy"] if path == "fused"
                else ["rrl_logprob_fwd", "rrl_logprob_bwd"])
-    timed = nat.time_calls(*kernels)
+    timed = nat.time_calls(*kernels, capacity=args.steps * 32)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -650,7 +652,7 @@ def main():
 
         for _ in range(args.warmup):
             vstep()
-        vt = nat.time_calls(kernels[0])
+        vt = nat.time_calls(kernels[0], capacity=args.steps * 32)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):

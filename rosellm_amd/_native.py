@@ -143,27 +143,35 @@ def lib() -> ctypes.CDLL:
 # Optional per-entry-point launch timing: name -> list of (start, end)
 # torch.cuda.Event pairs recorded on the stream the call is launched on.
 _timed: dict = {}
+_event_pool: list = []
 
 
-def time_calls(*names: str) -> dict:
+def time_calls(*names: str, capacity: int = 0) -> dict:
     """Record a HIP event pair around every later call of each named entry
     point (on torch's current stream, where the call launches its kernels).
-    Returns the live name -> [(start, end), ...] mapping; ``time_calls()``
-    with no names stops recording."""
+    ``capacity`` calls' events are created up front, so that recording adds
+    only the two event records to a timed call.  Returns the live
+    name -> [(start, end), ...] mapping; ``time_calls()`` with no names stops
+    recording."""
 
-    global _timed
+    global _timed, _event_pool
     _timed = {n: [] for n in names}
+    _event_pool = [torch.cuda.Event(enable_timing=True) for _ in range(2 * capacity)]
     return _timed
+
+
+def _event() -> "torch.cuda.Event":
+    return _event_pool.pop() if _event_pool else torch.cuda.Event(enable_timing=True)
 
 
 def call(name: str, *args) -> None:
     events = _timed.get(name) if _timed else None
     if events is not None:
-        start = torch.cuda.Event(enable_timing=True)
+        start = _event()
         start.record()
     rc = getattr(lib(), name)(*args)
     if events is not None:
-        end = torch.cuda.Event(enable_timing=True)
+        end = _event()
         end.record()
         events.append((start, end))
     if rc != 0:

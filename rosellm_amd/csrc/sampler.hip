@@ -11,18 +11,24 @@
 // pass (from L2 / the memory-side cache: a 151936-entry bf16 row is 297 KB).
 //
 // Passes (top-k, top-p and the tie searches only when active):
-//   1. row max and its lowest index (greedy choice), NaN/+inf check;
+//   1. row max and its lowest index (greedy choice), the sums of
+//      exp((x - max)/T) over every entry (Z without top-k) and over every
+//      entry but the maximum (the greedy token's S_other), NaN/+inf check;
 //   2. top-k: radix select of the k-th largest key, 8 bits per pass;
 //   3. Z = sum over the candidates of exp(x/T - max);
 //   4. top-p: radix select over fixed-point probability mass (exact,
 //      order-independent integer sums), descending key order;
 //   5. inverse CDF in vocabulary order: per-slab totals, then a lane scan
-//      inside the chosen slab;
-//   6. log-sum-exp over the other columns and the token's log-prob, in the
-//      form the training row kernels use (finish_row).
+//      inside the chosen slab; the same sweep sums S_other of the token;
+//   6. the token's log-prob in the form the training row kernels use
+//      (finish_row), with a pass of its own only if step 5 fell back.
+// Greedy decoding is pass 1 alone; sampling without top-k / top-p is passes 1
+// and 5.
 // Ties at a top-k or top-p threshold are kept lowest index first; they are
 // located with the same vocabulary-order search over 0/1 weights.
 #include "row_common.hpp"
+
+#include <type_traits>
 
 namespace rrl {
 
@@ -51,6 +57,10 @@ constexpr int SNT = 1024;
 constexpr int SWAVES = SNT / 64;
 constexpr int MAX_SLABS = 64;
 constexpr double kMassScale = 4503599627370496.0;  // 2^52: fixed-point probability
+constexpr float kLog2e = 1.4426950408889634f;
+
+// 2^x with the hardware exponential (v_exp_f32): exp(y / T) = 2^(y * log2(e) / T).
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 struct SampleArgs {
   const void* logits;
@@ -92,10 +102,10 @@ template <> struct Bits<TagF32> {
 // row that is not 16-byte aligned, or the row's last partial vector, is read
 // element by element.
 template <class Tag>
-__device__ __forceinline__ uint4 load_raw(const typename Tag::S* row, int64_t V, bool al16, int k,
+__device__ __forceinline__ uint4 load_raw(const typename Tag::S* row, int V, bool al16, int k,
                                           int tid) {
   constexpr int VEC = Tag::VEC;
-  const int64_t e0 = ((int64_t)k * SNT + tid) * VEC;
+  const int e0 = (k * SNT + tid) * VEC;
   if (al16 && e0 + VEC <= V) return *reinterpret_cast<const uint4*>(row + e0);
   uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -122,34 +132,84 @@ __device__ __forceinline__ void unpack_raw(const uint4& v, uint32_t (&u)[Tag::VE
   }
 }
 
-// f(k, e0, u) over the slabs of this lane, ten slab loads in flight at a
-// time: a pass re-reads the row from memory, and each batch costs one memory
-// latency, so a 19-slab bf16 row of 151936 entries takes two per pass.
+// f(k, e0, u, full) over the slabs of this lane, ten (f16: eight) slab loads
+// in flight at a time: a pass re-reads the row from memory, and each batch costs one
+// memory latency, so a 19-slab bf16 row of 151936 entries takes two per pass.
+// `full` is std::true_type for a slab that lies inside the row in every lane
+// (all but the last), so f's per-element bounds checks fold away there; the
+// row's last, partial slab gets std::false_type.
 template <class Tag, class F>
-__device__ __forceinline__ void for_slabs(const typename Tag::S* row, int64_t V, bool al16,
-                                          int nslab, F&& f) {
+__device__ __forceinline__ void for_slabs(const typename Tag::S* row, int V, bool al16, int nslab,
+                                          F&& f) {
   constexpr int VEC = Tag::VEC;
-  constexpr int UNR = 10;
+  // f16's conversions need more registers per slab than bf16 or f32 shifts.
+  constexpr int UNR = std::is_same<Tag, TagF16>::value ? 8 : 10;
   const int tid = threadIdx.x;
-  for (int k0 = 0; k0 < nslab; k0 += UNR) {
+  const int nfull = V / (SNT * VEC);
+  for (int k0 = 0; k0 < nfull; k0 += UNR) {
     uint4 w[UNR];
 #pragma unroll
     for (int j = 0; j < UNR; ++j)
-      w[j] = (k0 + j < nslab) ? load_raw<Tag>(row, V, al16, k0 + j, tid) : make_uint4(0, 0, 0, 0);
+      w[j] = (k0 + j < nfull) ? load_raw<Tag>(row, V, al16, k0 + j, tid) : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int j = 0; j < UNR; ++j) {
-      if (k0 + j < nslab) {
+      if (k0 + j < nfull) {
         uint32_t u[VEC];
         unpack_raw<Tag>(w[j], u);
-        f(k0 + j, ((long long)(k0 + j) * SNT + tid) * VEC, u);
+        f(k0 + j, ((k0 + j) * SNT + tid) * VEC, u, std::true_type{});
       }
     }
   }
+  if (nfull < nslab) {
+    uint32_t u[VEC];
+    unpack_raw<Tag>(load_raw<Tag>(row, V, al16, nfull, tid), u);
+    f(nfull, (nfull * SNT + tid) * VEC, u, std::false_type{});
+  }
+}
+
+// Wave64 sums, the same value in every lane: DPP butterflies inside each row
+// of 16 lanes (quad_perm [1,0,3,2], [2,3,0,1], then the half-row and row
+// mirrors), then the four row results through readlane.  VALU-latency steps
+// instead of a chain of LDS-permute round trips.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+  v += __uint_as_float(dpp_u32<0xB1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<0x4E>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<0x141>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<0x140>(__float_as_uint(v)));
+  const int b = __float_as_int(v);
+  return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) +
+          __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
+         (__int_as_float(__builtin_amdgcn_readlane(b, 32)) +
+          __int_as_float(__builtin_amdgcn_readlane(b, 48)));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned long long lo = dpp_u32<CTRL>((uint32_t)b);
+  const unsigned long long hi = dpp_u32<CTRL>((uint32_t)(b >> 32));
+  return __longlong_as_double((long long)((hi << 32) | lo));
+}
+__device__ __forceinline__ double lane_read_f64(double v, int l) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned long long lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+  const unsigned long long hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+  return __longlong_as_double((long long)((hi << 32) | lo));
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+  v += dpp_f64<0xB1>(v);
+  v += dpp_f64<0x4E>(v);
+  v += dpp_f64<0x141>(v);
+  v += dpp_f64<0x140>(v);
+  return (lane_read_f64(v, 0) + lane_read_f64(v, 16)) + (lane_read_f64(v, 32) + lane_read_f64(v, 48));
 }
 
 // Raw bits of element e of a row.
 template <class Tag>
-__device__ __forceinline__ uint32_t load_one(const typename Tag::S* row, long long e) {
+__device__ __forceinline__ uint32_t load_one(const typename Tag::S* row, int e) {
   if (sizeof(typename Tag::S) == 2) return reinterpret_cast<const uint16_t*>(row)[e];
   return reinterpret_cast<const uint32_t*>(row)[e];
 }
@@ -162,14 +222,14 @@ struct SearchShared {
   float slab_e[MAX_SLABS];
   float wave_f[SWAVES];
   int wave_i[SWAVES];
-  long long wave_l[SWAVES];
-  long long sel;
+  int wave_l[SWAVES];
+  int sel;
   float other;
   int other_ok;
 };
 
 // Lowest-index maximum over the workgroup: (value, index) pairs, NaN never wins.
-__device__ __forceinline__ void argmax_merge(float& bx, long long& bi, float ox, long long oi) {
+__device__ __forceinline__ void argmax_merge(float& bx, int& bi, float ox, int oi) {
   if (ox > bx || (ox == bx && oi < bi)) {
     bx = ox;
     bi = oi;
@@ -194,33 +254,38 @@ struct WE {
 // sh.other (sh.other_ok = 0 on the rounding fallback): per-slab totals from
 // the first sweep plus the chosen slab re-summed without the element, so no
 // total is ever reduced by subtraction.
-template <class Tag, bool OTHER, class WFn, class TFn>
-__device__ __forceinline__ long long vocab_search(const typename Tag::S* row, int64_t V, bool al16,
+//
+// ALL_POSITIVE: every element's weight is known to be > 0 (the floored
+// distribution without top-k / top-p), so the last positive element is V - 1
+// and is not tracked per element.
+template <class Tag, bool OTHER, bool ALL_POSITIVE, class WFn, class TFn>
+__device__ __forceinline__ int vocab_search(const typename Tag::S* row, int V, bool al16,
                                                   int nslab, WFn wfn, TFn tfn, SearchShared& sh) {
   constexpr int VEC = Tag::VEC;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  long long last_pos = -1;
-  for_slabs<Tag>(row, V, al16, nslab, [&](int k, long long e0, const uint32_t (&u)[VEC]) {
+  int last_pos = -1;
+  for_slabs<Tag>(row, V, al16, nslab, [&](int k, int e0, const uint32_t (&u)[VEC], auto full) {
     float facc = 0.0f, eacc = 0.0f;
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
       WE we = {0.0f, 0.0f};
-      if (e0 + i < V) we = wfn(e0 + i, u[i]);
+      if (full || e0 + i < V) we = wfn(e0 + i, u[i]);
       asm volatile("" : "+v"(we.w));  // the same rounding in both evaluations
-      if (we.w > 0.0f) last_pos = e0 + i;
+      if (!ALL_POSITIVE && we.w > 0.0f) last_pos = e0 + i;
       facc += we.w;
       if (OTHER) eacc += we.e;
     }
-    double acc = wave_sum((double)facc);
+    const double acc = wave_sum_d((double)facc);
     if (lane == 0) sh.wave_slab[wave][k] = acc;
     if (OTHER) {
-      eacc = wave_sum(eacc);
+      eacc = wave_sum_f(eacc);
       if (lane == 0) sh.wave_e[wave][k] = eacc;
     }
   });
   // last positive element over the workgroup
+  if (ALL_POSITIVE) last_pos = V - 1;
   for (int o = 32; o > 0; o >>= 1) {
-    const long long t = __shfl_xor(last_pos, o, 64);
+    const int t = __shfl_xor(last_pos, o, 64);
     last_pos = t > last_pos ? t : last_pos;
   }
   if (lane == 0) sh.wave_l[wave] = last_pos;
@@ -257,7 +322,7 @@ __device__ __forceinline__ long long vocab_search(const typename Tag::S* row, in
   // Lane scan inside slab ks.
   uint32_t u[VEC];
   unpack_raw<Tag>(load_raw<Tag>(row, V, al16, ks, tid), u);
-  const long long e0 = ((long long)ks * SNT + tid) * VEC;
+  const int e0 = (ks * SNT + tid) * VEC;
   float w8[VEC], e8[VEC];
   float flw = 0.0f;
 #pragma unroll
@@ -301,7 +366,7 @@ __device__ __forceinline__ long long vocab_search(const typename Tag::S* row, in
   const bool claim = lw > 0.0 && lexcl <= target && (target < lincl || tid == last_lane);
   if (claim) {
     double cum = lexcl;
-    long long pick = -1, lastp = -1;
+    int pick = -1, lastp = -1;
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
       if (w8[i] > 0.0f) {
@@ -313,7 +378,7 @@ __device__ __forceinline__ long long vocab_search(const typename Tag::S* row, in
     sh.sel = pick >= 0 ? pick : lastp;
   }
   __syncthreads();
-  const long long sel = sh.sel;
+  const int sel = sh.sel;
   if (OTHER) {
     // slab ks without the chosen element, plus every other slab's total
     float es = 0.0f;
@@ -329,8 +394,7 @@ __device__ __forceinline__ long long vocab_search(const typename Tag::S* row, in
       for (int k = 0; k < nslab; ++k)
         if (k != ks) o += sh.slab_e[k];
       sh.other = o;
-      sh.other_ok = (sel >= e0 - (long long)tid * VEC &&
-                     sel < e0 - (long long)tid * VEC + (long long)SNT * VEC) ? 1 : 0;
+      sh.other_ok = (sel >= e0 - tid * VEC && sel < e0 - tid * VEC + SNT * VEC) ? 1 : 0;
     }
   }
   __syncthreads();
@@ -345,9 +409,9 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   __shared__ SearchShared sh;
   __shared__ uint32_t hist[256];
   __shared__ unsigned long long histm[256];
-  __shared__ float sh_m[SWAVES], sh_s[SWAVES];
+  __shared__ float sh_m[SWAVES], sh_s[2 * SWAVES];
   __shared__ float sh_x[SWAVES];
-  __shared__ long long sh_e[SWAVES];
+  __shared__ int sh_e[SWAVES];
   __shared__ uint32_t sh_digit;
   __shared__ int sh_found;
   __shared__ unsigned long long sh_above;
@@ -355,38 +419,55 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   const int64_t r = blockIdx.x;
   if (r >= a.B) return;
   const S* row = static_cast<const S*>(a.logits) + r * a.stride;
-  const int64_t V = a.V;
+  const int V = (int)a.V;  // at most SNT * VEC * MAX_SLABS (checked on the host)
   const bool al16 = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
-  const int nslab = (int)((V + (int64_t)SNT * VEC - 1) / ((int64_t)SNT * VEC));
+  const int nslab = (V + SNT * VEC - 1) / (SNT * VEC);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // x / T as x * (1/T): within an ulp of the division, and one multiply in
   // the per-element work (the sampler is bound by its VALU issue rate).
   const float iT = 1.0f / a.temp;
 
-  // 1. row max with its lowest index and the online (max, sum exp) of x / T
-  // over the whole row.  A lane walks its elements in increasing index
-  // order, so a strict > keeps the first of equal maxima.  NaN and +inf
-  // reach the online sum (exp(NaN), exp(inf - inf)) and are caught there.
+  // 1. Per lane: the first maximum of the logits and its index, and the sum
+  // of exp((x - max) / T) over the lane's other entries.  A lane walks its
+  // slabs in increasing index order and keeps the first of equal maxima
+  // (strict >); fmaxf skips NaN, so NaN never wins, while NaN and +inf reach
+  // the sum (2^NaN, 2^(inf - inf)) and are caught there.  The maximum's own
+  // term (exactly 1) is kept out of the sum and added back per lane below, so
+  // S_other of the greedy token needs no subtraction and no second pass.
+  const float c2 = iT * kLog2e;  // exp(y / T) = 2^(y * c2)
   float bx = -__builtin_huge_valf();
   int bi32 = 0x7fffffff;
-  float om = -__builtin_huge_valf(), os = 0.0f;
-  for_slabs<Tag>(row, V, al16, nslab, [&](int, long long e0, const uint32_t (&u)[VEC]) {
+  float sx = 0.0f;
+  for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
     float v[VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      const bool ok = e0 + i < V;
-      const float x = ok ? Bits<Tag>::val(u[i]) : -__builtin_huge_valf();
-      const bool up = x > bx;
-      bx = up ? x : bx;
-      bi32 = up ? (int)(e0 + i) : bi32;
-      v[i] = x * iT;
-    }
-    online_update<float, VEC>(om, os, v, -1);
+    for (int i = 0; i < VEC; ++i)
+      v[i] = (full || e0 + i < V) ? Bits<Tag>::val(u[i]) : -__builtin_huge_valf();
+    float mc = v[0];
+#pragma unroll
+    for (int i = 1; i < VEC; ++i) mc = fmaxf(mc, v[i]);
+    int ic = VEC - 1;
+#pragma unroll
+    for (int i = VEC - 2; i >= 0; --i) ic = (v[i] == mc) ? i : ic;
+    const bool up = mc > bx;
+    const int skip = up ? ic : -1;  // the new maximum's own term stays out
+    const float mn = fmaxf(bx, mc);
+    const float mg = fmaxf(mn, -__FLT_MAX__);
+    float es = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) es += (i == skip) ? 0.0f : exp2_hw((v[i] - mg) * c2);
+    // A replaced maximum joins the other entries with its term 1.
+    const float old_term = (up && bx > -__builtin_huge_valf()) ? 1.0f : 0.0f;
+    sx = __builtin_fmaf(sx + old_term, exp2_hw((bx - mg) * c2), es);
+    bi32 = up ? e0 + ic : bi32;
+    bx = mn;
   });
-  long long bi = bi32;
+  const float lane_max = bx;
+  const int lane_arg = bi32;
+  int bi = bi32;
   for (int o = 32; o > 0; o >>= 1) {
     const float ox = __shfl_xor(bx, o, 64);
-    const long long oi = __shfl_xor(bi, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
     argmax_merge(bx, bi, ox, oi);
   }
   if (lane == 0) {
@@ -398,9 +479,19 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   bi = sh_e[0];
   for (int w = 1; w < SWAVES; ++w) argmax_merge(bx, bi, sh_x[w], sh_e[w]);
   __syncthreads();
-  block_online_combine<SNT, float>(om, os, sh_m, sh_s);
+  // Row totals relative to the row maximum: every entry (Z without top-k),
+  // and every entry but the argmax (the greedy token's S_other).
+  float tot[2];
+  {
+    const float own = lane_max > -__builtin_huge_valf() ? 1.0f : 0.0f;
+    const float f = bx > -__builtin_huge_valf() ? exp2_hw((lane_max - bx) * c2) : 0.0f;
+    tot[0] = (sx + own) * f;
+    tot[1] = (sx + (lane_arg == bi ? 0.0f : own)) * f;
+  }
+  block_sum<SNT, 2, float>(tot, sh_s);
+  const float os = tot[0], s_arg_other = tot[1];
   const bool row_bad = bx == -__builtin_huge_valf() || bi >= V || os != os ||
-                       om == __builtin_huge_valf();
+                       bx * iT == __builtin_huge_valf();
   if (row_bad) {
     if (tid == 0) {
       raise_flag(a.status, RRL_FLAG_BAD_PROBS);
@@ -412,27 +503,28 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   }
   const float m = bx * iT;  // max of x / T (scaling by 1/T > 0 is monotone)
 
-  long long tok = bi;
+  int tok = bi;
   float logq = 0.0f;
-  bool have_other = false;
-  float s_other = 0.0f;
+  bool have_other = a.greedy != 0;  // the argmax's S_other came with pass 1
+  float s_other = s_arg_other;
   if (!a.greedy) {
     // 2. top-k candidates: the k-th largest key by an MSB-first radix select.
     const bool use_k = a.top_k > 0 && a.top_k < V;
     uint32_t kth = 0;
     int need_k = 0, cnt_k = 0;
-    long long cut_k = -1;
+    int cut_k = -1;
     if (use_k) {
       uint32_t prefix = 0, pmask = 0;
       int kk = (int)a.top_k;
       for (int shift = KB - 8; shift >= 0; shift -= 8) {
         for (int i = tid; i < 256; i += SNT) hist[i] = 0;
         __syncthreads();
-        for_slabs<Tag>(row, V, al16, nslab, [&](int, long long e0, const uint32_t (&u)[VEC]) {
+        for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
 #pragma unroll
           for (int i = 0; i < VEC; ++i) {
             const uint32_t key = float_key<KB>(u[i]);
-            if (e0 + i < V && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+            if ((full || e0 + i < V) && (key & pmask) == prefix)
+              atomicAdd(&hist[(key >> shift) & 255u], 1u);
           }
         });
         __syncthreads();
@@ -467,24 +559,24 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
       need_k = kk;  // 1 <= need_k <= cnt_k tokens at the threshold are kept
       if (need_k < cnt_k) {
         const double nth = (double)(need_k - 1);
-        cut_k = vocab_search<Tag, false>(
+        cut_k = vocab_search<Tag, false, false>(
             row, V, al16, nslab,
-            [&](long long, uint32_t b) { return WE{float_key<KB>(b) == kth ? 1.0f : 0.0f, 0.0f}; },
+            [&](int, uint32_t b) { return WE{float_key<KB>(b) == kth ? 1.0f : 0.0f, 0.0f}; },
             [&](double) { return nth; }, sh);
       }
     }
-    auto cand = [&](long long e, uint32_t key) {
+    auto cand = [&](int e, uint32_t key) {
       return !use_k || key > kth || (key == kth && (need_k >= cnt_k || e <= cut_k));
     };
 
     // 3. Z over the candidates (the whole row's online sum without top-k).
-    float zs = os * expf(om - m);  // om == m: the same maximum
+    float zs = os;  // relative to the row maximum
     if (use_k) {
       zs = 0.0f;
-      for_slabs<Tag>(row, V, al16, nslab, [&](int, long long e0, const uint32_t (&u)[VEC]) {
+      for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          if (e0 + i < V && cand(e0 + i, float_key<KB>(u[i])))
+          if ((full || e0 + i < V) && cand(e0 + i, float_key<KB>(u[i])))
             zs += expf(Bits<Tag>::val(u[i]) * iT - m);
         }
       });
@@ -505,7 +597,7 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
     bool p_found = false;
     uint32_t pth = 0;
     unsigned long long n_keep = 0, cnt_p = 0;
-    long long cut_p = -1;
+    int cut_p = -1;
     if (use_p) {
       const unsigned long long P = (unsigned long long)(a.top_p * kMassScale);
       uint32_t prefix = 0, pmask = 0;
@@ -518,11 +610,11 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
         }
         if (tid == 0) sh_found = 0;
         __syncthreads();
-        for_slabs<Tag>(row, V, al16, nslab, [&](int, long long e0, const uint32_t (&u)[VEC]) {
+        for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
 #pragma unroll
           for (int i = 0; i < VEC; ++i) {
             const uint32_t key = float_key<KB>(u[i]);
-            if (e0 + i < V && (key & pmask) == prefix && cand(e0 + i, key)) {
+            if ((full || e0 + i < V) && (key & pmask) == prefix && cand(e0 + i, key)) {
               const unsigned long long fx =
                   (unsigned long long)((double)prob(u[i]) * kMassScale);
               atomicAdd(&hist[(key >> shift) & 255u], 1u);
@@ -576,9 +668,9 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
         if (pth == float_key<KB>(load_one<Tag>(row, bi)) && n_keep == 0) n_keep = 1;
         if (n_keep > 0 && n_keep < cnt_p) {
           const double nth = (double)(n_keep - 1);
-          cut_p = vocab_search<Tag, false>(
+          cut_p = vocab_search<Tag, false, false>(
               row, V, al16, nslab,
-              [&](long long e, uint32_t b) {
+              [&](int e, uint32_t b) {
                 const uint32_t key = float_key<KB>(b);
                 return WE{(key == pth && cand(e, key)) ? 1.0f : 0.0f, 0.0f};
               },
@@ -586,12 +678,12 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
         }
       }
     }
-    auto kept = [&](long long e, uint32_t key) {
+    auto kept = [&](int e, uint32_t key) {
       return !p_found || key > pth ||
              (key == pth && (n_keep >= cnt_p || (n_keep > 0 && e <= cut_p)));
     };
     // q weight with the element's exp(x/T - m) for the log-prob's S_other
-    auto qwe = [&](long long e, uint32_t b) {
+    auto qwe = [&](int e, uint32_t b) {
       const uint32_t key = float_key<KB>(b);
       const float ev = ex(b);
       WE r;
@@ -607,22 +699,38 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
     philox4x32_10(c, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
     const double u01 = (double)(c[0] >> 8) * 5.9604644775390625e-8;  // 2^-24
     __shared__ double sh_total;
-    tok = vocab_search<Tag, true>(
-        row, V, al16, nslab, qwe,
-        [&](double total) {
-          if (tid == 0) sh_total = total;
-          return u01 * total;
-        },
-        sh);
-    const double qtot = sh_total;
-    have_other = sh.other_ok != 0;
-    s_other = sh.other;
-    __syncthreads();
-    if (tok < 0 || tok >= V) {  // no positive weight: cannot happen, q >= 1e-9
-      tok = bi;
-      have_other = false;
+    auto target = [&](double total) {
+      if (tid == 0) sh_total = total;
+      return u01 * total;
+    };
+    auto draw = [&](auto wfn, auto all_positive) {
+      tok = vocab_search<Tag, true, decltype(all_positive)::value>(row, V, al16, nslab, wfn,
+                                                                   target, sh);
+      const double qtot = sh_total;
+      have_other = sh.other_ok != 0;
+      s_other = sh.other;
+      __syncthreads();
+      if (tok < 0 || tok >= V) {  // no positive weight: cannot happen, q >= 1e-9
+        tok = bi;
+        have_other = false;
+      }
+      if (tid == 0) logq = (float)(log((double)wfn(tok, load_one<Tag>(row, tok)).w) - log(qtot));
+    };
+    if (!use_k && !p_found) {
+      // The floored softmax itself: q = max(exp((x - max) / T) / Z, 1e-9) on
+      // every entry, one hardware exponential per entry.
+      draw(
+          [&](int, uint32_t b) {
+            const float ev = exp2_hw((Bits<Tag>::val(b) - bx) * c2);
+            WE r;
+            r.e = ev;
+            r.w = fmaxf(ev * inv_z, 1e-9f);
+            return r;
+          },
+          std::true_type{});
+    } else {
+      draw(qwe, std::false_type{});
     }
-    if (tid == 0) logq = (float)(log((double)qwe(tok, load_one<Tag>(row, tok)).w) - log(qtot));
   }
 
   // 6. log_softmax(x / T) at the token, as the training row kernels form it:
@@ -633,12 +741,12 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   if (!have_other) {
     mm = -__builtin_huge_valf();
     ss = 0.0f;
-    for_slabs<Tag>(row, V, al16, nslab, [&](int, long long e0, const uint32_t (&u)[VEC]) {
+    for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
       float v[VEC];
 #pragma unroll
       for (int i = 0; i < VEC; ++i)
-        v[i] = e0 + i < V ? Bits<Tag>::val(u[i]) * iT : -__builtin_huge_valf();
-      const long long rel = tok - e0;
+        v[i] = (full || e0 + i < V) ? Bits<Tag>::val(u[i]) * iT : -__builtin_huge_valf();
+      const int rel = tok - e0;
       online_update<float, VEC>(mm, ss, v, (rel >= 0 && rel < VEC) ? (int)rel : -1);
     });
     block_online_combine<SNT, float>(mm, ss, sh_m, sh_s);
