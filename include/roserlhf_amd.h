@@ -201,8 +201,10 @@ RRL_API int rrl_policy_bwd(const rrl_policy_params* params, int64_t B, int64_t T
  * RRL_POLICY_SUM), 1/(B*L_b) for SAPO, and flags EMPTY_MASK / EMPTY_ROW.  The objective scalars then come from
  * rrl_policy_fwd on the returned logp.
  * records: caller workspace of rrl_fused_records_bytes(B, T) bytes, where the
- * 16-bit fast path packs each token's target, old log-prob, advantage and
- * mask weight * row_coef (16 bytes per token) for one scalar load per row. */
+ * register-resident path (16-bit and float32 logits, V <= 163840 16-bit or
+ * 81920 float32 entries) packs each token's target, old log-prob, advantage
+ * and mask weight * row_coef (16 bytes per token) for one scalar load per
+ * row. */
 RRL_API int rrl_policy_row_coef(const rrl_policy_params* params, int64_t B, int64_t T,
                         rrl_view mask, int32_t acc_dtype, void* row_coef,
                         void* workspace, int32_t* status, void* stream);

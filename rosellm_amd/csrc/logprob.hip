@@ -5,9 +5,11 @@
 // 16-byte loads and keeps an online (max, sum exp) pair per lane, combined
 // across the wave with shuffles and across waves through LDS.  Sweep 2 (backward
 // and single pass) writes dlogits = g * (onehot - exp(x - lse)), so no softmax
-// tensor is ever materialised.  The bf16 fast path keeps the whole row in
-// registers between the sweeps (logprob_resident.hip); this file is the generic
-// path for every dtype, alignment and vocabulary size.
+// tensor is ever materialised.  The register-resident kernels
+// (logprob_resident.hip) keep the whole row in registers between the sweeps for
+// bf16, f16 and float32 rows up to 163840 (16-bit) or 81920 (float32) entries;
+// this file is the generic path for float64, longer rows, accumulation and
+// dlogits rows laid out differently from the logits rows.
 #include "policy_math.hpp"
 #include "rrl_common.hpp"
 #include "row_common.hpp"

@@ -27,7 +27,7 @@ struct RowArgs {
   rrl_policy_params pp;
   View old, adv, mask;
   const void* row_coef;
-  void* records;  // 16-bit fast path: packed per-token records (TokenRecord)
+  void* records;  // register-resident path: packed per-token records (TokenRecord)
   int32_t* status;
 };
 

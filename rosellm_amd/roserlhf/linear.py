@@ -356,7 +356,7 @@ class _FusedLinearPolicy(torch.autograd.Function):
 
         flags, dh, dw = sweep(params)
         if flags & nat.FLAG_FAST_RANGE:
-            # Some row's log-sum-exp lies beyond the 16-bit fast kernel's
+            # Some row's log-sum-exp lies beyond the register-resident 16-bit kernel's
             # exponent range: the logits are recomputed anyway, so redo the
             # sweep on the generic row kernel.
             generic = nat.RrlPolicyParams.from_buffer_copy(params)

@@ -800,7 +800,7 @@ class _FusedPolicy(torch.autograd.Function):
 
         flags = run(params)
         if flags & nat.FLAG_FAST_RANGE:
-            # A row's log-sum-exp lies beyond the 16-bit fast kernel's exponent
+            # A row's log-sum-exp lies beyond the register-resident 16-bit kernel's exponent
             # range (logits near the format's maximum): redo the call on the
             # generic row kernel.
             if inplace:

@@ -1,8 +1,8 @@
 """rrl_logprob_bwd through the C ABI against the float64 oracle (MI355X).
 
 dlogits = g * (onehot(target) - softmax(x)) (losses.py:34-38 backward, the
-composed path's second read of the logits).  16-bit rows with V % 8 == 0 and
-16-byte aligned rows take the register-resident kernel; the same call with
+composed path's second read of the logits).  16-byte aligned rows that are a
+whole number of 16-byte vectors take the register-resident kernel; the same call with
 accumulate = 1 into zeros takes the generic row kernel, so the two are also
 held against each other.  Float32 rows, odd vocabularies and rows that do not
 start on a 16-byte boundary take the resident variant that carries the
