@@ -19,9 +19,9 @@
 //   4. top-p: radix select over fixed-point probability mass (exact,
 //      order-independent integer sums), descending key order;
 //   5. inverse CDF in vocabulary order: per-slab totals, then a lane scan
-//      inside the chosen slab; the same sweep sums S_other of the token;
+//      inside the chosen slab;
 //   6. the token's log-prob in the form the training row kernels use
-//      (finish_row), with a pass of its own only if step 5 fell back.
+//      (finish_row), from pass 1's sums.
 // Greedy decoding is pass 1 alone; sampling without top-k / top-p is passes 1
 // and 5.
 // Ties at a top-k or top-p threshold are kept lowest index first; they are
@@ -167,24 +167,13 @@ __device__ __forceinline__ void for_slabs(const typename Tag::S* row, int V, boo
   }
 }
 
-// Wave64 sums, the same value in every lane: DPP butterflies inside each row
+// Wave64 sum, the same value in every lane: DPP butterflies inside each row
 // of 16 lanes (quad_perm [1,0,3,2], [2,3,0,1], then the half-row and row
 // mirrors), then the four row results through readlane.  VALU-latency steps
 // instead of a chain of LDS-permute round trips.
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
-}
-__device__ __forceinline__ float wave_sum_f(float v) {
-  v += __uint_as_float(dpp_u32<0xB1>(__float_as_uint(v)));
-  v += __uint_as_float(dpp_u32<0x4E>(__float_as_uint(v)));
-  v += __uint_as_float(dpp_u32<0x141>(__float_as_uint(v)));
-  v += __uint_as_float(dpp_u32<0x140>(__float_as_uint(v)));
-  const int b = __float_as_int(v);
-  return (__int_as_float(__builtin_amdgcn_readlane(b, 0)) +
-          __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
-         (__int_as_float(__builtin_amdgcn_readlane(b, 32)) +
-          __int_as_float(__builtin_amdgcn_readlane(b, 48)));
 }
 template <int CTRL>
 __device__ __forceinline__ double dpp_f64(double v) {
@@ -218,14 +207,9 @@ struct SearchShared {
   double wave_slab[SWAVES][MAX_SLABS];
   double slab_tot[MAX_SLABS];
   double wave_tot[SWAVES];
-  float wave_e[SWAVES][MAX_SLABS];
-  float slab_e[MAX_SLABS];
-  float wave_f[SWAVES];
   int wave_i[SWAVES];
   int wave_l[SWAVES];
   int sel;
-  float other;
-  int other_ok;
 };
 
 // Lowest-index maximum over the workgroup: (value, index) pairs, NaN never wins.
@@ -236,13 +220,8 @@ __device__ __forceinline__ void argmax_merge(float& bx, int& bi, float ox, int o
   }
 }
 
-// A weight and, for the log-prob, the element's exp(x/T - max).
-struct WE {
-  float w, e;
-};
-
 // First element, in vocabulary order, whose inclusive prefix of the weights
-// exceeds target(total of the weights).  wfn(e, bits).w >= 0 must be a pure
+// exceeds target(total of the weights).  wfn(e, bits) >= 0 must be a pure
 // function of its arguments (it is evaluated twice per element).  Each lane
 // adds its 8 (or 4) weights in float32 and the groups in float64, so ~1e5
 // floor weights of 1e-9 next to a weight near 1 keep their share of the
@@ -250,37 +229,27 @@ struct WE {
 // the last element with a positive weight is returned; -1 when every weight
 // is 0.
 //
-// OTHER: also sums wfn(...).e over every element but the one returned, into
-// sh.other (sh.other_ok = 0 on the rounding fallback): per-slab totals from
-// the first sweep plus the chosen slab re-summed without the element, so no
-// total is ever reduced by subtraction.
-//
 // ALL_POSITIVE: every element's weight is known to be > 0 (the floored
 // distribution without top-k / top-p), so the last positive element is V - 1
 // and is not tracked per element.
-template <class Tag, bool OTHER, bool ALL_POSITIVE, class WFn, class TFn>
+template <class Tag, bool ALL_POSITIVE, class WFn, class TFn>
 __device__ __forceinline__ int vocab_search(const typename Tag::S* row, int V, bool al16,
                                                   int nslab, WFn wfn, TFn tfn, SearchShared& sh) {
   constexpr int VEC = Tag::VEC;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int last_pos = -1;
   for_slabs<Tag>(row, V, al16, nslab, [&](int k, int e0, const uint32_t (&u)[VEC], auto full) {
-    float facc = 0.0f, eacc = 0.0f;
+    float facc = 0.0f;
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
-      WE we = {0.0f, 0.0f};
-      if (full || e0 + i < V) we = wfn(e0 + i, u[i]);
-      asm volatile("" : "+v"(we.w));  // the same rounding in both evaluations
-      if (!ALL_POSITIVE && we.w > 0.0f) last_pos = e0 + i;
-      facc += we.w;
-      if (OTHER) eacc += we.e;
+      float w = 0.0f;
+      if (full || e0 + i < V) w = wfn(e0 + i, u[i]);
+      asm volatile("" : "+v"(w));  // the same rounding in both evaluations
+      if (!ALL_POSITIVE && w > 0.0f) last_pos = e0 + i;
+      facc += w;
     }
     const double acc = wave_sum_d((double)facc);
     if (lane == 0) sh.wave_slab[wave][k] = acc;
-    if (OTHER) {
-      eacc = wave_sum_f(eacc);
-      if (lane == 0) sh.wave_e[wave][k] = eacc;
-    }
   });
   // last positive element over the workgroup
   if (ALL_POSITIVE) last_pos = V - 1;
@@ -289,17 +258,11 @@ __device__ __forceinline__ int vocab_search(const typename Tag::S* row, int V, b
     last_pos = t > last_pos ? t : last_pos;
   }
   if (lane == 0) sh.wave_l[wave] = last_pos;
-  if (tid == 0) sh.other_ok = 0;
   __syncthreads();
   if (tid < nslab) {
     double s = 0.0;
-    float se = 0.0f;
-    for (int w = 0; w < SWAVES; ++w) {
-      s += sh.wave_slab[w][tid];
-      if (OTHER) se += sh.wave_e[w][tid];
-    }
+    for (int w = 0; w < SWAVES; ++w) s += sh.wave_slab[w][tid];
     sh.slab_tot[tid] = s;
-    if (OTHER) sh.slab_e[tid] = se;
   }
   last_pos = sh.wave_l[0];
   for (int w = 1; w < SWAVES; ++w) last_pos = sh.wave_l[w] > last_pos ? sh.wave_l[w] : last_pos;
@@ -317,22 +280,21 @@ __device__ __forceinline__ int vocab_search(const typename Tag::S* row, int V, b
     }
     run += t;
   }
-  if (ks < 0) return last_pos;  // uniform over the workgroup; sh.other_ok stays 0
+  if (ks < 0) return last_pos;  // uniform over the workgroup
 
   // Lane scan inside slab ks.
   uint32_t u[VEC];
   unpack_raw<Tag>(load_raw<Tag>(row, V, al16, ks, tid), u);
   const int e0 = (ks * SNT + tid) * VEC;
-  float w8[VEC], e8[VEC];
+  float w8[VEC];
   float flw = 0.0f;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) {
-    WE we = {0.0f, 0.0f};
-    if (e0 + i < V) we = wfn(e0 + i, u[i]);
-    asm volatile("" : "+v"(we.w));
-    w8[i] = we.w;
-    e8[i] = we.e;
-    flw += we.w;
+    float w = 0.0f;
+    if (e0 + i < V) w = wfn(e0 + i, u[i]);
+    asm volatile("" : "+v"(w));
+    w8[i] = w;
+    flw += w;
   }
   const double lw = (double)flw;
   double incl = lw;
@@ -379,24 +341,6 @@ __device__ __forceinline__ int vocab_search(const typename Tag::S* row, int V, b
   }
   __syncthreads();
   const int sel = sh.sel;
-  if (OTHER) {
-    // slab ks without the chosen element, plus every other slab's total
-    float es = 0.0f;
-#pragma unroll
-    for (int i = 0; i < VEC; ++i)
-      if (e0 + i != sel) es += e8[i];
-    es = wave_sum(es);
-    if (lane == 0) sh.wave_f[wave] = es;
-    __syncthreads();
-    if (tid == 0) {
-      float o = 0.0f;
-      for (int w = 0; w < SWAVES; ++w) o += sh.wave_f[w];
-      for (int k = 0; k < nslab; ++k)
-        if (k != ks) o += sh.slab_e[k];
-      sh.other = o;
-      sh.other_ok = (sel >= e0 - tid * VEC && sel < e0 - tid * VEC + SNT * VEC) ? 1 : 0;
-    }
-  }
   __syncthreads();
   return sel;
 }
@@ -409,7 +353,7 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   __shared__ SearchShared sh;
   __shared__ uint32_t hist[256];
   __shared__ unsigned long long histm[256];
-  __shared__ float sh_m[SWAVES], sh_s[2 * SWAVES];
+  __shared__ float sh_s[2 * SWAVES];
   __shared__ float sh_x[SWAVES];
   __shared__ int sh_e[SWAVES];
   __shared__ uint32_t sh_digit;
@@ -505,8 +449,7 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
 
   int tok = bi;
   float logq = 0.0f;
-  bool have_other = a.greedy != 0;  // the argmax's S_other came with pass 1
-  float s_other = s_arg_other;
+  float s_other = s_arg_other;  // the argmax's; replaced below for another token
   if (!a.greedy) {
     // 2. top-k candidates: the k-th largest key by an MSB-first radix select.
     const bool use_k = a.top_k > 0 && a.top_k < V;
@@ -559,9 +502,9 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
       need_k = kk;  // 1 <= need_k <= cnt_k tokens at the threshold are kept
       if (need_k < cnt_k) {
         const double nth = (double)(need_k - 1);
-        cut_k = vocab_search<Tag, false, false>(
+        cut_k = vocab_search<Tag, false>(
             row, V, al16, nslab,
-            [&](int, uint32_t b) { return WE{float_key<KB>(b) == kth ? 1.0f : 0.0f, 0.0f}; },
+            [&](int, uint32_t b) { return float_key<KB>(b) == kth ? 1.0f : 0.0f; },
             [&](double) { return nth; }, sh);
       }
     }
@@ -668,11 +611,11 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
         if (pth == float_key<KB>(load_one<Tag>(row, bi)) && n_keep == 0) n_keep = 1;
         if (n_keep > 0 && n_keep < cnt_p) {
           const double nth = (double)(n_keep - 1);
-          cut_p = vocab_search<Tag, false, false>(
+          cut_p = vocab_search<Tag, false>(
               row, V, al16, nslab,
               [&](int e, uint32_t b) {
                 const uint32_t key = float_key<KB>(b);
-                return WE{(key == pth && cand(e, key)) ? 1.0f : 0.0f, 0.0f};
+                return (key == pth && cand(e, key)) ? 1.0f : 0.0f;
               },
               [&](double) { return nth; }, sh);
         }
@@ -682,18 +625,13 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
       return !p_found || key > pth ||
              (key == pth && (n_keep >= cnt_p || (n_keep > 0 && e <= cut_p)));
     };
-    // q weight with the element's exp(x/T - m) for the log-prob's S_other
-    auto qwe = [&](int e, uint32_t b) {
+    // q weight of a top-k candidate, floored; 0 outside the candidates
+    auto qw = [&](int e, uint32_t b) {
       const uint32_t key = float_key<KB>(b);
-      const float ev = ex(b);
-      WE r;
-      r.e = ev;
-      r.w = cand(e, key) ? fmaxf(kept(e, key) ? ev * inv_z : 0.0f, 1e-9f) : 0.0f;
-      return r;
+      return cand(e, key) ? fmaxf(kept(e, key) ? ex(b) * inv_z : 0.0f, 1e-9f) : 0.0f;
     };
 
-    // 5. inverse CDF with this row's uniform; the same sweep sums exp(x/T - m)
-    // over every column but the token (the log-prob's S_other).
+    // 5. inverse CDF with this row's uniform.
     uint32_t c[4] = {(uint32_t)r, (uint32_t)((uint64_t)r >> 32), (uint32_t)a.offset,
                      (uint32_t)(a.offset >> 32)};
     philox4x32_10(c, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
@@ -704,55 +642,35 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
       return u01 * total;
     };
     auto draw = [&](auto wfn, auto all_positive) {
-      tok = vocab_search<Tag, true, decltype(all_positive)::value>(row, V, al16, nslab, wfn,
-                                                                   target, sh);
+      tok = vocab_search<Tag, decltype(all_positive)::value>(row, V, al16, nslab, wfn, target,
+                                                             sh);
       const double qtot = sh_total;
-      have_other = sh.other_ok != 0;
-      s_other = sh.other;
       __syncthreads();
-      if (tok < 0 || tok >= V) {  // no positive weight: cannot happen, q >= 1e-9
-        tok = bi;
-        have_other = false;
-      }
-      if (tid == 0) logq = (float)(log((double)wfn(tok, load_one<Tag>(row, tok)).w) - log(qtot));
+      if (tok < 0 || tok >= V) tok = bi;  // no positive weight: cannot happen, q >= 1e-9
+      if (tid == 0) logq = (float)(log((double)wfn(tok, load_one<Tag>(row, tok))) - log(qtot));
     };
     if (!use_k && !p_found) {
       // The floored softmax itself: q = max(exp((x - max) / T) / Z, 1e-9) on
       // every entry, one hardware exponential per entry.
-      draw(
-          [&](int, uint32_t b) {
-            const float ev = exp2_hw((Bits<Tag>::val(b) - bx) * c2);
-            WE r;
-            r.e = ev;
-            r.w = fmaxf(ev * inv_z, 1e-9f);
-            return r;
-          },
-          std::true_type{});
+      draw([&](int, uint32_t b) { return fmaxf(exp2_hw((Bits<Tag>::val(b) - bx) * c2) * inv_z, 1e-9f); },
+           std::true_type{});
     } else {
-      draw(qwe, std::false_type{});
+      draw(qw, std::false_type{});
     }
+    // The token's S_other from pass 1: the sum without the maximum when the
+    // token is the argmax, else Z minus the token's own term.  S_other then
+    // holds the maximum's term 1 and e_tok <= 1, so the difference loses at
+    // most one bit.
+    if (tok != bi)
+      s_other = os - exp2_hw((Bits<Tag>::val(load_one<Tag>(row, tok)) - bx) * c2);
   }
 
   // 6. log_softmax(x / T) at the token, as the training row kernels form it:
   // finish_row of the maximum, the sum over the other columns and the
   // token's own value.
-  const float xt = Bits<Tag>::val(load_one<Tag>(row, tok)) * iT;
-  float mm = m, ss = s_other;
-  if (!have_other) {
-    mm = -__builtin_huge_valf();
-    ss = 0.0f;
-    for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
-      float v[VEC];
-#pragma unroll
-      for (int i = 0; i < VEC; ++i)
-        v[i] = (full || e0 + i < V) ? Bits<Tag>::val(u[i]) * iT : -__builtin_huge_valf();
-      const int rel = tok - e0;
-      online_update<float, VEC>(mm, ss, v, (rel >= 0 && rel < VEC) ? (int)rel : -1);
-    });
-    block_online_combine<SNT, float>(mm, ss, sh_m, sh_s);
-  }
   if (tid == 0) {
-    const RowLogprob<float> fr = finish_row<float>(mm, ss, xt);
+    const float xt = Bits<Tag>::val(load_one<Tag>(row, tok)) * iT;
+    const RowLogprob<float> fr = finish_row<float>(m, s_other, xt);
     a.token[r] = tok;
     a.logp[r] = fr.logp;
     if (a.logq) a.logq[r] = logq;
