@@ -212,6 +212,72 @@ struct SearchShared {
   int sel;
 };
 
+// Top-k candidates held in LDS, one per thread (top_k <= KCAP).
+constexpr int KCAP = SNT;
+
+struct CandShared {
+  int n;                          // entries gathered (may exceed KCAP: then unused)
+  int idx[KCAP];                  // vocabulary index: gathered, then dense candidates
+  uint32_t bits[KCAP];            // the entry as stored
+  int sidx[KCAP];                 // the gathered entries sorted by index
+  uint32_t sbits[KCAP];
+  unsigned long long mass[KCAP];  // top-p: fixed-point probability of candidate i
+  uint32_t key[KCAP];
+  int wave_cnt[SWAVES];
+  double wave_sum[SWAVES];
+  int found;                      // top-p threshold group
+  uint32_t pth;
+  unsigned long long A, M;
+  int C;
+  int pick;
+  float logq;
+};
+
+// Number of threads below this one (in thread order) whose flag is set, and
+// the total over the workgroup.
+__device__ __forceinline__ int block_excl_count(bool flag, int* wave_cnt, int& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const unsigned long long m = __ballot(flag);
+  const int below = __popcll(m & ((1ull << lane) - 1ull));
+  if (lane == 0) wave_cnt[wave] = __popcll(m);
+  __syncthreads();
+  int pre = 0, tot = 0;
+  for (int w = 0; w < SWAVES; ++w) {
+    const int c = wave_cnt[w];
+    pre += w < wave ? c : 0;
+    tot += c;
+  }
+  __syncthreads();
+  total = tot;
+  return pre + below;
+}
+
+// Inclusive and exclusive prefix sums of v in thread order and the total.  A
+// thread's exclusive value is exactly the previous thread's inclusive one
+// (the same operands in the same order), so the [excl, incl) ranges tile.
+__device__ __forceinline__ void block_scan_d(double v, double* wave_sum, double& incl,
+                                             double& excl, double& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  double in = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const double t = __shfl_up(in, o, 64);
+    if (lane >= o) in += t;
+  }
+  const double prev = __shfl_up(in, 1, 64);
+  if (lane == 63) wave_sum[wave] = in;
+  __syncthreads();
+  double pre = 0.0, tot = 0.0;  // one summation order in every thread
+  for (int w = 0; w < SWAVES; ++w) {
+    if (w == wave) pre = tot;
+    tot += wave_sum[w];
+  }
+  __syncthreads();
+  incl = pre + in;
+  excl = lane == 0 ? pre : pre + prev;
+  total = tot;
+}
+
 // Lowest-index maximum over the workgroup: (value, index) pairs, NaN never wins.
 __device__ __forceinline__ void argmax_merge(float& bx, int& bi, float ox, int oi) {
   if (ox > bx || (ox == bx && oi < bi)) {
@@ -351,6 +417,7 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   constexpr int VEC = Tag::VEC;
   constexpr int KB = Bits<Tag>::KB;
   __shared__ SearchShared sh;
+  __shared__ CandShared cs;
   __shared__ uint32_t hist[256];
   __shared__ unsigned long long histm[256];
   __shared__ float sh_s[2 * SWAVES];
@@ -456,6 +523,7 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
     uint32_t kth = 0;
     int need_k = 0, cnt_k = 0;
     int cut_k = -1;
+    bool listed = false;  // the top-k candidates sit in LDS (cs), in index order
     if (use_k) {
       uint32_t prefix = 0, pmask = 0;
       int kk = (int)a.top_k;
@@ -500,7 +568,27 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
       }
       kth = prefix;
       need_k = kk;  // 1 <= need_k <= cnt_k tokens at the threshold are kept
-      if (need_k < cnt_k) {
+      // Gather every entry at or above the k-th key (k - need_k + cnt_k of
+      // them) into LDS: the rest of the draw then never re-reads the row.
+      if (a.top_k <= KCAP) {
+        if (tid == 0) cs.n = 0;
+        __syncthreads();
+        for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            if ((full || e0 + i < V) && float_key<KB>(u[i]) >= kth) {
+              const int p = atomicAdd(&cs.n, 1);
+              if (p < KCAP) {
+                cs.idx[p] = e0 + i;
+                cs.bits[p] = u[i];
+              }
+            }
+          }
+        });
+        __syncthreads();
+        listed = cs.n <= KCAP;
+      }
+      if (!listed && need_k < cnt_k) {
         const double nth = (double)(need_k - 1);
         cut_k = vocab_search<Tag, false>(
             row, V, al16, nslab,
@@ -508,154 +596,255 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
             [&](double) { return nth; }, sh);
       }
     }
-    auto cand = [&](int e, uint32_t key) {
-      return !use_k || key > kth || (key == kth && (need_k >= cnt_k || e <= cut_k));
-    };
-
-    // 3. Z over the candidates (the whole row's online sum without top-k).
-    float zs = os;  // relative to the row maximum
-    if (use_k) {
-      zs = 0.0f;
-      for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) {
-          if ((full || e0 + i < V) && cand(e0 + i, float_key<KB>(u[i])))
-            zs += expf(Bits<Tag>::val(u[i]) * iT - m);
-        }
-      });
-      float v1[1] = {zs};
-      block_sum<SNT, 1, float>(v1, sh_s);
-      zs = v1[0];
-    }
-    const float inv_z = 1.0f / zs;
-    auto ex = [&](uint32_t b) {
-      float e = expf(Bits<Tag>::val(b) * iT - m);
-      asm volatile("" : "+v"(e));
-      return e;
-    };
-    auto prob = [&](uint32_t b) { return ex(b) * inv_z; };
-
-    // 4. top-p: radix select over fixed-point mass in descending key order.
     const bool use_p = a.top_p > 0.0 && a.top_p < 1.0;
-    bool p_found = false;
-    uint32_t pth = 0;
-    unsigned long long n_keep = 0, cnt_p = 0;
-    int cut_p = -1;
-    if (use_p) {
-      const unsigned long long P = (unsigned long long)(a.top_p * kMassScale);
-      uint32_t prefix = 0, pmask = 0;
-      unsigned long long A = 0;
-      p_found = true;
-      for (int shift = KB - 8; shift >= 0; shift -= 8) {
-        for (int i = tid; i < 256; i += SNT) {
-          hist[i] = 0;
-          histm[i] = 0;
-        }
-        if (tid == 0) sh_found = 0;
-        __syncthreads();
-        for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) {
-            const uint32_t key = float_key<KB>(u[i]);
-            if ((full || e0 + i < V) && (key & pmask) == prefix && cand(e0 + i, key)) {
-              const unsigned long long fx =
-                  (unsigned long long)((double)prob(u[i]) * kMassScale);
-              atomicAdd(&hist[(key >> shift) & 255u], 1u);
-              atomicAdd(&histm[(key >> shift) & 255u], fx);
-            }
-          }
-        });
-        __syncthreads();
-        if (wave == 0) {
-          unsigned long long c[4];
-          for (int b = 0; b < 4; ++b) c[b] = histm[4 * lane + b];
-          const unsigned long long t = c[0] + c[1] + c[2] + c[3];
-          unsigned long long incl = t;
-          for (int o = 1; o < 64; o <<= 1) {
-            const unsigned long long y = __shfl_down(incl, o, 64);
-            if (lane + o < 64) incl += y;
-          }
-          unsigned long long above = A + (incl - t);
-          for (int b = 3; b >= 0; --b) {
-            // the bin holding the first token whose inclusive mass passes P
-            if (c[b] > 0 && above <= P && P < above + c[b]) {
-              sh_digit = 4 * lane + b;
-              sh_above = above;
-              sh_found = 1;
-            }
-            above += c[b];
-          }
-        }
-        __syncthreads();
-        const bool f = sh_found != 0;
-        const uint32_t d = sh_digit;
-        const unsigned long long ab = sh_above;
-        const unsigned long long binm = histm[d], binc = hist[d];
-        __syncthreads();
-        if (!f) {  // every candidate fits under top_p
-          p_found = false;
-          break;
-        }
-        A = ab;
-        prefix |= d << shift;
-        pmask |= 255u << shift;
-        cnt_p = binc;
-        if (shift == 0) {
-          const unsigned long long each = binm / binc;  // equal keys, equal mass
-          n_keep = each > 0 ? (P - A) / each : binc;
-        }
-      }
-      if (p_found) {
-        pth = prefix;
-        // The first token in descending order (the row maximum) is always kept.
-        if (pth == float_key<KB>(load_one<Tag>(row, bi)) && n_keep == 0) n_keep = 1;
-        if (n_keep > 0 && n_keep < cnt_p) {
-          const double nth = (double)(n_keep - 1);
-          cut_p = vocab_search<Tag, false>(
-              row, V, al16, nslab,
-              [&](int e, uint32_t b) {
-                const uint32_t key = float_key<KB>(b);
-                return (key == pth && cand(e, key)) ? 1.0f : 0.0f;
-              },
-              [&](double) { return nth; }, sh);
-        }
-      }
-    }
-    auto kept = [&](int e, uint32_t key) {
-      return !p_found || key > pth ||
-             (key == pth && (n_keep >= cnt_p || (n_keep > 0 && e <= cut_p)));
-    };
-    // q weight of a top-k candidate, floored; 0 outside the candidates
-    auto qw = [&](int e, uint32_t b) {
-      const uint32_t key = float_key<KB>(b);
-      return cand(e, key) ? fmaxf(kept(e, key) ? ex(b) * inv_z : 0.0f, 1e-9f) : 0.0f;
-    };
-
-    // 5. inverse CDF with this row's uniform.
     uint32_t c[4] = {(uint32_t)r, (uint32_t)((uint64_t)r >> 32), (uint32_t)a.offset,
                      (uint32_t)(a.offset >> 32)};
     philox4x32_10(c, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
     const double u01 = (double)(c[0] >> 8) * 5.9604644775390625e-8;  // 2^-24
-    __shared__ double sh_total;
-    auto target = [&](double total) {
-      if (tid == 0) sh_total = total;
-      return u01 * total;
-    };
-    auto draw = [&](auto wfn, auto all_positive) {
-      tok = vocab_search<Tag, decltype(all_positive)::value>(row, V, al16, nslab, wfn, target,
-                                                             sh);
-      const double qtot = sh_total;
+
+    if (listed) {
+      // Top-k from the gathered entries, one per thread (n <= KCAP).
+      const int n = cs.n;
+      // Sort by vocabulary index: an entry's rank is the number of smaller
+      // indices.
+      if (tid < n) {
+        const int e = cs.idx[tid];
+        int rank = 0;
+        for (int j = 0; j < n; ++j) rank += cs.idx[j] < e ? 1 : 0;
+        cs.sidx[rank] = e;
+        cs.sbits[rank] = cs.bits[tid];
+      }
       __syncthreads();
-      if (tok < 0 || tok >= V) tok = bi;  // no positive weight: cannot happen, q >= 1e-9
-      if (tid == 0) logq = (float)(log((double)wfn(tok, load_one<Tag>(row, tok))) - log(qtot));
-    };
-    if (!use_k && !p_found) {
-      // The floored softmax itself: q = max(exp((x - max) / T) / Z, 1e-9) on
-      // every entry, one hardware exponential per entry.
-      draw([&](int, uint32_t b) { return fmaxf(exp2_hw((Bits<Tag>::val(b) - bx) * c2) * inv_z, 1e-9f); },
-           std::true_type{});
+      // The k candidates: every entry above the k-th key and the first need_k
+      // entries at it, lowest index first; relaid densely in index order.
+      const bool have = tid < n;
+      const int se = have ? cs.sidx[tid] : 0;
+      const uint32_t sb = have ? cs.sbits[tid] : 0u;
+      const bool tie = have && float_key<KB>(sb) == kth;
+      int ntie = 0;
+      const int tie_rank = block_excl_count(tie, cs.wave_cnt, ntie);
+      const bool is_cand = have && (!tie || tie_rank < need_k);
+      int kc = 0;
+      const int pos = block_excl_count(is_cand, cs.wave_cnt, kc);
+      if (is_cand) {
+        cs.idx[pos] = se;
+        cs.bits[pos] = sb;
+      }
+      __syncthreads();
+      const bool mine = tid < kc;
+      const uint32_t cb = mine ? cs.bits[tid] : 0u;
+      const uint32_t ck = float_key<KB>(cb);
+      // Z over the candidates, with the general path's exp(x/T - m).
+      const float ev = mine ? expf(Bits<Tag>::val(cb) * iT - m) : 0.0f;
+      float zt[1] = {ev};
+      block_sum<SNT, 1, float>(zt, sh_s);
+      const float pc = ev * (1.0f / zt[0]);
+      // Top-p over the candidates: the radix select's threshold group (first
+      // key, in descending order, whose inclusive fixed-point mass passes P),
+      // from exact integer sums over the list.
+      bool keep = true;
+      if (use_p) {
+        const unsigned long long P = (unsigned long long)(a.top_p * kMassScale);
+        cs.mass[tid] = mine ? (unsigned long long)((double)pc * kMassScale) : 0ull;
+        cs.key[tid] = ck;
+        if (tid == 0) cs.found = 0;
+        __syncthreads();
+        unsigned long long A = 0, M = 0;
+        int C = 0, tr = 0;
+        if (mine) {
+          for (int j = 0; j < kc; ++j) {
+            const uint32_t kj = cs.key[j];
+            const unsigned long long mj = cs.mass[j];
+            const bool same = kj == ck;
+            A += kj > ck ? mj : 0ull;
+            M += same ? mj : 0ull;
+            C += same ? 1 : 0;
+            tr += (same && j < tid) ? 1 : 0;
+          }
+          if (M > 0 && A <= P && P < A + M) {  // every member writes the same values
+            cs.found = 1;
+            cs.pth = ck;
+            cs.A = A;
+            cs.M = M;
+            cs.C = C;
+          }
+        }
+        __syncthreads();
+        if (cs.found) {
+          const uint32_t pth = cs.pth;
+          const unsigned long long A0 = cs.A, C0 = (unsigned long long)cs.C;
+          const unsigned long long each = cs.M / C0;  // equal keys, equal mass
+          unsigned long long n_keep = each > 0 ? (P - A0) / each : C0;
+          // The first token in descending order (the row maximum) is always kept.
+          if (pth == float_key<KB>(load_one<Tag>(row, bi)) && n_keep == 0) n_keep = 1;
+          keep = ck > pth ||
+                 (ck == pth && (n_keep >= C0 || (n_keep > 0 && (unsigned long long)tr < n_keep)));
+        }
+      }
+      // Inverse CDF over the candidates in vocabulary order.
+      const float wf = mine ? fmaxf(keep ? pc : 0.0f, 1e-9f) : 0.0f;
+      double incl, excl, tot;
+      block_scan_d((double)wf, cs.wave_sum, incl, excl, tot);
+      const double tgt = u01 * tot;
+      if (tid == 0) {
+        cs.pick = kc - 1;  // rounding past the last sum: the last candidate
+        cs.logq = 0.0f;
+      }
+      __syncthreads();
+      if (mine && excl <= tgt && tgt < incl) cs.pick = tid;
+      __syncthreads();
+      if (tid == cs.pick) cs.logq = (float)(log((double)wf) - log(tot));
+      __syncthreads();
+      tok = cs.idx[cs.pick];
+      logq = cs.logq;
     } else {
-      draw(qw, std::false_type{});
+      auto cand = [&](int e, uint32_t key) {
+        return !use_k || key > kth || (key == kth && (need_k >= cnt_k || e <= cut_k));
+      };
+
+      // 3. Z over the candidates (the whole row's online sum without top-k).
+      float zs = os;  // relative to the row maximum
+      if (use_k) {
+        zs = 0.0f;
+        for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            if ((full || e0 + i < V) && cand(e0 + i, float_key<KB>(u[i])))
+              zs += expf(Bits<Tag>::val(u[i]) * iT - m);
+          }
+        });
+        float v1[1] = {zs};
+        block_sum<SNT, 1, float>(v1, sh_s);
+        zs = v1[0];
+      }
+      const float inv_z = 1.0f / zs;
+      auto ex = [&](uint32_t b) {
+        float e = expf(Bits<Tag>::val(b) * iT - m);
+        asm volatile("" : "+v"(e));
+        return e;
+      };
+      auto prob = [&](uint32_t b) { return ex(b) * inv_z; };
+
+      // 4. top-p: radix select over fixed-point mass in descending key order.
+      bool p_found = false;
+      uint32_t pth = 0;
+      unsigned long long n_keep = 0, cnt_p = 0;
+      int cut_p = -1;
+      if (use_p) {
+        const unsigned long long P = (unsigned long long)(a.top_p * kMassScale);
+        uint32_t prefix = 0, pmask = 0;
+        unsigned long long A = 0;
+        p_found = true;
+        for (int shift = KB - 8; shift >= 0; shift -= 8) {
+          for (int i = tid; i < 256; i += SNT) {
+            hist[i] = 0;
+            histm[i] = 0;
+          }
+          if (tid == 0) sh_found = 0;
+          __syncthreads();
+          for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+              const uint32_t key = float_key<KB>(u[i]);
+              if ((full || e0 + i < V) && (key & pmask) == prefix && cand(e0 + i, key)) {
+                const unsigned long long fx =
+                    (unsigned long long)((double)prob(u[i]) * kMassScale);
+                atomicAdd(&hist[(key >> shift) & 255u], 1u);
+                atomicAdd(&histm[(key >> shift) & 255u], fx);
+              }
+            }
+          });
+          __syncthreads();
+          if (wave == 0) {
+            unsigned long long c[4];
+            for (int b = 0; b < 4; ++b) c[b] = histm[4 * lane + b];
+            const unsigned long long t = c[0] + c[1] + c[2] + c[3];
+            unsigned long long incl = t;
+            for (int o = 1; o < 64; o <<= 1) {
+              const unsigned long long y = __shfl_down(incl, o, 64);
+              if (lane + o < 64) incl += y;
+            }
+            unsigned long long above = A + (incl - t);
+            for (int b = 3; b >= 0; --b) {
+              // the bin holding the first token whose inclusive mass passes P
+              if (c[b] > 0 && above <= P && P < above + c[b]) {
+                sh_digit = 4 * lane + b;
+                sh_above = above;
+                sh_found = 1;
+              }
+              above += c[b];
+            }
+          }
+          __syncthreads();
+          const bool f = sh_found != 0;
+          const uint32_t d = sh_digit;
+          const unsigned long long ab = sh_above;
+          const unsigned long long binm = histm[d], binc = hist[d];
+          __syncthreads();
+          if (!f) {  // every candidate fits under top_p
+            p_found = false;
+            break;
+          }
+          A = ab;
+          prefix |= d << shift;
+          pmask |= 255u << shift;
+          cnt_p = binc;
+          if (shift == 0) {
+            const unsigned long long each = binm / binc;  // equal keys, equal mass
+            n_keep = each > 0 ? (P - A) / each : binc;
+          }
+        }
+        if (p_found) {
+          pth = prefix;
+          // The first token in descending order (the row maximum) is always kept.
+          if (pth == float_key<KB>(load_one<Tag>(row, bi)) && n_keep == 0) n_keep = 1;
+          if (n_keep > 0 && n_keep < cnt_p) {
+            const double nth = (double)(n_keep - 1);
+            cut_p = vocab_search<Tag, false>(
+                row, V, al16, nslab,
+                [&](int e, uint32_t b) {
+                  const uint32_t key = float_key<KB>(b);
+                  return (key == pth && cand(e, key)) ? 1.0f : 0.0f;
+                },
+                [&](double) { return nth; }, sh);
+          }
+        }
+      }
+      auto kept = [&](int e, uint32_t key) {
+        return !p_found || key > pth ||
+               (key == pth && (n_keep >= cnt_p || (n_keep > 0 && e <= cut_p)));
+      };
+      // q weight of a top-k candidate, floored; 0 outside the candidates
+      auto qw = [&](int e, uint32_t b) {
+        const uint32_t key = float_key<KB>(b);
+        return cand(e, key) ? fmaxf(kept(e, key) ? ex(b) * inv_z : 0.0f, 1e-9f) : 0.0f;
+      };
+
+      // 5. inverse CDF with this row's uniform.
+      __shared__ double sh_total;
+      auto target = [&](double total) {
+        if (tid == 0) sh_total = total;
+        return u01 * total;
+      };
+      auto draw = [&](auto wfn, auto all_positive) {
+        tok = vocab_search<Tag, decltype(all_positive)::value>(row, V, al16, nslab, wfn, target,
+                                                               sh);
+        const double qtot = sh_total;
+        __syncthreads();
+        if (tok < 0 || tok >= V) tok = bi;  // no positive weight: cannot happen, q >= 1e-9
+        if (tid == 0) logq = (float)(log((double)wfn(tok, load_one<Tag>(row, tok))) - log(qtot));
+      };
+      if (!use_k && !p_found) {
+        // The floored softmax itself: q = max(exp((x - max) / T) / Z, 1e-9) on
+        // every entry, one hardware exponential per entry.
+        draw(
+            [&](int, uint32_t b) {
+              return fmaxf(exp2_hw((Bits<Tag>::val(b) - bx) * c2) * inv_z, 1e-9f);
+            },
+            std::true_type{});
+      } else {
+        draw(qw, std::false_type{});
+      }
     }
     // The token's S_other from pass 1: the sum without the maximum when the
     // token is the argmax, else Z minus the token's own term.  S_other then
