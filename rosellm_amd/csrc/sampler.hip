@@ -23,7 +23,9 @@
 //   6. the token's log-prob in the form the training row kernels use
 //      (finish_row), from pass 1's sums.
 // Greedy decoding is pass 1 alone; sampling without top-k / top-p is passes 1
-// and 5.
+// and 5.  With top-k (k <= 1024), one pass after step 2 gathers the entries
+// at or above the k-th key into LDS and steps 3-5 run on that list, one
+// candidate per thread, without re-reading the row.
 // Ties at a top-k or top-p threshold are kept lowest index first; they are
 // located with the same vocabulary-order search over 0/1 weights.
 #include "row_common.hpp"
