@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Throughput of the RoseRLHF GRPO training-step hot path on one MI355X.
 
-Workload: 32 prompts x group 8 = 256 sequences x 1024
+Workload (config 2, the headline): 32 prompts x group 8 = 256 sequences x 1024
 tokens, vocabulary 151936, bf16 logits ~ N(0, 3) with 5% of rows given one
 dominant logit (+15).  Actions are sampled from softmax(logits) (Gumbel-max,
 exact), old_logprobs = logprobs + N(0, 0.1), rewards uniform {0, 1} per
@@ -507,7 +507,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the path "
-              "shards by whole GRPO groups with one scalar all-reduce (see DESIGN.md), which "
+              "shards by whole GRPO groups with one scalar all-reduce per step, which "
               "is not run here.", file=sys.stderr)
         sys.exit(2)
     if args.steps is None:

@@ -5,7 +5,7 @@
  * The reference (rosellm.roserlhf) is pure PyTorch and has no native layer; each
  * entry point below replaces the ATen op sequence of one reference function,
  * cited as file:line into rosellm/roserlhf/.  Python (rosellm_amd/_native.py)
- * binds these with ctypes; INTEGRATION.md shows the binding.
+ * binds these with ctypes.
  *
  * Conventions shared by every entry point:
  *   - Every pointer is a device pointer unless named *_host.  All outputs and

@@ -1,4 +1,4 @@
-"""The hot path at BASELINE.json's full sizes (configs 2, 3 and 4), checked
+"""The hot path at the benchmark configs' full sizes (configs 2, 3 and 4), checked
 through what does not depend on size:
 
 * a random sample of token rows against the float64 oracle (log-probs, and
