@@ -1,5 +1,6 @@
-"""The hot path at the benchmark configs' full sizes (configs 2, 3 and 4), checked
-through what does not depend on size:
+"""The hot path at the benchmark configs' full sizes (configs 2, 3 and 4; config
+1 compared with the oracle on every row), checked through what does not depend
+on size:
 
 * a random sample of token rows against the float64 oracle (log-probs, and
   dlogits rebuilt from the oracle's d loss / d logp over the whole batch);
@@ -100,6 +101,43 @@ def _oracle_g(kind, lp, old, adv, mask, **kw):
     out = fn(cur, old.double().cpu(), adv.double().cpu(), mask.cpu(), **kw)
     out["loss"].backward()
     return out, cur.grad.reshape(-1)
+
+
+def test_config1_fullsize_every_row(device):
+    """Config 1 in full (32 x 128 rows of 50257 float32 logits, rows 4-byte
+    aligned: the register-resident kernel's head/tail variant) against the
+    float64 oracle on every row, for the fused path and for the composed
+    path (gather_token_logprobs, clipped_policy_loss, autograd)."""
+
+    print("[fullsize] config 1 every row", flush=True)
+    cfg = bench.CONFIGS["c1"]
+    with torch.no_grad():
+        inp = bench.make_inputs(cfg, device, 1234)
+    B, T, V = inp["B"], inp["T"], inp["V"]
+    x, t, old, mask = inp["logits"], inp["actions"], inp["old"], inp["mask"]
+    adv = R.group_standardized_advantages(inp["rewards"]).reshape(-1)[:, None].expand(B, T)
+    kw = cfg["kw"]
+    xc, tc, oc, ac, mc = (v.detach().cpu() for v in (x, t, old, adv, mask))
+    out_o, lpo, dlo = o.policy_step("ppo", xc, tc, oc, ac.contiguous(), mc, exact=True, **kw)
+    g = out_o["dloss_dlogp"]
+    scale = max(abs(float(out_o["loss"])), float(ac.abs().mean()))
+    for path in ("fused", "composed"):
+        xd = x.detach().clone().requires_grad_()
+        if path == "fused":
+            out, lp = R.fused_policy_loss(xd, t, old, adv, mask, return_logprobs=True, **kw)
+        else:
+            lp = R.gather_token_logprobs(xd, t)
+            out = R.clipped_policy_loss(lp, old, adv, mask, **kw)
+        out.loss.backward()
+        err = (lp.detach().double().cpu() - lpo).abs()
+        assert bool((err <= 1e-5 * lpo.abs() + 1e-7).all()), (path, float(err.max()))
+        assert abs(float(out.loss) - float(out_o["loss"])) <= 1e-5 * scale, path
+        e = (xd.grad.double().cpu() - dlo).abs().reshape(-1, V).max(dim=-1).values
+        bound = 1e-5 * g.reshape(-1).abs() + 1e-12
+        assert bool((e <= bound).all()), (path, float((e / bound).max()))
+        del xd
+    del x, inp
+    _free()
 
 
 def test_config2_grpo_fullsize(device):
