@@ -47,8 +47,9 @@ def _dominant(x, g, frac=0.05, bump=15.0):
 
 
 @pytest.mark.parametrize("reduction", ["mean", "sum"])
-def test_cross_entropy_f32_generic_rows(device, reduction):
-    """float32 [N, V] with V = 50257 (rows not 16-byte aligned: generic kernel)."""
+def test_cross_entropy_f32_unaligned_rows(device, reduction):
+    """float32 [N, V] with V = 50257: rows not 16-byte aligned, the
+    register-resident kernel's head/tail variant."""
 
     print(f"[sft-f32] reduction={reduction}", flush=True)
     g = _gen(101)
@@ -72,7 +73,7 @@ def test_cross_entropy_f32_generic_rows(device, reduction):
                                      (torch.bfloat16, 32001)])
 def test_causal_lm_loss_16bit(device, dtype, V):
     """[B, T, V] causal shift through strided views; V % 8 == 0 takes the
-    register-resident kernel, V = 32001 the generic one."""
+    register-resident kernel's plain variant, V = 32001 its head/tail variant."""
 
     print(f"[sft-causal] dtype={dtype} V={V}", flush=True)
     g = _gen(102)
