@@ -1,5 +1,6 @@
 """The hot path at the benchmark configs' full sizes (configs 2, 3 and 4; config
-1 compared with the oracle on every row), checked through what does not depend
+1 compared with the oracle on every row; config 5's fused LM head against the
+logits-level path on the same inputs), checked through what does not depend
 on size:
 
 * a random sample of token rows against the float64 oracle (log-probs, and
@@ -248,4 +249,63 @@ def test_config4_gae_sapo_inplace_fullsize(device):
     _row_sums_vanish(dl, "c4")
     _masked_rows_zero(dl, mask, "c4")
     del xd, x, dl, out, inp
+    _free()
+
+
+def _rows_close(a, b, tol, what, chunk=16384):
+    """Row-wise ||a - b|| <= tol * ||b|| (rows of the last dimension)."""
+
+    fa, fb = a.reshape(-1, a.shape[-1]), b.reshape(-1, b.shape[-1])
+    worst = 0.0
+    for r0 in range(0, fa.shape[0], chunk):
+        x, y = fa[r0:r0 + chunk].float(), fb[r0:r0 + chunk].float()
+        num, den = (x - y).norm(dim=-1), y.norm(dim=-1)
+        worst = max(worst, float(torch.where(den > 0, num / den.clamp_min(1e-30), num).max()))
+    assert worst <= tol, f"{what}: worst row-norm rel diff {worst:.3e}"
+    return worst
+
+
+def test_config5_linear_fullsize_matches_logits_path(device):
+    """Config 5 in full (262144 tokens, hidden 1024, V = 151936 bf16): the
+    fused LM-head path (16384-token row blocks between the GEMMs, float32 dW
+    accumulation) against the logits-level path on the same inputs
+    (F.linear, fused_policy_loss in place, autograd through F.linear).  Loss
+    within 1e-5 of its scale; d hidden and d weight row by row within 1e-2
+    norm-wise (both carry bf16 products; the logits-level dW is one K = 262144
+    product, the fused one 16 accumulated blocks)."""
+
+    import torch.nn.functional as F
+
+    print("[fullsize] config 5 fused LM head vs logits path", flush=True)
+    cfg = bench.CONFIGS["c5"]
+    with torch.no_grad():
+        inp = bench.make_inputs(cfg, device, 1234)
+    B, T = inp["B"], inp["T"]
+    h, w = inp["hidden"], inp["weight"]
+    t, old, mask = inp["actions"], inp["old"], inp["mask"]
+    adv = R.group_standardized_advantages(inp["rewards"]).reshape(-1)[:, None].expand(B, T)
+    kw = cfg["kw"]
+    del inp
+    _free()
+    h1, w1 = h.detach().clone().requires_grad_(), w.detach().clone().requires_grad_()
+    out1 = R.fused_linear_policy_loss(h1, w1, t, old, adv, mask,
+                                      row_block=bench.LM_HEAD_ROW_BLOCK, **kw)
+    out1.loss.backward()
+    gh1, gw1, loss1 = h1.grad, w1.grad, float(out1.loss)
+    del out1, h1, w1
+    _free()
+    h2, w2 = h.detach().clone().requires_grad_(), w.detach().clone().requires_grad_()
+    logits = F.linear(h2, w2)
+    out2 = R.fused_policy_loss(logits, t, old, adv, mask, inplace=True, **kw)
+    out2.loss.backward()
+    loss2 = float(out2.loss)
+    del out2, logits
+    _free()
+    scale = max(abs(loss2), float(adv.abs().mean()))
+    assert abs(loss1 - loss2) <= 1e-5 * scale, (loss1, loss2)
+    dh = _rows_close(gh1, h2.grad, 1e-2, "d hidden")
+    dw = _rows_close(gw1, w2.grad, 1e-2, "d weight")
+    print(f"[fullsize] c5: loss {loss1:.6g} vs {loss2:.6g}; d hidden {dh:.2e}, d weight {dw:.2e}",
+          flush=True)
+    del gh1, gw1, h2, w2, h, w
     _free()
