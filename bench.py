@@ -98,8 +98,11 @@ def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None,
-                   help="timed steps (default 10; 200 for config c1, whose step is under 1 ms)")
-    p.add_argument("--warmup", type=int, default=2)
+                   help="timed steps (default 10; 200 for c1 and the sampler, whose steps "
+                        "are under 1 ms)")
+    p.add_argument("--warmup", type=int, default=None,
+                   help="untimed steps first (default 2; 20 for c1 and the sampler, whose "
+                        "host-bound steps settle over more calls)")
     p.add_argument("--config", choices=sorted(CONFIGS) + ["sample"], default="c2")
     p.add_argument("--path", choices=["fused", "composed"], default="fused")
     p.add_argument("--objective", choices=["gspo", "gspo_token"], default=None,
@@ -415,6 +418,31 @@ def traffic_from_profiles(kernel_key, workload_key):
         return None
 
 
+def timed_steps(step, steps, kernels):
+    """Time `steps` calls of `step` by the wall clock, bracketed by device
+    synchronisations, then run as many again with HIP events recorded around
+    every launch of `kernels` (on the stream each is launched on).  Returns
+    (seconds of the first loop, its last output, {kernel: [(start, end)]}):
+    the events never sit inside the wall-clock loop."""
+
+    import torch
+
+    from rosellm_amd import _native as nat
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timed = nat.time_calls(*kernels, capacity=steps * 32)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    nat.time_calls()
+    return elapsed, out, timed
+
+
 SAMPLE_ROWS = 256
 SAMPLE_VARIANTS = {"default": dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=True),
                    "topk50_topp0.9_T0.7": dict(temperature=0.7, top_k=50, top_p=0.9,
@@ -444,14 +472,10 @@ def bench_sample(args):
     for name, kw in SAMPLE_VARIANTS.items():
         for i in range(args.warmup):
             sample_next_token_batch(x, seed=args.seed, offset=i, **kw)
-        torch.cuda.synchronize()
-        timed = nat.time_calls("rrl_sample_logprobs", capacity=args.steps)
-        t0 = time.perf_counter()
-        for i in range(args.steps):
-            out = sample_next_token_batch(x, seed=args.seed, offset=100 + i, **kw)
-        torch.cuda.synchronize()
-        el = time.perf_counter() - t0
-        nat.time_calls()
+        offs = iter(range(100, 100 + 2 * args.steps))
+        el, out, timed = timed_steps(
+            lambda: sample_next_token_batch(x, seed=args.seed, offset=next(offs), **kw),
+            args.steps, ["rrl_sample_logprobs"])
         kms = [s.elapsed_time(e) for s, e in timed["rrl_sample_logprobs"]]
         results[name] = dict(ms=el * 1e3 / args.steps, kernel_ms=sum(kms) / len(kms),
                              tokens=out.token_ids)
@@ -511,7 +535,9 @@ def main():
               "is not run here.", file=sys.stderr)
         sys.exit(2)
     if args.steps is None:
-        args.steps = 200 if args.config == "c1" else 10
+        args.steps = 200 if args.config in ("c1", "sample") else 10
+    if args.warmup is None:
+        args.warmup = 20 if args.config in ("c1", "sample") else 2
     if args.config == "sample":
         bench_sample(args)
         return
@@ -549,14 +575,7 @@ def main():
 
     kernels = (["rrl_fused_logprob_policy"] if path == "fused"
                else ["rrl_logprob_fwd", "rrl_logprob_bwd"])
-    timed = nat.time_calls(*kernels, capacity=args.steps * 32)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        out = step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    nat.time_calls()
+    elapsed, out, timed = timed_steps(step, args.steps, kernels)
     ms_step = elapsed * 1e3 / args.steps
     tok_s = N / (elapsed / args.steps)
     in_b = (inp["hidden"] if cfg.get("lm_head") else inp["logits"]).element_size()
@@ -652,14 +671,7 @@ def main():
 
         for _ in range(args.warmup):
             vstep()
-        vt = nat.time_calls(kernels[0], capacity=args.steps * 32)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            vout = vstep()
-        torch.cuda.synchronize()
-        v_el = time.perf_counter() - t0
-        nat.time_calls()
+        v_el, vout, vt = timed_steps(vstep, args.steps, kernels[:1])
         v_ms = [s.elapsed_time(e) for s, e in vt[kernels[0]]]
         return v_el, sum(v_ms) / len(v_ms), vout
 

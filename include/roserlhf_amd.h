@@ -306,8 +306,11 @@ RRL_API int rrl_masked_whiten(int64_t B, int64_t T, rrl_view x, rrl_view mask, d
  * log_softmax(x / T) over the whole row, T = 1 when greedy, formed as the
  * training kernels form log-probs; logq_out (float32, may be NULL) log(q/sum q),
  * the log-probability of the sampling distribution (0 when greedy).
- * status gets BAD_PROBS.  The arithmetic is float32 on the exact upcast of
- * the logits (the reference divides and normalises in the logits dtype). */
+ * A row with NaN or +inf logits, no finite maximum, or a maximum whose x/T
+ * overflows raises BAD_PROBS in *status (status may be NULL) and gets
+ * logp_out = logq_out = NaN; every other row's logp_out is not NaN.  The
+ * arithmetic is float32 on the exact upcast of the logits (the reference
+ * divides and normalises in the logits dtype). */
 RRL_API int rrl_sample_logprobs(const void* logits, int32_t logits_dtype, int64_t B, int64_t V,
                         int64_t row_stride, double temperature, int64_t top_k, double top_p,
                         int32_t do_sample, uint64_t seed, uint64_t offset, int64_t* token_out,

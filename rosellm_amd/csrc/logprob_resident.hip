@@ -27,27 +27,13 @@
 
 #include "policy_math.hpp"
 #include "row_common.hpp"
+#include "wave_common.hpp"
 
 namespace rrl {
 
 namespace {
 
 constexpr int RNT = 1024;                 // lanes per workgroup (16 waves)
-constexpr float kLog2e = 1.4426950408889634f;
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Buffer resource over `bytes` bytes at `base`.  The last dword selects a
-// non-zero 32-bit data format, which enables raw (untyped) accesses; stride 0
-// makes num_records a byte count checked against each access's offset.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                           0x00020000);
-}
-
-// Cache-policy bits of a buffer access on gfx950: bit 1 = non-temporal.
-constexpr int kAuxLoad = 0;
-constexpr int kAuxStoreNT = 2;
 
 // Element access of one 16-byte vector per tag: EPV elements, their float
 // values, the packed form written back (round to nearest even for 16-bit),
@@ -173,8 +159,6 @@ __device__ __forceinline__ int32_t extra_index(const RowGeo& g, int tid) {
   return -1;
 }
 
-__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
-
 // Per-token records for the resident kernel (TokenRecord): the views' dtype
 // and stride handling happens here, once per token, so that the row loop reads
 // its scalars with one uniform 16-byte load.
@@ -222,36 +206,6 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-}
-
-// Butterfly steps inside a row of 16 lanes: DPP quad_perm [1,0,3,2] and
-// [2,3,0,1] exchange with lanes i^1 and i^2; once quads agree, the half-row
-// and row mirrors pair each half with the other (i^4, i^8 for a reduction).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
-
-__device__ __forceinline__ float lane_read(float v, int l) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-
-// Wave64 max / sum, the same value in every lane: DPP within rows of 16,
-// then the four row results through readlane (scalar operands).
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  v = fmaxf(v, dpp_f<kDppXor1>(v));
-  v = fmaxf(v, dpp_f<kDppXor2>(v));
-  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
-  v = fmaxf(v, dpp_f<kDppMirror>(v));
-  return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)), fmaxf(lane_read(v, 32), lane_read(v, 48)));
-}
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v += dpp_f<kDppXor1>(v);
-  v += dpp_f<kDppXor2>(v);
-  v += dpp_f<kDppHalfMirror>(v);
-  v += dpp_f<kDppMirror>(v);
-  return (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
 }
 
 // s * exp(m - M) for the combine: exact s when m == M (also for M = -inf or

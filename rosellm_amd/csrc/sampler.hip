@@ -29,6 +29,7 @@
 // Ties at a top-k or top-p threshold are kept lowest index first; they are
 // located with the same vocabulary-order search over 0/1 weights.
 #include "row_common.hpp"
+#include "wave_common.hpp"
 
 #include <type_traits>
 
@@ -59,10 +60,6 @@ constexpr int SNT = 1024;
 constexpr int SWAVES = SNT / 64;
 constexpr int MAX_SLABS = 64;
 constexpr double kMassScale = 4503599627370496.0;  // 2^52: fixed-point probability
-constexpr float kLog2e = 1.4426950408889634f;
-
-// 2^x with the hardware exponential (v_exp_f32): exp(y / T) = 2^(y * log2(e) / T).
-__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 struct SampleArgs {
   const void* logits;
@@ -88,14 +85,17 @@ __device__ __forceinline__ uint32_t float_key(uint32_t b) {
 
 template <class Tag> struct Bits;
 template <> struct Bits<TagBF16> {
+  static constexpr uint32_t NEG_INF = 0xFF80FF80u;  // -inf in every element of a dword
   static constexpr int KB = 16;
   static __device__ __forceinline__ float val(uint32_t u) { return __uint_as_float(u << 16); }
 };
 template <> struct Bits<TagF16> {
+  static constexpr uint32_t NEG_INF = 0xFC00FC00u;  // -inf in every element of a dword
   static constexpr int KB = 16;
   static __device__ __forceinline__ float val(uint32_t u) { return f16_bits_to_f32((uint16_t)u); }
 };
 template <> struct Bits<TagF32> {
+  static constexpr uint32_t NEG_INF = 0xFF800000u;  // -inf in every element of a dword
   static constexpr int KB = 32;
   static __device__ __forceinline__ float val(uint32_t u) { return __uint_as_float(u); }
 };
@@ -504,7 +504,7 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   block_sum<SNT, 2, float>(tot, sh_s);
   const float os = tot[0], s_arg_other = tot[1];
   const bool row_bad = bx == -__builtin_huge_valf() || bi >= V || os != os ||
-                       bx * iT == __builtin_huge_valf();
+                       __builtin_fabsf(bx * iT) == __builtin_huge_valf();
   if (row_bad) {
     if (tid == 0) {
       raise_flag(a.status, RRL_FLAG_BAD_PROBS);
@@ -874,6 +874,305 @@ int launch_sample(const SampleArgs& a, hipStream_t st) {
   return check_launch("sample_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// Register-resident rows: sampling without top-k / top-p, and greedy
+// decoding, of 16-bit rows made of whole 16-byte vectors (V % 8 == 0, rows
+// 16-byte aligned, V <= 8 * 1024 * RES_MAX_SLABS).  Lane j holds vector
+// k*1024 + j of its row in four VGPRs per slab k (the sample_kernel layout),
+// so the row is read from memory once:
+//   A. as the slab loads land: the lane's first maximum (value and slab) and
+//      its online sum of exp((x - max) / T); one LDS exchange gives the row
+//      maximum, Z and the lowest-index argmax;
+//   B. (sampling) each lane's float sum of the floored softmax weights per
+//      slab into LDS, float64 slab totals, the slab holding u * total, a
+//      prefix scan of that slab's lane sums and the claiming lane's own
+//      entries: the search and tiling rule of vocab_search;
+//   C. the sampled token's S_other: for the argmax, the sum over every other
+//      entry relative to the row maximum, formed by the argmax lane's wave
+//      (the other lanes' sweep-A sums, the argmax lane's entries shared out
+//      over the wave through LDS); no subtraction, so the log-prob of a
+//      dominant token keeps its relative precision.  Any other token: Z - e_tok.
+constexpr int RES_MAX_SLABS = 20;  // V <= 163840
+
+template <class Tag>
+__device__ __forceinline__ void unpack8(const u32x4& u, float (&v)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = Bits<Tag>::val(w[i] & 0xffffu);
+    v[2 * i + 1] = Bits<Tag>::val(w[i] >> 16);
+  }
+}
+
+// IEEE maximum (v_maximum3_f32): NaN propagates, so the raw loaded values need
+// no quieting first; a NaN row is flagged through its sum either way.
+__device__ __forceinline__ float mx(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float max8(const float (&v)[8]) {
+  return mx(mx(mx(v[0], v[1]), mx(v[2], v[3])), mx(mx(v[4], v[5]), mx(v[6], v[7])));
+}
+__device__ __forceinline__ float sum8(const float (&e)[8]) {
+  return ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+}
+
+// The defaults' floored softmax weight max(2^((x - max) * c2) / Z, 1e-9),
+// rounded the same way wherever it is evaluated.
+__device__ __forceinline__ float floored_weight(float x, float M, float c2, float inv_z) {
+  float w = fmaxf(exp2_hw((x - M) * c2) * inv_z, 1e-9f);
+  asm volatile("" : "+v"(w));
+  return w;
+}
+
+template <class Tag, int SL>
+__global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
+  static_assert(Tag::VEC == 8, "16-bit rows");
+  __shared__ float part[SL][SNT];  // sweep B: lane sums of the weights per slab
+  __shared__ double slab_tot[SL];
+  __shared__ double scan_ws[SWAVES];
+  __shared__ float sh_m[SWAVES], sh_s[SWAVES];
+  __shared__ int sh_i[SWAVES];
+  __shared__ int sh_sel;
+  __shared__ float sh_w, sh_x;
+  __shared__ u32x4 arg_row[SL];  // the argmax lane's registers (sweep C)
+
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int V = (int)a.V;
+  const int nvec = V >> 3;
+  const int nslab = (nvec + SNT - 1) / SNT;
+  const int nfull = nvec / SNT;  // slabs whose every lane lies inside the row
+  const float NEG = -__builtin_huge_valf();
+  const typename Tag::S* row = static_cast<const typename Tag::S*>(a.logits) + (int64_t)r * a.stride;
+  const __amdgpu_buffer_rsrc_t src = row_rsrc(row, (uint32_t)V * 2u);
+  u32x4 x[SL];
+#pragma unroll
+  for (int k = 0; k < SL; ++k)
+    x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, tid * 16, k * SNT * 16, kAuxLoad);
+
+  const float iT = 1.0f / a.temp;
+  const float c2 = iT * kLog2e;  // exp(y / T) = 2^(y * c2)
+
+  // A. The lane's first maximum, the slab it lies in, and the sum of
+  // exp((x - max) / T) over the lane's entries, slab by slab as they land.
+  // fmaxf skips NaN; NaN and +inf reach the sum and flag the row.
+  float lm = NEG, ls = 0.0f;
+  int lk = 0;
+#pragma unroll
+  for (int k = 0; k < SL; ++k) {
+    if (k < nslab) {
+      if (k >= nfull) {
+        // The row's last, partial slab: lanes past the end read zeros and
+        // hold -inf from here on (the empty asm keeps this a branch rather
+        // than a select in every slab).
+        asm volatile("");
+        if (k * SNT + tid >= nvec) x[k] = u32x4{Bits<Tag>::NEG_INF, Bits<Tag>::NEG_INF,
+                                                Bits<Tag>::NEG_INF, Bits<Tag>::NEG_INF};
+      }
+      float v[8];
+      unpack8<Tag>(x[k], v);
+      const float mc = max8(v);
+      lk = mc > lm ? k : lk;
+      const float mn = fmaxf(lm, mc);
+      const float mg = fmaxf(mn, -__FLT_MAX__);
+      float e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = exp2_hw((v[i] - mg) * c2);
+      ls = __builtin_fmaf(ls, exp2_hw((lm - mg) * c2), sum8(e));
+      lm = mn;
+    }
+  }
+  // Per wave: maximum, sum relative to it, and the lowest index holding it
+  // (found in the one slab where each such lane first met its maximum).
+  const float wm = wave_max_dpp(lm);
+  const float ws = wave_sum_dpp(ls * exp2_hw((lm - fmaxf(wm, -__FLT_MAX__)) * c2));
+  int ci = 0x7fffffff;
+  if (lm == wm && wm > NEG) {
+#pragma unroll
+    for (int k = 0; k < SL; ++k) {
+      if (k == lk) {
+        float v[8];
+        unpack8<Tag>(x[k], v);
+        int ic = 7;
+#pragma unroll
+        for (int i = 6; i >= 0; --i) ic = v[i] == wm ? i : ic;
+        ci = (k * SNT + tid) * 8 + ic;
+      }
+    }
+  }
+  const int wi = wave_min_dpp(ci);
+  if (lane == 0) {
+    sh_m[wave] = wm;
+    sh_s[wave] = ws;
+    sh_i[wave] = wi;
+  }
+  __syncthreads();
+  float M = sh_m[0];
+  for (int w = 1; w < SWAVES; ++w) M = fmaxf(M, sh_m[w]);
+  const float Mg = fmaxf(M, -__FLT_MAX__);
+  float Z = 0.0f;
+  int bi = 0x7fffffff;
+  for (int w = 0; w < SWAVES; ++w) {
+    Z += sh_s[w] * exp2_hw((sh_m[w] - Mg) * c2);
+    bi = sh_m[w] == M ? min(bi, sh_i[w]) : bi;
+  }
+  if (M == NEG || Z != Z || __builtin_fabsf(M * iT) == __builtin_huge_valf() || bi >= V) {
+    if (tid == 0) {
+      raise_flag(a.status, RRL_FLAG_BAD_PROBS);
+      a.token[r] = bi < V ? bi : 0;
+      a.logp[r] = __builtin_nanf("");
+      if (a.logq) a.logq[r] = __builtin_nanf("");
+    }
+    return;
+  }
+
+  int tok = bi;
+  float logq = 0.0f;
+  float xt_raw = M;  // the token's logit
+  if (!a.greedy) {
+    // B. Inverse CDF of the floored softmax in vocabulary order.
+    const float inv_z = 1.0f / Z;
+#pragma unroll
+    for (int k = 0; k < SL; ++k) {
+      if (k < nslab) {
+        float v[8];
+        unpack8<Tag>(x[k], v);
+        float w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = floored_weight(v[i], M, c2, inv_z);
+        float f = sum8(w);
+        if (k >= nfull) {
+          asm volatile("");
+          if (k * SNT + tid >= nvec) f = 0.0f;  // -inf entries past the end weigh nothing
+        }
+        part[k][tid] = f;
+      }
+    }
+    __syncthreads();
+    for (int k = wave; k < nslab; k += SWAVES) {
+      double s = 0.0;
+#pragma unroll
+      for (int j = 0; j < SNT / 64; ++j) s += (double)part[k][lane + 64 * j];
+      s = wave_sum_d(s);
+      if (lane == 0) slab_tot[k] = s;
+    }
+    __syncthreads();
+    double total = 0.0;
+    for (int k = 0; k < nslab; ++k) total += slab_tot[k];
+    uint32_t c[4] = {(uint32_t)r, 0u, (uint32_t)a.offset, (uint32_t)(a.offset >> 32)};
+    philox4x32_10(c, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
+    const double u01 = (double)(c[0] >> 8) * 5.9604644775390625e-8;  // 2^-24
+    const double target = u01 * total;
+    int ks = -1;
+    double run = 0.0;
+    for (int k = 0; k < nslab; ++k) {
+      const double t = slab_tot[k];
+      if (run + t > target) {
+        ks = k;
+        break;
+      }
+      run += t;
+    }
+    if (ks < 0) {  // rounding left the target past the end: the last slab
+      ks = nslab - 1;
+      run -= slab_tot[ks];
+    }
+    if (tid == 0) sh_sel = -1;
+    const double lw = (double)part[ks][tid];
+    double incl, excl, scan_total;
+    block_scan_d(lw, scan_ws, incl, excl, scan_total);
+    const double lexcl = run + excl, lincl = run + incl;
+    // [lexcl, lincl) of consecutive lanes tile the slab from `run`; the last
+    // lane inside the row takes what rounding leaves past the end.
+    const int last_lane = min(nvec - ks * SNT, SNT) - 1;
+    if (lw > 0.0 && lexcl <= target && (target < lincl || tid == last_lane)) {
+      u32x4 xv = x[0];
+#pragma unroll
+      for (int k = 1; k < SL; ++k) xv = k == ks ? x[k] : xv;
+      float v[8];
+      unpack8<Tag>(xv, v);
+      double cum = lexcl;
+      int pick = -1;
+      float wp = 0.0f, xp = v[7];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float w = floored_weight(v[i], M, c2, inv_z);
+        if (pick < 0 && (cum + (double)w > target || i == 7)) {
+          pick = i;
+          wp = w;
+          xp = v[i];
+        }
+        cum += (double)w;
+      }
+      sh_sel = (ks * SNT + tid) * 8 + pick;
+      sh_w = wp;
+      sh_x = xp;
+    }
+    __syncthreads();
+    const int sel = sh_sel;
+    if (sel >= 0) {
+      tok = sel;
+      xt_raw = sh_x;
+      logq = (float)(log((double)sh_w) - log(total));
+    } else {  // no lane claimed (not reached): the argmax with its own weight
+      logq = (float)(log((double)fmaxf(inv_z, 1e-9f)) - log(total));
+    }
+  }
+
+  // C. S_other of the token and its log-prob, by the wave holding it.
+  const int W = ((tok >> 3) & (SNT - 1)) >> 6;
+  if (wave != W) return;
+  float s_other;
+  if (tok == bi) {
+    // Every entry but the argmax itself, relative to the row maximum: the
+    // other lanes of this wave add their sweep-A sums, and the argmax lane's
+    // own entries are shared out over the wave through LDS (a few per lane).
+    const int L = (tok >> 3) & (SNT - 1);
+    if (tid == L) {
+#pragma unroll
+      for (int k = 0; k < SL; ++k) arg_row[k] = x[k];  // -inf past the row's end
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    float s = (tid == L || lm == NEG) ? 0.0f : (lm == M ? ls : ls * exp2_hw((lm - M) * c2));
+    const uint16_t* er = reinterpret_cast<const uint16_t*>(arg_row);
+#pragma unroll
+    for (int m = 0; m < (8 * SL + 63) / 64; ++m) {
+      const int t = lane + 64 * m;  // entry t & 7 of slab t >> 3
+      if (t < 8 * nslab) {
+        const float e = exp2_hw((Bits<Tag>::val(er[t]) - M) * c2);
+        s += ((t >> 3) * SNT + L) * 8 + (t & 7) == tok ? 0.0f : e;
+      }
+    }
+    float so = wave_sum_dpp(s);
+    for (int w = 0; w < SWAVES; ++w)
+      if (w != W) so += sh_s[w] * exp2_hw((sh_m[w] - M) * c2);
+    s_other = so;
+  } else {
+    // Z holds the maximum's term 1 >= e_tok, so the difference loses at most a bit.
+    s_other = Z - exp2_hw((xt_raw - M) * c2);
+  }
+  if (lane == 0) {
+    const RowLogprob<float> fr = finish_row<float>(M * iT, s_other, xt_raw * iT);
+    a.token[r] = tok;
+    a.logp[r] = fr.logp;
+    if (a.logq) a.logq[r] = logq;
+  }
+}
+
+template <class Tag, int SL>
+int launch_resident_sl(const SampleArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((sample_resident_kernel<Tag, SL>), dim3((unsigned)a.B), dim3(SNT), 0, st, a);
+  return check_launch("sample_resident_kernel");
+}
+
+template <class Tag>
+int launch_sample_resident(const SampleArgs& a, int nslab, hipStream_t st) {
+  if (nslab <= 4) return launch_resident_sl<Tag, 4>(a, st);
+  if (nslab <= 8) return launch_resident_sl<Tag, 8>(a, st);
+  if (nslab <= 12) return launch_resident_sl<Tag, 12>(a, st);
+  if (nslab <= 16) return launch_resident_sl<Tag, 16>(a, st);
+  return launch_resident_sl<Tag, RES_MAX_SLABS>(a, st);
+}
+
 }  // namespace
 }  // namespace rrl
 
@@ -910,6 +1209,18 @@ extern "C" int rrl_sample_logprobs(const void* logits, int32_t logits_dtype, int
   a.seed = seed; a.offset = offset;
   a.token = token_out; a.logp = logp_out; a.logq = logq_out; a.status = status;
   hipStream_t st = as_stream(stream);
+  // Plain sampling and greedy decoding of whole-vector, 16-byte aligned
+  // 16-bit rows hold the row in registers; everything else streams it.
+  const bool use_k = top_k > 0 && top_k < V;
+  const bool use_p = top_p > 0.0 && top_p < 1.0;
+  const int64_t nvec = V / 8;
+  if (logits_dtype != RRL_F32 && (greedy || (!use_k && !use_p)) && V % 8 == 0 &&
+      nvec <= (int64_t)SNT * RES_MAX_SLABS && ((uintptr_t)logits & 15u) == 0 &&
+      (B == 1 || row_stride % 8 == 0)) {
+    const int nslab = (int)((nvec + SNT - 1) / SNT);
+    if (logits_dtype == RRL_BF16) return launch_sample_resident<TagBF16>(a, nslab, st);
+    return launch_sample_resident<TagF16>(a, nslab, st);
+  }
   switch (logits_dtype) {
     case RRL_BF16: return launch_sample<TagBF16>(a, st);
     case RRL_F16: return launch_sample<TagF16>(a, st);

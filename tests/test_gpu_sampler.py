@@ -137,3 +137,112 @@ def test_bad_rows_and_shapes(device):
         RI.sample_next_token_batch(x[0], 1.0, 0, 1.0, True)
     empty = RI.sample_next_token_batch(torch.randn(0, 100, device=device), 1.0, 0, 1.0, True)
     assert empty.token_ids.numel() == 0
+
+
+def _rows(seed, B, V, dtype, scale=3.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, V, generator=g) * scale
+    hot = torch.randint(0, V, (B,), generator=g)
+    x[torch.arange(0, B, 4), hot[::4]] += 15.0  # dominant rows
+    x[1, V // 3] = x[1].max()  # a tie at the maximum (lowest index wins)
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("dtype,V", [
+    (torch.bfloat16, 151936),  # 19 slabs of the 20-slab variant, last one partial
+    (torch.bfloat16, 163840),  # 20 whole slabs
+    (torch.float16, 65536),    # 8 whole slabs
+    (torch.bfloat16, 50264),   # 7 slabs, last one partial
+    (torch.float16, 20000),    # 3 slabs, 451 lanes of the last
+    (torch.bfloat16, 8),       # one vector
+])
+@pytest.mark.parametrize("temperature,do_sample", [(1.0, True), (0.7, True), (1.0, False)])
+def test_resident_rows_match_oracle_and_streamed(device, dtype, V, temperature, do_sample):
+    """Whole-vector, 16-byte aligned 16-bit rows without top-k / top-p are held
+    in registers; the same logits one element off a 16-byte boundary take the
+    streaming kernel.  Both follow the oracle, and each other on every row
+    whose uniform is decided."""
+
+    print(f"[sampler] resident dtype={dtype} V={V} T={temperature} sample={do_sample}", flush=True)
+    B = 40
+    x = _rows(31 + V % 97, B, V, dtype)
+    kw = dict(temperature=temperature, top_k=0, top_p=1.0, do_sample=do_sample)
+    xd = x.to(device)
+    wide = torch.zeros(B, V + 8, dtype=dtype, device=device)
+    wide[:, 1:V + 1] = xd
+    for off in (0, 1):
+        res = RI.sample_next_token_batch(xd, seed=99, offset=off, **kw)
+        st = RI.sample_next_token_batch(wide[:, 1:V + 1], seed=99, offset=off, **kw)
+        tok = _check(x, res, seed=99, offset=off, what=f"resident V={V} off={off}", **kw)
+        _check(x, st, seed=99, offset=off, what=f"streamed V={V} off={off}", **kw)
+        want = so.sample_rows(x.float().numpy(), seed=99, offset=off, **kw)
+        sure = want["margin"] > MARGIN
+        assert (tok[sure] == st.token_ids.cpu().numpy()[sure]).all()
+        if temperature == 1.0:
+            lp = R.gather_token_logprobs(xd, res.token_ids).cpu().double()
+            assert torch.allclose(res.logprobs.cpu().double(), lp, rtol=1e-6, atol=1e-6)
+        if not do_sample:
+            assert torch.equal(res.token_ids.cpu(), torch.argmax(x.float(), dim=-1))
+            assert (res.sampling_logprobs == 0).all()
+
+
+def test_resident_draws_follow_the_distribution(device):
+    """8192 draws from one bf16 row held in registers (a stride-0 view)."""
+
+    V, B = 64, 8192
+    g = torch.Generator().manual_seed(25)
+    row = (torch.randn(V, generator=g) * 1.5).to(torch.bfloat16)
+    xd = row.to(device)[None].expand(B, V)
+    out = RI.sample_next_token_batch(xd, 1.0, 0, 1.0, True, seed=6)
+    q, _ = so.sampling_distribution(row.double().numpy(), 1.0, 0, 1.0)
+    counts = np.bincount(out.token_ids.cpu().numpy(), minlength=V)
+    expect = q / q.sum() * B
+    big = expect > 5
+    chi2 = float((((counts[big] - expect[big]) ** 2) / expect[big]).sum())
+    dof = int(big.sum()) - 1
+    assert chi2 < dof + 6 * np.sqrt(2 * dof), (chi2, dof)
+
+
+@pytest.mark.parametrize("bad", ["nan", "inf", "all_neg_inf"])
+def test_resident_bad_rows(device, bad):
+    x = torch.randn(4, 4096, device=device).to(torch.bfloat16)
+    if bad == "nan":
+        x[2, 4000] = float("nan")
+    elif bad == "inf":
+        x[2, 7] = float("inf")
+    else:
+        x[2] = -float("inf")
+    for do_sample in (True, False):
+        with pytest.raises(RuntimeError, match="inf"):
+            RI.sample_next_token_batch(x, 1.0, 0, 1.0, do_sample, seed=1)
+    # the other rows of a call are unaffected when run alone
+    ok = RI.sample_next_token_batch(x[:2], 1.0, 0, 1.0, False)
+    assert torch.equal(ok.token_ids.cpu(), torch.argmax(x[:2].float(), dim=-1).cpu())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_bad_rows_through_the_c_abi(device, dtype):
+    """The status word gets BAD_PROBS and the bad row's log-probs are NaN,
+    the others finite (register-resident bf16 rows and streamed float32
+    rows); -3e38 logits at T = 0.5 overflow x / T and count as bad."""
+
+    from rosellm_amd import _native as nat
+
+    B, V = 4, 4096
+    x = torch.randn(B, V, device=device).to(dtype)
+    x[1, 100] = float("nan")
+    x[3] = -3.0e38
+    for temperature, do_sample in ((0.5, 1), (1.0, 0)):
+        tok = torch.empty(B, dtype=torch.int64, device=device)
+        lp = torch.empty(B, device=device)
+        lq = torch.empty(B, device=device)
+        st = torch.zeros(1, dtype=torch.int32, device=device)
+        nat.call("rrl_sample_logprobs", x.data_ptr(), nat.dtype_code(dtype), B, V, V,
+                 temperature, 0, 1.0, do_sample, 3, 0, tok.data_ptr(), lp.data_ptr(),
+                 lq.data_ptr(), st.data_ptr(), nat.stream_ptr(device))
+        flagged = int(st.item()) & nat.FLAG_BAD_PROBS
+        bad = torch.isnan(lp).cpu()
+        want_bad = torch.tensor([False, True, False, temperature < 1.0])
+        assert torch.equal(bad, want_bad), (temperature, bad)
+        assert bool(flagged)
+        assert torch.isnan(lq.cpu()[want_bad]).all() and torch.isfinite(lp.cpu()[~want_bad]).all()
