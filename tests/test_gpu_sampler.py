@@ -153,6 +153,8 @@ def _rows(seed, B, V, dtype, scale=3.0):
     (torch.bfloat16, 163840),  # 20 whole slabs
     (torch.float16, 65536),    # 8 whole slabs
     (torch.bfloat16, 50264),   # 7 slabs, last one partial
+    (torch.bfloat16, 98296),   # 12 slabs of the 12-slab variant, last one partial
+    (torch.float16, 128256),   # 16 slabs of the 16-slab variant (Llama-3's vocabulary)
     (torch.float16, 20000),    # 3 slabs, 451 lanes of the last
     (torch.bfloat16, 8),       # one vector
 ])
