@@ -6,11 +6,15 @@
 // per row picks the token and forms both log-probabilities in the same launch.
 //
 // Row layout: slab k, lane j holds elements (k*1024 + j)*VEC .. +VEC-1 (VEC =
-// 16 bytes of logits), so every pass streams the row with coalesced 16-byte
-// loads, and vocabulary order is (slab, lane, element).  A row is re-read per
-// pass (from L2 / the memory-side cache: a 151936-entry bf16 row is 297 KB).
+// 16 bytes of logits), so every pass moves the row with coalesced 16-byte
+// loads, and vocabulary order is (slab, lane, element).  Two kernels:
+//   * sample_resident_kernel (plain sampling and greedy decoding of 16-bit
+//     rows made of whole, aligned 16-byte vectors): the row stays in VGPRs
+//     and is read from memory once; its sweeps are described at its definition.
+//   * sample_kernel (everything else): a row is re-read per pass (from L2 /
+//     the memory-side cache: a 151936-entry bf16 row is 297 KB).
 //
-// Passes (top-k, top-p and the tie searches only when active):
+// sample_kernel's passes (top-k, top-p and the tie searches only when active):
 //   1. row max and its lowest index (greedy choice), the sums of
 //      exp((x - max)/T) over every entry (Z without top-k) and over every
 //      entry but the maximum (the greedy token's S_other), NaN/+inf check;
