@@ -517,7 +517,8 @@ def bench_sample(args):
                    "rows": B, "vocab": V, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "kernel": "rrl_sample_logprobs",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles("rrl_sample_logprobs", "sample-default"),
                      "kernel_ms": round(head["kernel_ms"], 4), "alg_bytes_per_launch": alg},
         "cpu_baseline": cpu,
         "variants": {k: {"ms_per_step": round(v["ms"], 4), "kernel_ms": round(v["kernel_ms"], 4),
