@@ -8,9 +8,10 @@
 // Row layout: slab k, lane j holds elements (k*1024 + j)*VEC .. +VEC-1 (VEC =
 // 16 bytes of logits), so every pass moves the row with coalesced 16-byte
 // loads, and vocabulary order is (slab, lane, element).  Two kernels:
-//   * sample_resident_kernel (plain sampling and greedy decoding of 16-bit
-//     rows made of whole, aligned 16-byte vectors): the row stays in VGPRs
-//     and is read from memory once; its sweeps are described at its definition.
+//   * sample_resident_kernel (plain sampling, greedy decoding and top-k with
+//     or without top-p, of 16-bit rows made of whole, aligned 16-byte
+//     vectors): the row stays in VGPRs and is read from memory once; its
+//     sweeps are described at its definition.
 //   * sample_kernel (everything else): a row is re-read per pass (from L2 /
 //     the memory-side cache: a 151936-entry bf16 row is 297 KB).
 //
@@ -73,6 +74,7 @@ struct SampleArgs {
   double top_p;     // active iff 0 < top_p < 1
   int greedy;
   uint64_t seed, offset;
+  int fill_in;      // sample_kernel only redoes rows whose token is -1
   int64_t* token;
   float* logp;
   float* logq;
@@ -87,21 +89,32 @@ __device__ __forceinline__ uint32_t float_key(uint32_t b) {
   return (b & sign) ? (~b & all) : (b | sign);
 }
 
+// The bit pattern whose float_key is `key`.
+template <int KB>
+__device__ __forceinline__ uint32_t key_bits(uint32_t key) {
+  constexpr uint32_t sign = 1u << (KB - 1);
+  constexpr uint32_t all = KB == 32 ? 0xffffffffu : ((1u << KB) - 1u);
+  return (key & sign) ? (key & ~sign) : (~key & all);
+}
+
 template <class Tag> struct Bits;
 template <> struct Bits<TagBF16> {
   static constexpr uint32_t NEG_INF = 0xFF80FF80u;  // -inf in every element of a dword
   static constexpr int KB = 16;
   static __device__ __forceinline__ float val(uint32_t u) { return __uint_as_float(u << 16); }
+  static __device__ __forceinline__ uint32_t bits_of(float v) { return __float_as_uint(v) >> 16; }
 };
 template <> struct Bits<TagF16> {
   static constexpr uint32_t NEG_INF = 0xFC00FC00u;  // -inf in every element of a dword
   static constexpr int KB = 16;
   static __device__ __forceinline__ float val(uint32_t u) { return f16_bits_to_f32((uint16_t)u); }
+  static __device__ __forceinline__ uint32_t bits_of(float v) { return f32_to_f16_bits(v); }
 };
 template <> struct Bits<TagF32> {
   static constexpr uint32_t NEG_INF = 0xFF800000u;  // -inf in every element of a dword
   static constexpr int KB = 32;
   static __device__ __forceinline__ float val(uint32_t u) { return __uint_as_float(u); }
+  static __device__ __forceinline__ uint32_t bits_of(float v) { return __float_as_uint(v); }
 };
 
 // Lane `tid`'s 16 bytes of slab k as stored (zeros past the row's end); a
@@ -417,6 +430,120 @@ __device__ __forceinline__ int vocab_search(const typename Tag::S* row, int V, b
   return sel;
 }
 
+// Top-k (and top-p) draw from a candidate list in LDS, one entry per thread:
+// cs.idx / cs.bits hold n <= KCAP entries (vocabulary index, stored bits) in
+// any order, among them every entry whose key is >= kth.  The k candidates are
+// every entry above the k-th key kth and the first need_k entries at it,
+// lowest index first.  Z is taken over the candidates with exp(x/T - m)
+// (m = the row maximum of x/T), top-p is the radix select's threshold group
+// from exact integer sums over the list (max_key: the key of the row
+// maximum, which is always kept), and the token is drawn by inverse CDF over
+// the floored q in vocabulary order with the uniform u01.  Every thread
+// returns the token, log q(token) and the token's stored bits.
+template <class Tag>
+__device__ __forceinline__ void list_draw(CandShared& cs, float* sh_s, int n, uint32_t kth,
+                                          int need_k, bool use_p, double top_p, float iT,
+                                          float m, uint32_t max_key, double u01, int& tok,
+                                          float& logq, uint32_t& tok_bits) {
+  constexpr int KB = Bits<Tag>::KB;
+  const int tid = threadIdx.x;
+  // Sort by vocabulary index: an entry's rank is the number of smaller
+  // indices.
+  if (tid < n) {
+    const int e = cs.idx[tid];
+    int rank = 0;
+    for (int j = 0; j < n; ++j) rank += cs.idx[j] < e ? 1 : 0;
+    cs.sidx[rank] = e;
+    cs.sbits[rank] = cs.bits[tid];
+  }
+  __syncthreads();
+  // The k candidates: every entry above the k-th key and the first need_k
+  // entries at it, lowest index first; relaid densely in index order.
+  const bool have = tid < n;
+  const int se = have ? cs.sidx[tid] : 0;
+  const uint32_t sb = have ? cs.sbits[tid] : 0u;
+  const uint32_t skey = float_key<KB>(sb);
+  const bool tie = have && skey == kth;
+  int ntie = 0;
+  const int tie_rank = block_excl_count(tie, cs.wave_cnt, ntie);
+  const bool is_cand = have && (skey > kth || (tie && tie_rank < need_k));
+  int kc = 0;
+  const int pos = block_excl_count(is_cand, cs.wave_cnt, kc);
+  if (is_cand) {
+    cs.idx[pos] = se;
+    cs.bits[pos] = sb;
+  }
+  __syncthreads();
+  const bool mine = tid < kc;
+  const uint32_t cb = mine ? cs.bits[tid] : 0u;
+  const uint32_t ck = float_key<KB>(cb);
+  // Z over the candidates, with the general path's exp(x/T - m).
+  const float ev = mine ? expf(Bits<Tag>::val(cb) * iT - m) : 0.0f;
+  float zt[1] = {ev};
+  block_sum<SNT, 1, float>(zt, sh_s);
+  const float pc = ev * (1.0f / zt[0]);
+  // Top-p over the candidates: the radix select's threshold group (first
+  // key, in descending order, whose inclusive fixed-point mass passes P),
+  // from exact integer sums over the list.
+  bool keep = true;
+  if (use_p) {
+    const unsigned long long P = (unsigned long long)(top_p * kMassScale);
+    cs.mass[tid] = mine ? (unsigned long long)((double)pc * kMassScale) : 0ull;
+    cs.key[tid] = ck;
+    if (tid == 0) cs.found = 0;
+    __syncthreads();
+    unsigned long long A = 0, M = 0;
+    int C = 0, tr = 0;
+    if (mine) {
+      for (int j = 0; j < kc; ++j) {
+        const uint32_t kj = cs.key[j];
+        const unsigned long long mj = cs.mass[j];
+        const bool same = kj == ck;
+        A += kj > ck ? mj : 0ull;
+        M += same ? mj : 0ull;
+        C += same ? 1 : 0;
+        tr += (same && j < tid) ? 1 : 0;
+      }
+      if (M > 0 && A <= P && P < A + M) {  // every member writes the same values
+        cs.found = 1;
+        cs.pth = ck;
+        cs.A = A;
+        cs.M = M;
+        cs.C = C;
+      }
+    }
+    __syncthreads();
+    if (cs.found) {
+      const uint32_t pth = cs.pth;
+      const unsigned long long A0 = cs.A, C0 = (unsigned long long)cs.C;
+      const unsigned long long each = cs.M / C0;  // equal keys, equal mass
+      unsigned long long n_keep = each > 0 ? (P - A0) / each : C0;
+      // The first token in descending order (the row maximum) is always kept.
+      if (pth == max_key && n_keep == 0) n_keep = 1;
+      keep = ck > pth ||
+             (ck == pth && (n_keep >= C0 || (n_keep > 0 && (unsigned long long)tr < n_keep)));
+    }
+  }
+  // Inverse CDF over the candidates in vocabulary order.
+  const float wf = mine ? fmaxf(keep ? pc : 0.0f, 1e-9f) : 0.0f;
+  double incl, excl, tot;
+  block_scan_d((double)wf, cs.wave_sum, incl, excl, tot);
+  const double tgt = u01 * tot;
+  if (tid == 0) {
+    cs.pick = kc - 1;  // rounding past the last sum: the last candidate
+    cs.logq = 0.0f;
+  }
+  __syncthreads();
+  if (mine && excl <= tgt && tgt < incl) cs.pick = tid;
+  __syncthreads();
+  if (tid == cs.pick) cs.logq = (float)(log((double)wf) - log(tot));
+  __syncthreads();
+  tok = cs.idx[cs.pick];
+  tok_bits = cs.bits[cs.pick];
+  logq = cs.logq;
+  __syncthreads();
+}
+
 template <class Tag>
 __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   using S = typename Tag::S;
@@ -435,6 +562,8 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
 
   const int64_t r = blockIdx.x;
   if (r >= a.B) return;
+  // After the register-resident kernel, only the rows it handed back.
+  if (a.fill_in && a.token[r] != -1) return;
   const S* row = static_cast<const S*>(a.logits) + r * a.stride;
   const int V = (int)a.V;  // at most SNT * VEC * MAX_SLABS (checked on the host)
   const bool al16 = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
@@ -609,100 +738,9 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
     const double u01 = (double)(c[0] >> 8) * 5.9604644775390625e-8;  // 2^-24
 
     if (listed) {
-      // Top-k from the gathered entries, one per thread (n <= KCAP).
-      const int n = cs.n;
-      // Sort by vocabulary index: an entry's rank is the number of smaller
-      // indices.
-      if (tid < n) {
-        const int e = cs.idx[tid];
-        int rank = 0;
-        for (int j = 0; j < n; ++j) rank += cs.idx[j] < e ? 1 : 0;
-        cs.sidx[rank] = e;
-        cs.sbits[rank] = cs.bits[tid];
-      }
-      __syncthreads();
-      // The k candidates: every entry above the k-th key and the first need_k
-      // entries at it, lowest index first; relaid densely in index order.
-      const bool have = tid < n;
-      const int se = have ? cs.sidx[tid] : 0;
-      const uint32_t sb = have ? cs.sbits[tid] : 0u;
-      const bool tie = have && float_key<KB>(sb) == kth;
-      int ntie = 0;
-      const int tie_rank = block_excl_count(tie, cs.wave_cnt, ntie);
-      const bool is_cand = have && (!tie || tie_rank < need_k);
-      int kc = 0;
-      const int pos = block_excl_count(is_cand, cs.wave_cnt, kc);
-      if (is_cand) {
-        cs.idx[pos] = se;
-        cs.bits[pos] = sb;
-      }
-      __syncthreads();
-      const bool mine = tid < kc;
-      const uint32_t cb = mine ? cs.bits[tid] : 0u;
-      const uint32_t ck = float_key<KB>(cb);
-      // Z over the candidates, with the general path's exp(x/T - m).
-      const float ev = mine ? expf(Bits<Tag>::val(cb) * iT - m) : 0.0f;
-      float zt[1] = {ev};
-      block_sum<SNT, 1, float>(zt, sh_s);
-      const float pc = ev * (1.0f / zt[0]);
-      // Top-p over the candidates: the radix select's threshold group (first
-      // key, in descending order, whose inclusive fixed-point mass passes P),
-      // from exact integer sums over the list.
-      bool keep = true;
-      if (use_p) {
-        const unsigned long long P = (unsigned long long)(a.top_p * kMassScale);
-        cs.mass[tid] = mine ? (unsigned long long)((double)pc * kMassScale) : 0ull;
-        cs.key[tid] = ck;
-        if (tid == 0) cs.found = 0;
-        __syncthreads();
-        unsigned long long A = 0, M = 0;
-        int C = 0, tr = 0;
-        if (mine) {
-          for (int j = 0; j < kc; ++j) {
-            const uint32_t kj = cs.key[j];
-            const unsigned long long mj = cs.mass[j];
-            const bool same = kj == ck;
-            A += kj > ck ? mj : 0ull;
-            M += same ? mj : 0ull;
-            C += same ? 1 : 0;
-            tr += (same && j < tid) ? 1 : 0;
-          }
-          if (M > 0 && A <= P && P < A + M) {  // every member writes the same values
-            cs.found = 1;
-            cs.pth = ck;
-            cs.A = A;
-            cs.M = M;
-            cs.C = C;
-          }
-        }
-        __syncthreads();
-        if (cs.found) {
-          const uint32_t pth = cs.pth;
-          const unsigned long long A0 = cs.A, C0 = (unsigned long long)cs.C;
-          const unsigned long long each = cs.M / C0;  // equal keys, equal mass
-          unsigned long long n_keep = each > 0 ? (P - A0) / each : C0;
-          // The first token in descending order (the row maximum) is always kept.
-          if (pth == float_key<KB>(load_one<Tag>(row, bi)) && n_keep == 0) n_keep = 1;
-          keep = ck > pth ||
-                 (ck == pth && (n_keep >= C0 || (n_keep > 0 && (unsigned long long)tr < n_keep)));
-        }
-      }
-      // Inverse CDF over the candidates in vocabulary order.
-      const float wf = mine ? fmaxf(keep ? pc : 0.0f, 1e-9f) : 0.0f;
-      double incl, excl, tot;
-      block_scan_d((double)wf, cs.wave_sum, incl, excl, tot);
-      const double tgt = u01 * tot;
-      if (tid == 0) {
-        cs.pick = kc - 1;  // rounding past the last sum: the last candidate
-        cs.logq = 0.0f;
-      }
-      __syncthreads();
-      if (mine && excl <= tgt && tgt < incl) cs.pick = tid;
-      __syncthreads();
-      if (tid == cs.pick) cs.logq = (float)(log((double)wf) - log(tot));
-      __syncthreads();
-      tok = cs.idx[cs.pick];
-      logq = cs.logq;
+      uint32_t tok_bits;
+      list_draw<Tag>(cs, sh_s, cs.n, kth, need_k, use_p, a.top_p, iT, m,
+                     float_key<KB>(load_one<Tag>(row, bi)), u01, tok, logq, tok_bits);
     } else {
       auto cand = [&](int e, uint32_t key) {
         return !use_k || key > kth || (key == kth && (need_k >= cnt_k || e <= cut_k));
@@ -879,15 +917,21 @@ int launch_sample(const SampleArgs& a, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
-// Register-resident rows: sampling without top-k / top-p, and greedy
-// decoding, of 16-bit rows made of whole 16-byte vectors (V % 8 == 0, rows
-// 16-byte aligned, V <= 8 * 1024 * RES_MAX_SLABS).  Lane j holds vector
+// Register-resident rows: sampling without top-k / top-p, greedy decoding,
+// and top-k (top_k <= the lanes holding row data) with or without top-p, of
+// 16-bit rows made of whole 16-byte vectors (V % 8 == 0, rows 16-byte
+// aligned, V <= 8 * 1024 * RES_MAX_SLABS).  Lane j holds vector
 // k*1024 + j of its row in four VGPRs per slab k (the sample_kernel layout),
 // so the row is read from memory once:
 //   A. as the slab loads land: the lane's first maximum (value and slab) and
 //      its online sum of exp((x - max) / T); one LDS exchange gives the row
 //      maximum, Z and the lowest-index argmax;
-//   B. (sampling) each lane's float sum of the floored softmax weights per
+//   K. (top-k) the k-th largest lane maximum t0 (a radix select over the
+//      1024 lane maxima), every entry >= t0 gathered into the LDS list, the
+//      exact k-th key on the list, then list_draw (ties, top-p, the draw);
+//      a row whose list overflows gets token -1 for sample_kernel's
+//      fill-in launch;
+//   B. (plain sampling) each lane's float sum of the floored softmax weights per
 //      slab into LDS, float64 slab totals, the slab holding u * total, a
 //      prefix scan of that slab's lane sums and the claiming lane's own
 //      entries: the search and tiling rule of vocab_search;
@@ -918,6 +962,49 @@ __device__ __forceinline__ float sum8(const float (&e)[8]) {
   return ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
 }
 
+// The k-th largest of one 16-bit key per thread (threads with valid = false
+// take no part; 1 <= k <= the number of valid threads): MSB-first radix
+// select, 8 bits per pass, over an LDS histogram of 256 bins.
+__device__ __forceinline__ uint32_t block_kth_key16(uint32_t key, bool valid, int k,
+                                                    uint32_t* hist, uint32_t* sh_digit,
+                                                    uint32_t* sh_above) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t prefix = 0, pmask = 0;
+  uint32_t kk = (uint32_t)k;
+  for (int shift = 8; shift >= 0; shift -= 8) {
+    if (tid < 256) hist[tid] = 0;
+    __syncthreads();
+    if (valid && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    __syncthreads();
+    if (wave == 0) {
+      // lane l owns bins 4l..4l+3; the count above a bin is a suffix sum.
+      uint32_t c[4];
+      for (int b = 0; b < 4; ++b) c[b] = hist[4 * lane + b];
+      const uint32_t t = c[0] + c[1] + c[2] + c[3];
+      uint32_t incl = t;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_down(incl, o, 64);
+        if (lane + o < 64) incl += y;
+      }
+      uint32_t above = incl - t;
+      for (int b = 3; b >= 0; --b) {
+        if (above < kk && kk <= above + c[b]) {
+          *sh_digit = 4 * lane + b;
+          *sh_above = above;
+        }
+        above += c[b];
+      }
+    }
+    __syncthreads();
+    const uint32_t d = *sh_digit;
+    kk -= *sh_above;
+    prefix |= d << shift;
+    pmask |= 255u << shift;
+    __syncthreads();
+  }
+  return prefix;
+}
+
 // The defaults' floored softmax weight max(2^((x - max) * c2) / Z, 1e-9),
 // rounded the same way wherever it is evaluated.
 __device__ __forceinline__ float floored_weight(float x, float M, float c2, float inv_z) {
@@ -929,7 +1016,17 @@ __device__ __forceinline__ float floored_weight(float x, float M, float c2, floa
 template <class Tag, int SL>
 __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   static_assert(Tag::VEC == 8, "16-bit rows");
-  __shared__ float part[SL][SNT];  // sweep B: lane sums of the weights per slab
+  // Sweep B's lane sums of the weights per slab, or top-k's candidate list.
+  __shared__ union {
+    float part[SL][SNT];
+    CandShared cs;
+  } u;
+  auto& part = u.part;
+  auto& cs = u.cs;
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t sh_digit, sh_above, sh_kth;
+  __shared__ int sh_need;
+  __shared__ float sh_z[SWAVES];
   __shared__ double slab_tot[SL];
   __shared__ double scan_ws[SWAVES];
   __shared__ float sh_m[SWAVES], sh_s[SWAVES];
@@ -1028,10 +1125,87 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
     return;
   }
 
+  // The argmax lane's registers, for its wave's S_other (sweep C).
+  if (tid == ((bi >> 3) & (SNT - 1))) {
+#pragma unroll
+    for (int k = 0; k < SL; ++k) arg_row[k] = x[k];  // -inf past the row's end
+  }
+  // Greedy decoding reads it next in the same wave, with no barrier between.
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  uint32_t c[4] = {(uint32_t)r, 0u, (uint32_t)a.offset, (uint32_t)(a.offset >> 32)};
+  philox4x32_10(c, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
+  const double u01 = (double)(c[0] >> 8) * 5.9604644775390625e-8;  // 2^-24
+
   int tok = bi;
   float logq = 0.0f;
   float xt_raw = M;  // the token's logit
-  if (!a.greedy) {
+  const bool use_k = a.top_k > 0 && a.top_k < V;
+  if (!a.greedy && use_k) {
+    // Top-k (top_k <= the lanes holding row data, so every lane maximum
+    // counts): the k-th largest lane maximum t0 has at least k entries at or
+    // above it.  Those entries (a float compare: a superset of the keys
+    // >= t0 when -0 and +0 meet) go to the LDS list; the exact k-th key,
+    // its ties, top-p and the draw are found on the list.  A row whose list
+    // overflows gets token -1 and is redone by sample_kernel.
+    const int kq = (int)a.top_k;
+    constexpr int KB = Bits<Tag>::KB;
+    const uint32_t t0 = block_kth_key16(float_key<KB>(Bits<Tag>::bits_of(lm)), tid < nvec, kq,
+                                        hist, &sh_digit, &sh_above);
+    const float t0f = Bits<Tag>::val(key_bits<KB>(t0));
+    if (tid == 0) cs.n = 0;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < SL; ++k) {
+      if (k < nslab) {
+        float v[8];
+        unpack8<Tag>(x[k], v);
+        const bool inside = k * SNT + tid < nvec;
+        bool any = false;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) any = any || v[i] >= t0f;
+        if (inside && any) {
+          const uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (v[i] >= t0f) {
+              const int p = atomicAdd(&cs.n, 1);
+              if (p < KCAP) {
+                cs.idx[p] = (k * SNT + tid) * 8 + i;
+                cs.bits[p] = (w[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+              }
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const int n = cs.n;
+    if (n > KCAP) {
+      if (tid == 0) a.token[r] = -1;
+      return;
+    }
+    // The exact k-th key: the entry with fewer than k keys above it and at
+    // least k at or above it (every such entry writes the same values).
+    if (tid < n) {
+      const uint32_t ki = float_key<KB>(cs.bits[tid]);
+      int gt = 0, eq = 0;
+      for (int j = 0; j < n; ++j) {
+        const uint32_t kj = float_key<KB>(cs.bits[j]);
+        gt += kj > ki ? 1 : 0;
+        eq += kj == ki ? 1 : 0;
+      }
+      if (gt < kq && kq <= gt + eq) {
+        sh_kth = ki;
+        sh_need = kq - gt;
+      }
+    }
+    __syncthreads();
+    uint32_t tok_bits;
+    list_draw<Tag>(cs, sh_z, n, sh_kth, sh_need, a.top_p > 0.0 && a.top_p < 1.0, a.top_p, iT,
+                   M * iT, float_key<KB>(Bits<Tag>::bits_of(M)), u01, tok, logq, tok_bits);
+    xt_raw = Bits<Tag>::val(tok_bits);
+  } else if (!a.greedy) {
     // B. Inverse CDF of the floored softmax in vocabulary order.
     const float inv_z = 1.0f / Z;
 #pragma unroll
@@ -1061,9 +1235,6 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
     __syncthreads();
     double total = 0.0;
     for (int k = 0; k < nslab; ++k) total += slab_tot[k];
-    uint32_t c[4] = {(uint32_t)r, 0u, (uint32_t)a.offset, (uint32_t)(a.offset >> 32)};
-    philox4x32_10(c, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
-    const double u01 = (double)(c[0] >> 8) * 5.9604644775390625e-8;  // 2^-24
     const double target = u01 * total;
     int ks = -1;
     double run = 0.0;
@@ -1130,12 +1301,6 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
     // other lanes of this wave add their sweep-A sums, and the argmax lane's
     // own entries are shared out over the wave through LDS (a few per lane).
     const int L = (tok >> 3) & (SNT - 1);
-    if (tid == L) {
-#pragma unroll
-      for (int k = 0; k < SL; ++k) arg_row[k] = x[k];  // -inf past the row's end
-    }
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
     float s = (tid == L || lm == NEG) ? 0.0f : (lm == M ? ls : ls * exp2_hw((lm - M) * c2));
     const uint16_t* er = reinterpret_cast<const uint16_t*>(arg_row);
 #pragma unroll
@@ -1218,12 +1383,19 @@ extern "C" int rrl_sample_logprobs(const void* logits, int32_t logits_dtype, int
   const bool use_k = top_k > 0 && top_k < V;
   const bool use_p = top_p > 0.0 && top_p < 1.0;
   const int64_t nvec = V / 8;
-  if (logits_dtype != RRL_F32 && (greedy || (!use_k && !use_p)) && V % 8 == 0 &&
+  // Top-k in registers needs every one of the k-th largest lane maxima.
+  const bool res_topk = !greedy && use_k && top_k <= std::min<int64_t>(nvec, SNT);
+  if (logits_dtype != RRL_F32 && (greedy || (!use_k && !use_p) || res_topk) && V % 8 == 0 &&
       nvec <= (int64_t)SNT * RES_MAX_SLABS && ((uintptr_t)logits & 15u) == 0 &&
       (B == 1 || row_stride % 8 == 0)) {
     const int nslab = (int)((nvec + SNT - 1) / SNT);
-    if (logits_dtype == RRL_BF16) return launch_sample_resident<TagBF16>(a, nslab, st);
-    return launch_sample_resident<TagF16>(a, nslab, st);
+    const int rc = logits_dtype == RRL_BF16 ? launch_sample_resident<TagBF16>(a, nslab, st)
+                                            : launch_sample_resident<TagF16>(a, nslab, st);
+    if (rc != RRL_OK || !res_topk) return rc;
+    // Rows whose candidate list overflowed (token -1) go through the
+    // streaming kernel, which returns at once for every other row.
+    a.fill_in = 1;
+    return logits_dtype == RRL_BF16 ? launch_sample<TagBF16>(a, st) : launch_sample<TagF16>(a, st);
   }
   switch (logits_dtype) {
     case RRL_BF16: return launch_sample<TagBF16>(a, st);

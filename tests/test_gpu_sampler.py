@@ -158,17 +158,25 @@ def _rows(seed, B, V, dtype, scale=3.0):
     (torch.float16, 20000),    # 3 slabs, 451 lanes of the last
     (torch.bfloat16, 8),       # one vector
 ])
-@pytest.mark.parametrize("temperature,do_sample", [(1.0, True), (0.7, True), (1.0, False)])
-def test_resident_rows_match_oracle_and_streamed(device, dtype, V, temperature, do_sample):
-    """Whole-vector, 16-byte aligned 16-bit rows without top-k / top-p are held
-    in registers; the same logits one element off a 16-byte boundary take the
-    streaming kernel.  Both follow the oracle, and each other on every row
-    whose uniform is decided."""
+@pytest.mark.parametrize("kw", [
+    dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=True),
+    dict(temperature=0.7, top_k=0, top_p=1.0, do_sample=True),
+    dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=False),
+    dict(temperature=0.7, top_k=50, top_p=1.0, do_sample=True),
+    dict(temperature=1.2, top_k=200, top_p=0.8, do_sample=True),
+    dict(temperature=1.0, top_k=1000, top_p=0.95, do_sample=True),
+], ids=lambda c: f"T{c['temperature']}-k{c['top_k']}-p{c['top_p']}-s{int(c['do_sample'])}")
+def test_resident_rows_match_oracle_and_streamed(device, dtype, V, kw):
+    """Whole-vector, 16-byte aligned 16-bit rows are held in registers for
+    plain sampling, greedy decoding and top-k (with or without top-p); the
+    same logits one element off a 16-byte boundary take the streaming kernel.
+    Both follow the oracle, and each other on every row whose uniform is
+    decided."""
 
-    print(f"[sampler] resident dtype={dtype} V={V} T={temperature} sample={do_sample}", flush=True)
+    print(f"[sampler] resident dtype={dtype} V={V} {kw}", flush=True)
     B = 40
     x = _rows(31 + V % 97, B, V, dtype)
-    kw = dict(temperature=temperature, top_k=0, top_p=1.0, do_sample=do_sample)
+    temperature, do_sample = kw["temperature"], kw["do_sample"]
     xd = x.to(device)
     wide = torch.zeros(B, V + 8, dtype=dtype, device=device)
     wide[:, 1:V + 1] = xd
@@ -186,6 +194,26 @@ def test_resident_rows_match_oracle_and_streamed(device, dtype, V, temperature, 
         if not do_sample:
             assert torch.equal(res.token_ids.cpu(), torch.argmax(x.float(), dim=-1))
             assert (res.sampling_logprobs == 0).all()
+
+
+@pytest.mark.parametrize("top_k,top_p", [(10, 1.0), (600, 0.9)])
+def test_resident_topk_list_overflow(device, top_k, top_p):
+    """Rows whose entries at or above the k-th largest lane maximum exceed the
+    1024-entry list (here 2000 copies of the maximum, or coarse logits) are
+    handed to the streaming kernel in the same call; the other rows of the
+    batch stay with the register-resident kernel.  All follow the oracle."""
+
+    B, V = 12, 32768
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(B, V, generator=g) * 3.0
+    x[0, torch.randperm(V, generator=g)[:2000]] = 20.0   # 2000 tied maxima
+    x[3] = torch.round(x[3] * 2.0) / 2.0                 # coarse grid: many ties
+    x[5, 7] = 30.0
+    x = x.to(torch.bfloat16)
+    kw = dict(temperature=1.0, top_k=top_k, top_p=top_p, do_sample=True)
+    for off in range(3):
+        out = RI.sample_next_token_batch(x.to(device), seed=13, offset=off, **kw)
+        _check(x, out, seed=13, offset=off, what=f"overflow k={top_k} off={off}", **kw)
 
 
 def test_resident_draws_follow_the_distribution(device):
