@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define RRL_ABI_VERSION 2
+#define RRL_ABI_VERSION 3
 
 #if defined(__GNUC__)
 #define RRL_API __attribute__((visibility("default")))
@@ -210,6 +210,16 @@ RRL_API int rrl_policy_row_coef(const rrl_policy_params* params, int64_t B, int6
                         void* workspace, int32_t* status, void* stream);
 
 RRL_API size_t rrl_fused_records_bytes(int64_t B, int64_t T);
+
+/* Target ids checked ahead of the single-pass sweep: TARGET_RANGE in *status
+ * for any target[b, t] (int32 or int64 view) outside [0, V) that is not NLL's
+ * ignore_index (params->ignore_index for kind RRL_OBJ_NLL).  The sweep makes
+ * the same check; this entry lets a caller read the status before launching
+ * it, so the host need not wait for the sweep to raise the index error of
+ * torch.gather (losses.py:34-38) or F.cross_entropy (model.py:643-649).  It
+ * replaces no reference function of its own. */
+RRL_API int rrl_check_targets(const rrl_policy_params* params, int64_t B, int64_t T, int64_t V,
+                      rrl_view target, int32_t* status, void* stream);
 
 RRL_API int rrl_fused_logprob_policy(const rrl_policy_params* params, const void* logits,
                              int32_t logits_dtype, int64_t B, int64_t T, int64_t V,

@@ -343,6 +343,27 @@ int run_policy_fwd(const PolicyArgs& a, hipStream_t st) {
   return RRL_OK;
 }
 
+// Target ids in [0, V) (NLL's ignore_index exempt), one token per thread,
+// ahead of the single-pass sweep that makes the same check.
+struct TargetCheckArgs {
+  rrl_policy_params pp;
+  int64_t B, T, V;
+  View tgt;
+  int32_t* status;
+};
+
+__global__ __launch_bounds__(256) void check_targets_kernel(TargetCheckArgs a) {
+  const PolicyConsts<float> c = PolicyConsts<float>::make(a.pp);
+  const int64_t n = a.B * a.T;
+  bool bad = false;
+  for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t b = i / a.T, t = i - b * a.T;
+    const int64_t tgt = load_index(a.tgt.ptr, a.tgt.dt, b * a.tgt.sr + t * a.tgt.sc);
+    bad = bad || ((tgt < 0 || tgt >= a.V) && !target_ignored(c, tgt));
+  }
+  if (__any(bad) && (threadIdx.x & 63) == 0) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+}
+
 int validate_policy(const rrl_policy_params* p, int64_t B, int64_t T, int acc) {
   RRL_REQUIRE(p != nullptr, RRL_EINVAL, "params is null");
   RRL_REQUIRE(p->kind >= RRL_OBJ_PPO && p->kind <= RRL_OBJ_NLL, RRL_EINVAL, "unknown objective kind");
@@ -438,4 +459,22 @@ extern "C" int rrl_policy_row_coef(const rrl_policy_params* params, int64_t B, i
   else
     hipLaunchKernelGGL((row_coef_kernel<float, 1024>), dim3(1), dim3(1024), 0, st, a);
   return check_launch("row_coef_kernel");
+}
+
+extern "C" int rrl_check_targets(const rrl_policy_params* params, int64_t B, int64_t T,
+                                 int64_t V, rrl_view target, int32_t* status, void* stream) {
+  clear_error();
+  if (int rc = validate_policy(params, B, T, RRL_F32)) return rc;
+  RRL_REQUIRE(V >= 1, RRL_EINVAL, "vocabulary must be non-empty");
+  RRL_REQUIRE(status && (B * T == 0 || target.ptr), RRL_EINVAL, "null pointer argument");
+  RRL_REQUIRE(target.dtype == RRL_I32 || target.dtype == RRL_I64, RRL_EDTYPE,
+              "target ids must be int32 or int64");
+  const int64_t n = B * T;
+  if (n == 0) return RRL_OK;
+  TargetCheckArgs a{};
+  a.pp = *params; a.B = B; a.T = T; a.V = V; a.tgt = to_view(target); a.status = status;
+  const int64_t blocks = (n + 255) / 256;
+  const unsigned grid = (unsigned)(blocks < 4096 ? blocks : 4096);
+  hipLaunchKernelGGL(check_targets_kernel, dim3(grid), dim3(256), 0, as_stream(stream), a);
+  return check_launch("check_targets_kernel");
 }

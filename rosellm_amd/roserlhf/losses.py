@@ -255,6 +255,20 @@ def _raise_flags(flags: int, kind: int) -> None:
         raise ValueError("cannot reduce an empty mask")
 
 
+def _check_before_sweep(logits: Tensor) -> bool:
+    """Whether the single-pass call reads its status before the sweep.
+
+    For float32 and float64 logits every data error is known before the
+    sweep runs: the row coefficients flag empty masks and rrl_check_targets
+    the targets.  The one host synchronisation then waits for those small
+    kernels only, and the host runs ahead of the sweep.  16-bit logits read
+    it after the sweep, because the register-resident kernel may ask for a
+    rerun on the generic kernel (FLAG_FAST_RANGE).
+    """
+
+    return logits.element_size() >= 4
+
+
 def _scalar_dtypes(kind: int, cur: Tensor, old: Tensor, adv: Tensor) -> Tuple[torch.dtype, ...]:
     ratio = torch.promote_types(cur.dtype, old.dtype)
     obj = torch.promote_types(ratio, adv.dtype)
@@ -784,11 +798,16 @@ class _FusedPolicy(torch.autograd.Function):
         trusted = torch.empty(B * T if kind == nat.OBJ_SAO else 0, dtype=torch.bool, device=dev)
         lview = nat.RrlView(logp.data_ptr(), acc_code, T, 1)
 
+        early = _check_before_sweep(logits)
+
         def run(p):
             status = nat.new_status(dev)
             pref = ctypes_ref(p)
             nat.call("rrl_policy_row_coef", pref, B, T, mv, acc_code, coef.data_ptr(),
                      ws.data_ptr(), status.data_ptr(), stream)
+            if early:
+                nat.call("rrl_check_targets", pref, B, T, V, tview, status.data_ptr(), stream)
+                _raise_flags(nat.read_status(status), kind)
             nat.call("rrl_fused_logprob_policy", pref, x.data_ptr(), nat.dtype_code(x.dtype), B,
                      T, V, s_b, s_t, tview, ov, av, mv, coef.data_ptr(), records.data_ptr(),
                      logp.data_ptr(), lse.data_ptr(), dl.data_ptr(),
@@ -796,7 +815,7 @@ class _FusedPolicy(torch.autograd.Function):
             nat.call("rrl_policy_fwd", pref, B, T, lview, ov, av, mv, acc_code, ws.data_ptr(),
                      scal.data_ptr(), None, nat.ptr(trusted) if trusted.numel() else None,
                      status.data_ptr(), stream)
-            return nat.read_status(status)
+            return 0 if early else nat.read_status(status)
 
         flags = run(params)
         if flags & nat.FLAG_FAST_RANGE:

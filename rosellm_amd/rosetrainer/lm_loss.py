@@ -116,18 +116,23 @@ class _CrossEntropyRows(torch.autograd.Function):
             dptr = dl.data_ptr()
         lview = nat.RrlView(logp.data_ptr(), acc_code, T, 1)
 
+        early = _losses._check_before_sweep(logits)
+
         def run(p):
             status = nat.new_status(dev)
             pref = _losses.ctypes_ref(p)
             nat.call("rrl_policy_row_coef", pref, B, T, tview, acc_code, coef.data_ptr(),
                      ws.data_ptr(), status.data_ptr(), stream)
+            if early:
+                nat.call("rrl_check_targets", pref, B, T, V, tview, status.data_ptr(), stream)
+                _losses._raise_flags(nat.read_status(status), nat.OBJ_NLL)
             nat.call("rrl_fused_logprob_policy", pref, x.data_ptr(), nat.dtype_code(x.dtype), B,
                      T, V, s_b, s_t, tview, unused, unused, tview, coef.data_ptr(),
                      records.data_ptr(), logp.data_ptr(), lse.data_ptr(), dptr,
                      nat.dtype_code(logits.dtype), d_b, d_t, status.data_ptr(), stream)
             nat.call("rrl_policy_fwd", pref, B, T, lview, unused, unused, tview, acc_code,
                      ws.data_ptr(), scal.data_ptr(), None, None, status.data_ptr(), stream)
-            return nat.read_status(status)
+            return 0 if early else nat.read_status(status)
 
         flags = run(params)
         if flags & nat.FLAG_FAST_RANGE:

@@ -199,6 +199,68 @@ def test_logprob_target_out_of_range_raises(device):
         R.gather_token_logprobs(x, t)
 
 
+@pytest.mark.parametrize("tdtype", [torch.int64, torch.int32])
+def test_check_targets_through_the_c_abi(device, tdtype):
+    """rrl_check_targets flags TARGET_RANGE for any id outside [0, V) except
+    NLL's ignore_index, on strided views too, and never for valid ids."""
+
+    from rosellm_amd import _native as nat
+    from rosellm_amd.rosetrainer import lm_loss as LM
+
+    B, T, V = 5, 300, 1000
+    wide = torch.randint(0, V, (B, T + 3), device=device, dtype=tdtype)
+    view = wide[:, 1:T + 1]
+
+    def flags(t, params):
+        st = torch.zeros(1, dtype=torch.int32, device=device)
+        tv, _keep = nat.rows_view(t, B, T)
+        nat.call("rrl_check_targets", L.ctypes_ref(params), B, T, V, tv, st.data_ptr(),
+                 nat.stream_ptr(device))
+        return int(st.item())
+
+    ppo = L._params(nat.OBJ_PPO, clip_low=0.2, clip_high=0.2)
+    nll = LM._nll_params(-100, "mean")
+    assert flags(view, ppo) == 0 and flags(view, nll) == 0
+    wide[0, 0] = V  # outside the view: not checked
+    assert flags(view, ppo) == 0
+    for badv in (V, -1, -100):
+        w2 = wide.clone()
+        w2[3, 17] = badv
+        want = 0 if (badv == -100) else nat.FLAG_TARGET_RANGE
+        assert flags(w2[:, 1:T + 1], ppo) == nat.FLAG_TARGET_RANGE
+        assert flags(w2[:, 1:T + 1], nll) == want
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
+def test_fused_data_errors_raise(device, dtype):
+    """Out-of-range targets, an empty mask and SAPO's empty rows raise the
+    reference's errors whether the status is read before the sweep (float32
+    and float64 logits) or after it (16-bit); a valid call right after works."""
+
+    B, T, V = 4, 6, 4096
+    x, t, old, adv, mask = _fused_inputs(71, B, T, V, dtype)
+    d = lambda v: v.to(device)  # noqa: E731
+    for badv in (V, -1):
+        bad = t.clone()
+        bad[2, 3] = badv
+        with pytest.raises(RuntimeError, match="out of bounds"):
+            R.fused_policy_loss(d(x), d(bad), d(old), d(adv), d(mask))
+    with pytest.raises(ValueError, match="empty mask"):
+        R.fused_policy_loss(d(x), d(t), d(old), d(adv), d(torch.zeros_like(mask)))
+    rows = mask.clone()
+    rows[1] = False
+    with pytest.raises(ValueError, match="at least one action token"):
+        R.fused_policy_loss(d(x), d(t), d(old), d(adv), d(rows), objective="sapo")
+    xd = d(x).requires_grad_()
+    out = R.fused_policy_loss(xd, d(t), d(old), d(adv), d(mask), clip_low=0.2, clip_high=0.28)
+    out.loss.backward()
+    out_o, _, dlo = o.policy_step("ppo", x, t, old, adv, mask, exact=True, clip_low=0.2,
+                                  clip_high=0.28)
+    scale = max(abs(float(out_o["loss"])), float(adv.abs().mean()))
+    assert abs(out.loss.item() - float(out_o["loss"])) <= 2e-3 * scale
+    _rownorm16(xd.grad, dlo, 2e-3, "dlogits after the errors")
+
+
 def test_logprob_empty(device):
     x = torch.randn(0, 4, 11, device=device, requires_grad=True)
     t = torch.zeros(0, 4, dtype=torch.long, device=device)
