@@ -121,11 +121,17 @@ template <> struct Pack16<TagF32> {
 };
 
 // A row as the resident kernels hold it: `head` single elements up to the
-// first 16-byte boundary, `nbody` aligned 16-byte vectors (the register
-// slabs), then `tail` single elements.  head <= EPV - 1 and tail <= EPV - 1,
-// so lanes 0-7 carry the head and lanes 8-15 the tail in one extra register.
-// Without EXTRAS every row is 16-byte aligned with V % EPV == 0: head = tail
-// = 0 and nbody is the same for every row.
+// first 128-byte boundary, `nbody` 16-byte vectors (the register slabs), then
+// `tail` single elements.  The body starts on a 128-byte boundary so that
+// each wave's 1 KB run of vector stores covers whole cache lines: runs that
+// share a partly written line with the next wave's run cost up to 10% of the
+// write rate.  head < 128 / element size (at most 63) and tail <= EPV - 1,
+// so lanes 0-63 carry the head and lanes 64-71 the tail in one extra
+// register.  Without EXTRAS every row is 16-byte aligned with V % EPV == 0:
+// head = tail = 0 and nbody is the same for every row.
+constexpr uint32_t kBodyAlign = 128;
+constexpr int kHeadLanes = 64;
+
 struct RowGeo {
   uint32_t head, nbody, tail;
 };
@@ -135,8 +141,8 @@ __device__ __forceinline__ RowGeo row_geo(const void* row, uint32_t V, int32_t n
   constexpr uint32_t EPV = Pack16<Tag>::EPV, ESZ = 16 / EPV;
   RowGeo g;
   if constexpr (EXTRAS) {
-    const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(row) & 15u);
-    uint32_t h = mis ? (16u - mis) / ESZ : 0u;
+    const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(row) & (kBodyAlign - 1u));
+    uint32_t h = mis ? (kBodyAlign - mis) / ESZ : 0u;
     h = h < V ? h : V;
     const uint32_t rem = V - h;
     g.head = h;
@@ -154,8 +160,9 @@ __device__ __forceinline__ RowGeo row_geo(const void* row, uint32_t V, int32_t n
 template <class Tag>
 __device__ __forceinline__ int32_t extra_index(const RowGeo& g, int tid) {
   constexpr int EPV = Pack16<Tag>::EPV;
-  if (tid < 8) return tid < (int)g.head ? tid : -1;
-  if (tid < 16) return tid - 8 < (int)g.tail ? (int)(g.head + g.nbody * EPV) + tid - 8 : -1;
+  if (tid < kHeadLanes) return tid < (int)g.head ? tid : -1;
+  if (tid < kHeadLanes + EPV)
+    return tid - kHeadLanes < (int)g.tail ? (int)(g.head + g.nbody * EPV) + tid - kHeadLanes : -1;
   return -1;
 }
 
@@ -753,12 +760,13 @@ constexpr int64_t kMaxResidentVec = 20 * RNT;  // SL = 20 fits 128 VGPRs without
 // Takes the register-resident kernel (mode 2: the fused single pass; mode 1:
 // rrl_logprob_bwd with the forward's log-probs given) for 16-bit and float32
 // logits when the row's 16-byte vectors fit the register budget (V <= 163840
-// 16-bit or 81920 float32 entries).  Rows that are 16-byte aligned with
-// V % (16 / element size) == 0 take the plain variant; any other row takes the
-// variant with head and tail elements, provided every dlogits row sits at its
-// logits row's offset from a 16-byte boundary (same strides mod 16 bytes, as
-// for contiguous tensors or in place).  Otherwise *launched stays false and
-// the caller runs the generic row kernel.
+// 16-bit or 81920 float32 entries).  Rows that are 128-byte aligned with
+// V % (16 / element size) == 0 take the plain variant.  Other rows take the
+// variant with head and tail elements, whose body starts on a 128-byte
+// boundary, provided every dlogits row sits at its logits row's offset from a
+// 128-byte boundary (same strides mod 128 bytes, as for contiguous tensors or
+// in place); failing that, 16-byte aligned rows take the plain variant.
+// Otherwise *launched stays false and the caller runs the generic row kernel.
 int maybe_launch_resident(const RowArgs& a, int mode, int logits_dtype, hipStream_t stream,
                           bool* launched) {
   *launched = false;
@@ -771,12 +779,16 @@ int maybe_launch_resident(const RowArgs& a, int mode, int logits_dtype, hipStrea
   const int64_t epv = 16 / esz;
   if (a.B * a.T == 0 || a.V / epv > kMaxResidentVec) return RRL_OK;
   if (a.B * a.T >= ((int64_t)1 << 31) || a.T >= ((int64_t)1 << 31)) return RRL_OK;
-  const auto al16 = [&](int64_t elems) { return ((elems * esz) % 16) == 0; };
-  const bool aligned = a.V % epv == 0 && (uintptr_t)a.logits % 16 == 0 &&
-                       (uintptr_t)a.dl % 16 == 0 && al16(a.ls_b) && al16(a.ls_t) &&
-                       al16(a.ds_b) && al16(a.ds_t);
-  const bool same_offset = ((uintptr_t)a.dl - (uintptr_t)a.logits) % 16 == 0 &&
-                           al16(a.ds_b - a.ls_b) && al16(a.ds_t - a.ls_t);
+  const auto al = [&](int64_t elems, int64_t n) { return ((elems * esz) % n) == 0; };
+  const auto rows_aligned = [&](int64_t n) {
+    return a.V % epv == 0 && (uintptr_t)a.logits % n == 0 && (uintptr_t)a.dl % n == 0 &&
+           al(a.ls_b, n) && al(a.ls_t, n) && al(a.ds_b, n) && al(a.ds_t, n);
+  };
+  const bool same_offset = ((uintptr_t)a.dl - (uintptr_t)a.logits) % kBodyAlign == 0 &&
+                           al(a.ds_b - a.ls_b, kBodyAlign) && al(a.ds_t - a.ls_t, kBodyAlign);
+  // Plain: 128-byte aligned rows, or 16-byte aligned ones the head/tail
+  // variant cannot take.
+  const bool aligned = rows_aligned(kBodyAlign) || (!same_offset && rows_aligned(16));
   if (!aligned && !same_offset) return RRL_OK;
   const int32_t nvec = (int32_t)(a.V / epv);
   if (mode == 1) {
