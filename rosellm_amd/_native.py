@@ -213,7 +213,17 @@ def require_device(*tensors: Optional[torch.Tensor]) -> torch.device:
     return dev
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device) -> int:
+    """The current HIP stream of `device` as an integer handle.  torch's raw
+    accessor skips building a Stream object (about 2 us per call, paid by
+    every entry point); the public call is the fallback."""
+
+    if _raw_stream is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

@@ -31,6 +31,7 @@ from __future__ import annotations
 
 from typing import NamedTuple, Optional
 
+import numpy as np
 import torch
 from torch import Tensor
 
@@ -94,7 +95,8 @@ def sample_next_token_batch(
              x.stride(0) if B > 1 else V, float(temperature), int(top_k), float(top_p),
              int(bool(do_sample)), int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 64 - 1),
              tokens.data_ptr(), logp.data_ptr(), logq.data_ptr(), None, nat.stream_ptr(dev))
-    if B and bool(torch.isnan(logp.cpu()).any()):
+    # NaN anywhere makes the sum NaN (the log-probs are never +inf).
+    if B and bool(np.isnan(logp.cpu().numpy().sum())):
         raise RuntimeError("probability tensor contains either `inf`, `nan` or element < 0")
     return SampleOutput(tokens, logp, logq)
 
