@@ -1,4 +1,4 @@
-"""Next-token sampling with behaviour log-probs in one launch.
+"""Next-token sampling with behaviour log-probs on the device, in one call.
 
 The reference picks the next token in ``InferenceEngine._sample_next_token_batch``
 (roseinfer/engine.py:1103-1171): greedy argmax, or ``logits / temperature``
