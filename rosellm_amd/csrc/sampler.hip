@@ -82,10 +82,14 @@ struct SampleArgs {
 };
 
 // Order-preserving unsigned key of a float's bit pattern (16- or 32-bit).
+// -0 takes +0's key: the two compare equal, so at a top-k or top-p threshold
+// they are one group of ties, kept lowest index first (as value comparisons
+// rank them).
 template <int KB>
 __device__ __forceinline__ uint32_t float_key(uint32_t b) {
   constexpr uint32_t sign = 1u << (KB - 1);
   constexpr uint32_t all = KB == 32 ? 0xffffffffu : ((1u << KB) - 1u);
+  b = (b & (all ^ sign)) == 0u ? 0u : b;
   return (b & sign) ? (~b & all) : (b | sign);
 }
 

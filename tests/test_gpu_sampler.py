@@ -276,3 +276,32 @@ def test_bad_rows_through_the_c_abi(device, dtype):
         assert torch.equal(bad, want_bad), (temperature, bad)
         assert bool(flagged)
         assert torch.isnan(lq.cpu()[want_bad]).all() and torch.isfinite(lp.cpu()[~want_bad]).all()
+
+
+@pytest.mark.parametrize("dtype,misaligned", [(torch.bfloat16, False), (torch.bfloat16, True),
+                                              (torch.float32, False)])
+def test_signed_zero_ties(device, dtype, misaligned):
+    """-0.0 and +0.0 compare equal: at a top-k or top-p threshold that falls
+    among zeros of both signs they form one group of ties, kept lowest index
+    first, in the register-resident and the streaming kernel alike."""
+
+    g = torch.Generator().manual_seed(51)
+    B, V = 16, 4096
+    x = torch.randn(B, V, generator=g) - 2.0
+    zero = torch.rand(B, V, generator=g) < 0.2
+    neg = torch.rand(B, V, generator=g) < 0.5
+    x = torch.where(zero, torch.where(neg, torch.tensor(-0.0), torch.tensor(0.0)), x)
+    x[:, :16] = torch.rand(B, 16, generator=g) + 0.5  # a few entries above the zeros
+    assert bool((torch.signbit(x) & (x == 0)).any()) and bool((~torch.signbit(x) & (x == 0)).any())
+    x = x.to(dtype)
+    if misaligned:
+        wide = torch.zeros(B, V + 8, dtype=dtype, device=device)
+        wide[:, 1:V + 1] = x.to(device)
+        xd = wide[:, 1:V + 1]
+    else:
+        xd = x.to(device)
+    for k, p in ((100, 1.0), (0, 0.5), (400, 0.5), (900, 0.5)):
+        kw = dict(temperature=1.0, top_k=k, top_p=p, do_sample=True)
+        for off in range(3):
+            out = RI.sample_next_token_batch(xd, seed=17, offset=off, **kw)
+            _check(x, out, seed=17, offset=off, what=f"signed zeros k={k} p={p} off={off}", **kw)
