@@ -258,15 +258,16 @@ def _raise_flags(flags: int, kind: int) -> None:
 def _check_before_sweep(logits: Tensor) -> bool:
     """Whether the single-pass call reads its status before the sweep.
 
-    For float32 and float64 logits every data error is known before the
-    sweep runs: the row coefficients flag empty masks and rrl_check_targets
-    the targets.  The one host synchronisation then waits for those small
-    kernels only, and the host runs ahead of the sweep.  16-bit logits read
-    it after the sweep, because the register-resident kernel may ask for a
+    Every data error is known before the sweep runs: the row coefficients
+    flag empty masks and rrl_check_targets the targets.  The one host
+    synchronisation then waits for those small kernels only, and the host
+    runs ahead of the sweep.  bfloat16 logits read it after the sweep
+    instead: a log-sum-exp beyond 2e38, which only bfloat16's range allows
+    (float16 stops at 65504), makes the register-resident kernel ask for a
     rerun on the generic kernel (FLAG_FAST_RANGE).
     """
 
-    return logits.element_size() >= 4
+    return logits.dtype != torch.bfloat16
 
 
 def _scalar_dtypes(kind: int, cur: Tensor, old: Tensor, adv: Tensor) -> Tuple[torch.dtype, ...]:

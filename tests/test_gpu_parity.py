@@ -231,11 +231,12 @@ def test_check_targets_through_the_c_abi(device, tdtype):
         assert flags(w2[:, 1:T + 1], nll) == want
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16, torch.bfloat16])
 def test_fused_data_errors_raise(device, dtype):
     """Out-of-range targets, an empty mask and SAPO's empty rows raise the
-    reference's errors whether the status is read before the sweep (float32
-    and float64 logits) or after it (16-bit); a valid call right after works."""
+    reference's errors whether the status is read before the sweep (float32,
+    float64, float16 logits) or after it (bfloat16); a valid call right after
+    works."""
 
     B, T, V = 4, 6, 4096
     x, t, old, adv, mask = _fused_inputs(71, B, T, V, dtype)
