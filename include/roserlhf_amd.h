@@ -73,7 +73,8 @@ enum rrl_flag {
   RRL_FLAG_FAST_RANGE = 16,      /* rrl_fused_logprob_policy's 16-bit register-resident kernel met a
                                     row with finite |log-sum-exp| > 2e38, outside its exponent range;
                                     that call's outputs are undefined: rerun it with
-                                    RRL_POLICY_GENERIC set (no reference counterpart) */
+                                    RRL_POLICY_GENERIC set, or queue a rerun with
+                                    RRL_POLICY_RERUN_FAST_RANGE (no reference counterpart) */
   RRL_FLAG_BAD_PROBS = 32        /* rrl_sample_logprobs: a row holds NaN or +inf logits (torch.multinomial
                                     rejects such probabilities, roseinfer/engine.py:1155,1169) */
 };
@@ -85,7 +86,13 @@ enum rrl_policy_flag {
                                  is not read; its dlogits row is written as zeros and its logp /
                                  lse as 0 (equal to the reference for finite logits, where such a
                                  row contributes exactly 0; no reference counterpart) */
-  RRL_POLICY_SUM = 4          /* RRL_OBJ_NLL: reduction "sum" instead of "mean" */
+  RRL_POLICY_SUM = 4,         /* RRL_OBJ_NLL: reduction "sum" instead of "mean" */
+  RRL_POLICY_RERUN_FAST_RANGE = 8 /* rrl_fused_logprob_policy: launch the generic row kernel as a
+                                 conditional rerun of the call just made with the same arguments
+                                 on the same stream and status word (status required): its
+                                 workgroups return at once unless the status word holds
+                                 RRL_FLAG_FAST_RANGE, so a caller need not read the status between
+                                 the two launches (no reference counterpart) */
 };
 
 /* Policy objectives (losses.py). */

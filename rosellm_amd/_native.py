@@ -45,6 +45,7 @@ FLAG_BAD_PROBS = 32
 POLICY_GENERIC = 1
 POLICY_SKIP_MASKED = 2
 POLICY_SUM = 4
+POLICY_RERUN_FAST_RANGE = 8
 
 # rrl_objective
 OBJ_PPO, OBJ_SAO, OBJ_GSPO, OBJ_GSPO_TOKEN, OBJ_SAPO, OBJ_NLL = range(6)
@@ -165,8 +166,12 @@ def _event() -> "torch.cuda.Event":
     return _event_pool.pop() if _event_pool else torch.cuda.Event(enable_timing=True)
 
 
-def call(name: str, *args) -> None:
-    events = _timed.get(name) if _timed else None
+def call(name: str, *args, timed: bool = True) -> None:
+    """Call an entry point and raise on a non-zero return code.  ``timed=False``
+    keeps the call out of ``time_calls``' records: a launch that is not the
+    entry point's own work (the conditional rerun behind a single-pass sweep)."""
+
+    events = _timed.get(name) if _timed and timed else None
     if events is not None:
         start = _event()
         start.record()

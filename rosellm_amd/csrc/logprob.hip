@@ -29,6 +29,12 @@ __global__ __launch_bounds__(NT) void row_kernel(RowArgs a) {
   __shared__ Acc sh_s[NT / 64];
 
   const int64_t rows = a.B * a.T;
+  // A conditional rerun (RRL_POLICY_RERUN_FAST_RANGE) does the call again
+  // only when the register-resident launch before it flagged a row outside
+  // its exponent range; otherwise every workgroup returns here.
+  if (MODE == MODE_FUSED && (a.pp.flags & RRL_POLICY_RERUN_FAST_RANGE) &&
+      (*static_cast<const volatile int32_t*>(a.status) & RRL_FLAG_FAST_RANGE) == 0)
+    return;
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     const int64_t b = r / a.T, t = r - (r / a.T) * a.T;
     const S* row = static_cast<const S*>(a.logits) + b * a.ls_b + t * a.ls_t;
@@ -125,7 +131,11 @@ int launch_row(const RowArgs& a, hipStream_t stream) {
   constexpr int NT = 256;
   const int64_t rows = a.B * a.T;
   if (rows == 0) return RRL_OK;
-  const int64_t grid = rows < (int64_t)(1 << 30) ? rows : (int64_t)(1 << 30);
+  // A conditional rerun mostly returns at once: a grid of 2048 workgroups
+  // keeps that launch short and still streams every row when it does run.
+  const int64_t cap = (MODE == MODE_FUSED && (a.pp.flags & RRL_POLICY_RERUN_FAST_RANGE))
+                          ? (int64_t)2048 : (int64_t)(1 << 30);
+  const int64_t grid = rows < cap ? rows : cap;
   hipLaunchKernelGGL((row_kernel<Tag, MODE, NT>), dim3((unsigned)grid), dim3(NT), 0, stream, a);
   return check_launch("row_kernel");
 }
@@ -252,6 +262,11 @@ extern "C" int rrl_fused_logprob_policy(const rrl_policy_params* params, const v
   a.dl = dlogits; a.dl_dt = dl_dtype; a.ds_b = ds_b; a.ds_t = ds_t;
   a.pp = *params; a.old = to_view(old); a.adv = to_view(adv); a.mask = to_view(mask);
   a.row_coef = row_coef; a.records = records; a.status = status;
+  if (params->flags & RRL_POLICY_RERUN_FAST_RANGE) {
+    RRL_REQUIRE(status != nullptr, RRL_EINVAL,
+                "RRL_POLICY_RERUN_FAST_RANGE needs the first call's status word");
+    return dispatch_row<MODE_FUSED>(a, logits_dtype, as_stream(stream));
+  }
   bool launched = false;
   rc = maybe_launch_resident(a, 2, logits_dtype, as_stream(stream), &launched);
   if (rc || launched) return rc;

@@ -255,19 +255,33 @@ def _raise_flags(flags: int, kind: int) -> None:
         raise ValueError("cannot reduce an empty mask")
 
 
-def _check_before_sweep(logits: Tensor) -> bool:
+def _check_before_sweep(logits: Tensor, inplace: bool) -> bool:
     """Whether the single-pass call reads its status before the sweep.
 
     Every data error is known before the sweep runs: the row coefficients
     flag empty masks and rrl_check_targets the targets.  The one host
     synchronisation then waits for those small kernels only, and the host
-    runs ahead of the sweep.  bfloat16 logits read it after the sweep
-    instead: a log-sum-exp beyond 2e38, which only bfloat16's range allows
-    (float16 stops at 65504), makes the register-resident kernel ask for a
-    rerun on the generic kernel (FLAG_FAST_RANGE).
+    runs ahead of the sweep.  A log-sum-exp beyond 2e38, which only
+    bfloat16's range allows (float16 stops at 65504), makes the
+    register-resident kernel flag FAST_RANGE instead; a conditional generic
+    launch queued behind it (_rerun_on_device) redoes the call on the GPU in
+    that case.  In place the logits are gone by then, so bfloat16 in place
+    reads the status after the sweep and raises.
     """
 
-    return logits.dtype != torch.bfloat16
+    return logits.dtype != torch.bfloat16 or not inplace
+
+
+def _rerun_on_device(logits: Tensor, inplace: bool) -> bool:
+    """Whether the single-pass call queues RRL_POLICY_RERUN_FAST_RANGE."""
+
+    return logits.dtype == torch.bfloat16 and not inplace
+
+
+def _rerun_params(params):
+    p = nat.RrlPolicyParams.from_buffer_copy(params)
+    p.flags |= nat.POLICY_RERUN_FAST_RANGE
+    return p
 
 
 def _scalar_dtypes(kind: int, cur: Tensor, old: Tensor, adv: Tensor) -> Tuple[torch.dtype, ...]:
@@ -799,7 +813,8 @@ class _FusedPolicy(torch.autograd.Function):
         trusted = torch.empty(B * T if kind == nat.OBJ_SAO else 0, dtype=torch.bool, device=dev)
         lview = nat.RrlView(logp.data_ptr(), acc_code, T, 1)
 
-        early = _check_before_sweep(logits)
+        early = _check_before_sweep(logits, inplace)
+        rerun = _rerun_on_device(logits, inplace)
 
         def run(p):
             status = nat.new_status(dev)
@@ -809,10 +824,12 @@ class _FusedPolicy(torch.autograd.Function):
             if early:
                 nat.call("rrl_check_targets", pref, B, T, V, tview, status.data_ptr(), stream)
                 _raise_flags(nat.read_status(status), kind)
-            nat.call("rrl_fused_logprob_policy", pref, x.data_ptr(), nat.dtype_code(x.dtype), B,
-                     T, V, s_b, s_t, tview, ov, av, mv, coef.data_ptr(), records.data_ptr(),
-                     logp.data_ptr(), lse.data_ptr(), dl.data_ptr(),
-                     nat.dtype_code(logits.dtype), d_b, d_t, status.data_ptr(), stream)
+            for q in (pref, ctypes_ref(_rerun_params(p))) if rerun else (pref,):
+                nat.call("rrl_fused_logprob_policy", q, x.data_ptr(), nat.dtype_code(x.dtype),
+                         B, T, V, s_b, s_t, tview, ov, av, mv, coef.data_ptr(),
+                         records.data_ptr(), logp.data_ptr(), lse.data_ptr(), dl.data_ptr(),
+                         nat.dtype_code(logits.dtype), d_b, d_t, status.data_ptr(), stream,
+                         timed=q is pref)
             nat.call("rrl_policy_fwd", pref, B, T, lview, ov, av, mv, acc_code, ws.data_ptr(),
                      scal.data_ptr(), None, nat.ptr(trusted) if trusted.numel() else None,
                      status.data_ptr(), stream)

@@ -116,7 +116,8 @@ class _CrossEntropyRows(torch.autograd.Function):
             dptr = dl.data_ptr()
         lview = nat.RrlView(logp.data_ptr(), acc_code, T, 1)
 
-        early = _losses._check_before_sweep(logits)
+        early = _losses._check_before_sweep(logits, inplace)
+        rerun = _losses._rerun_on_device(logits, inplace)
 
         def run(p):
             status = nat.new_status(dev)
@@ -126,10 +127,12 @@ class _CrossEntropyRows(torch.autograd.Function):
             if early:
                 nat.call("rrl_check_targets", pref, B, T, V, tview, status.data_ptr(), stream)
                 _losses._raise_flags(nat.read_status(status), nat.OBJ_NLL)
-            nat.call("rrl_fused_logprob_policy", pref, x.data_ptr(), nat.dtype_code(x.dtype), B,
-                     T, V, s_b, s_t, tview, unused, unused, tview, coef.data_ptr(),
-                     records.data_ptr(), logp.data_ptr(), lse.data_ptr(), dptr,
-                     nat.dtype_code(logits.dtype), d_b, d_t, status.data_ptr(), stream)
+            for q in (pref, _losses.ctypes_ref(_losses._rerun_params(p))) if rerun else (pref,):
+                nat.call("rrl_fused_logprob_policy", q, x.data_ptr(), nat.dtype_code(x.dtype), B,
+                         T, V, s_b, s_t, tview, unused, unused, tview, coef.data_ptr(),
+                         records.data_ptr(), logp.data_ptr(), lse.data_ptr(), dptr,
+                         nat.dtype_code(logits.dtype), d_b, d_t, status.data_ptr(), stream,
+                         timed=q is pref)
             nat.call("rrl_policy_fwd", pref, B, T, lview, unused, unused, tview, acc_code,
                      ws.data_ptr(), scal.data_ptr(), None, None, status.data_ptr(), stream)
             return 0 if early else nat.read_status(status)

@@ -234,9 +234,9 @@ def test_check_targets_through_the_c_abi(device, tdtype):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16, torch.bfloat16])
 def test_fused_data_errors_raise(device, dtype):
     """Out-of-range targets, an empty mask and SAPO's empty rows raise the
-    reference's errors whether the status is read before the sweep (float32,
-    float64, float16 logits) or after it (bfloat16); a valid call right after
-    works."""
+    reference's errors whether the status is read before the sweep (every
+    dtype out of place) or after it (bfloat16 in place); a valid call right
+    after works."""
 
     B, T, V = 4, 6, 4096
     x, t, old, adv, mask = _fused_inputs(71, B, T, V, dtype)
@@ -246,6 +246,8 @@ def test_fused_data_errors_raise(device, dtype):
         bad[2, 3] = badv
         with pytest.raises(RuntimeError, match="out of bounds"):
             R.fused_policy_loss(d(x), d(bad), d(old), d(adv), d(mask))
+        with pytest.raises(RuntimeError, match="out of bounds"):
+            R.fused_policy_loss(d(x), d(bad), d(old), d(adv), d(mask), inplace=True)
     with pytest.raises(ValueError, match="empty mask"):
         R.fused_policy_loss(d(x), d(t), d(old), d(adv), d(torch.zeros_like(mask)))
     rows = mask.clone()
@@ -714,8 +716,9 @@ def test_fused_many_rows_persistent(device, dtype, objective):
 def test_fused_extreme_logits(device):
     """Rows at the edge of the 16-bit range: an all -inf row but one entry, a
     half -inf (masked vocabulary) row, and a row whose log-sum-exp (3e38)
-    exceeds the register-resident kernel's exponent range, which the host then
-    reruns on the generic kernel.  All must match the float64 oracle."""
+    exceeds the register-resident kernel's exponent range, which the generic
+    kernel launched behind it (RRL_POLICY_RERUN_FAST_RANGE) then redoes on the
+    device.  All must match the float64 oracle."""
 
     B, T, V = 4, 8, 4096
     x, t, old, adv, mask = _fused_inputs(35, B, T, V, torch.bfloat16)
@@ -744,6 +747,29 @@ def test_fused_extreme_logits(device):
     assert abs(out.loss.item() - out_o["loss"].item()) <= 2e-3 * scale
     assert _ulp16(xd.grad, dlo, "dlogits") > 0.98
     _rownorm16(xd.grad, dlo, 2e-3, "dlogits")
+
+
+@pytest.mark.parametrize("V", [4096, 151936])
+def test_fused_rerun_only_when_flagged(device, V):
+    """The conditional generic launch queued behind an out-of-place bfloat16
+    sweep returns at once when no row was flagged: log-probs, loss and
+    dlogits equal the register-resident kernel's own (an in-place call, which
+    queues no rerun) bit for bit."""
+
+    print(f"[rerun-if-flagged] V={V}", flush=True)
+    B, T = 4, 8
+    x, t, old, adv, mask = _fused_inputs(73, B, T, V, torch.bfloat16)
+    d = lambda v: v.to(device)  # noqa: E731
+    kw = dict(clip_low=0.2, clip_high=0.28, return_logprobs=True)
+    xd = d(x).requires_grad_()
+    out, lp = R.fused_policy_loss(xd, d(t), d(old), d(adv), d(mask), **kw)
+    out.loss.backward()
+    buf = d(x).detach()
+    out_i, lp_i = R.fused_policy_loss(buf.requires_grad_(), d(t), d(old), d(adv), d(mask),
+                                      inplace=True, **kw)
+    assert torch.equal(lp, lp_i)
+    _close(out_i.loss, out.loss, 1e-6, 1e-8, "loss")
+    assert torch.equal(buf.detach(), xd.grad), "dlogits differ from the resident kernel's"
 
 
 @pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 151936), (torch.bfloat16, 20000),
