@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define RRL_ABI_VERSION 3
+#define RRL_ABI_VERSION 4
 
 #if defined(__GNUC__)
 #define RRL_API __attribute__((visibility("default")))
