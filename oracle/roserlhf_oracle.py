@@ -288,12 +288,21 @@ def leave_one_out(rewards: Tensor, *, dim: int = -1) -> Tensor:
 
 
 def group_standardize(rewards: Tensor, *, dim: int = -1, eps: float = 1e-8) -> Tensor:
-    """(r - mean) / max(std_pop, eps), zero where std_pop <= eps (advantages.py:236-258)."""
+    """(r - mean) / max(std_pop, eps), zero where std_pop <= eps (advantages.py:236-258).
+
+    A uniform group (max == min) has std 0 exactly, the contract the
+    reference's docstring states (advantages.py:243-244).  torch's vectorised
+    CPU ``std`` leaves a few 1e-8 on uniform groups of 8 or more non-dyadic
+    values (e.g. 8 x 0.3 gives 2.98e-8 > eps = 1e-8, hence +-1 outputs); that
+    rounding artefact is not reproduced.
+    """
 
     if rewards.shape[dim] < 2:
         raise ValueError("group standardization requires group_size >= 2")
     mu = rewards.mean(dim=dim, keepdim=True)
     sd = rewards.std(dim=dim, unbiased=False, keepdim=True)
+    uniform = rewards.amax(dim=dim, keepdim=True) == rewards.amin(dim=dim, keepdim=True)
+    sd = torch.where(uniform, torch.zeros_like(sd), sd)
     z = (rewards - mu) / sd.clamp_min(eps)
     return torch.where(sd > eps, z, torch.zeros_like(z))
 

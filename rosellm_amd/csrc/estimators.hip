@@ -196,14 +196,23 @@ __global__ void group_std_kernel(int64_t n, int64_t G, View r, Acc eps, void* ou
   for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < n;
        gi += (int64_t)gridDim.x * blockDim.x) {
     Acc sum = Acc(0);
-    for (int64_t k = 0; k < G; ++k) sum += r.get<Acc>(gi, k);
+    Acc lo = r.get<Acc>(gi, 0), hi = lo;
+    for (int64_t k = 0; k < G; ++k) {
+      const Acc x = r.get<Acc>(gi, k);
+      sum += x;
+      lo = x < lo ? x : lo;
+      hi = x > hi ? x : hi;
+    }
     const Acc mean = sum / (Acc)G;
     Acc ss = Acc(0);
     for (int64_t k = 0; k < G; ++k) {
       const Acc d = r.get<Acc>(gi, k) - mean;
       ss += d * d;
     }
-    const Acc sd = M<Acc>::sqrt(ss / (Acc)G);
+    // A uniform group has std 0 exactly ("uniform-reward groups return exactly
+    // zero", advantages.py:243-244): the float mean of a non-dyadic value is
+    // often an ulp off, which would otherwise leave a std above eps.
+    const Acc sd = hi == lo ? Acc(0) : M<Acc>::sqrt(ss / (Acc)G);
     const Acc den = sd > eps ? sd : eps;  // clamp_min(eps) (advantages.py:257)
     for (int64_t k = 0; k < G; ++k) {
       const Acc z = (r.get<Acc>(gi, k) - mean) / den;

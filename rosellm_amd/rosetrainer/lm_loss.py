@@ -152,7 +152,14 @@ class _CrossEntropyRows(torch.autograd.Function):
         if shift and logits.shape[1] > 0:
             dl[:, -1].zero_()  # the last position predicts nothing
         del keep0, tkeep
+        # Row geometry of the whole gradient tensor for the backward's rescale:
+        # in place it is the caller's logits, which may be a strided view (a
+        # padded-vocabulary slice, a [:, :-1] shift) whose rows are not V apart.
+        gx, gB, gT, gV, gs_b, gs_t = nat.logits_rows(dl)
+        if gx.data_ptr() != dl.data_ptr():
+            raise RuntimeError("cross-entropy gradient rows cannot be addressed in place")
         ctx.dl = dl
+        ctx.geom = (gB, gT, gV, gs_b, gs_t)
         ctx.set_materialize_grads(False)
         return -scal[0]
 
@@ -162,10 +169,9 @@ class _CrossEntropyRows(torch.autograd.Function):
         ctx.dl = None
         if g is None or dl is None or not ctx.needs_input_grad[3]:
             return None, None, None, None, None
-        V = dl.shape[-1]
-        rows = dl.numel() // V if V else 0
+        B, T, V, s_b, s_t = ctx.geom
         scale = g.reshape(1).to(torch.float64 if dl.dtype == torch.float64 else torch.float32)
-        nat.call("rrl_scale_rows", dl.data_ptr(), nat.dtype_code(dl.dtype), 1, rows, V, 0, V,
+        nat.call("rrl_scale_rows", dl.data_ptr(), nat.dtype_code(dl.dtype), B, T, V, s_b, s_t,
                  scale.data_ptr(), nat.dtype_code(scale.dtype), 1.0, nat.stream_ptr(dl.device))
         return None, None, None, dl, None
 

@@ -109,6 +109,9 @@ def test_group_estimators_sweep(device, i):
     r[0] = 1.0  # a uniform group
     if G > 2:
         r[1] = torch.randint(0, 2, (n,), generator=g).to(dt)  # binary rewards
+        # uniform groups of non-dyadic values: exactly zero, whose float mean
+        # is often an ulp off the value itself
+        r[2] = [0.1, 0.3, 0.7][i % 3]
     x = r if dim == -1 else r.t().contiguous()
     if n < 2:  # the reference's rule (advantages.py:230-231, 250-251)
         with pytest.raises(ValueError, match="group standardization requires group_size >= 2"):
@@ -119,6 +122,9 @@ def test_group_estimators_sweep(device, i):
     got = R.group_standardized_advantages(x.to(device), dim=dim)
     want = o.group_standardize(x, dim=dim)
     _close(got, want, *_tol(want, dt), "group standardize")
+    uni = [0, 2] if G > 2 else [0]
+    got_rows = got.cpu() if dim == -1 else got.cpu().t()
+    assert (got_rows[uni] == 0).all(), "a uniform group must standardize to exactly zero"
     got = R.leave_one_out_advantages(x.to(device), dim=dim)
     want = o.leave_one_out(x, dim=dim)
     _close(got, want, *_tol(want, dt), "leave one out")

@@ -157,6 +157,43 @@ def test_inplace_and_upstream_scale(device):
     assert torch.equal(buf.detach(), a.grad), "in-place gradient differs"
 
 
+@pytest.mark.parametrize("layout", ["padded_vocab", "shifted_rows"])
+def test_inplace_strided_views_upstream_scale(device, layout):
+    """In place on a strided view, with an upstream gradient of 2.5: every
+    gradient row of the view is the unscaled in-place gradient (same view,
+    same kernel) times 2.5, rounded once to bf16; the unscaled gradient
+    matches the out-of-place one; memory outside the view is untouched."""
+
+    print(f"[sft-inplace-strided] layout={layout}", flush=True)
+    g = _gen(107)
+    B, T, V, PAD = 3, 40, 4104, 56
+    full = (torch.randn(B, T, V + PAD, generator=g) * 3.0).to(torch.bfloat16)
+    y = _labels(g, (B, T), V)
+
+    def view_of(buf):
+        return buf[..., :V] if layout == "padded_vocab" else buf[:, :-1, :V]
+
+    lab = (y if layout == "padded_vocab" else y[:, 1:]).to(device)
+    grads = []
+    for upstream in (1.0, 2.5):
+        buf = full.to(device)
+        leaf = view_of(buf).detach().requires_grad_()
+        (upstream * RT.cross_entropy(leaf, lab, inplace=True)).backward()
+        torch.cuda.synchronize()
+        grads.append(leaf.detach().clone())
+        host = buf.cpu()
+        assert torch.equal(host[..., V:], full[..., V:]), "padding columns were written"
+        if layout == "shifted_rows":
+            assert torch.equal(host[:, -1], full[:, -1]), "rows outside the view were written"
+    g1, g25 = grads
+    assert torch.equal(g25, (g1.float() * 2.5).to(torch.bfloat16)), "rows scaled wrongly"
+    a = view_of(full).contiguous().to(device).requires_grad_()
+    RT.cross_entropy(a, lab).backward()
+    # another kernel variant (rows off 128-byte boundaries): within one bf16 ulp
+    same = _ulp16(g1, a.grad.float(), "in place vs out of place")
+    assert same >= 0.98, same
+
+
 @pytest.mark.parametrize("row_block", [64, 4096])
 def test_linear_causal_lm_loss(device, row_block):
     """LM head + shift + cross-entropy without logits: loss vs the float64

@@ -273,6 +273,21 @@ def test_gspo_equals_gspo_token_for_uniform_advantages():
     torch.testing.assert_close(c1.grad, c2.grad)
 
 
+def test_group_uniform_float32_groups_are_zero():
+    """Uniform groups of non-dyadic float32 values standardize to exactly 0
+    (advantages.py:243-244), for every group size; the float64 scalar loop
+    agrees (its mean of a uniform group is exact)."""
+
+    for v in (0.1, 0.3, 0.7, 1.0):
+        for G in (2, 3, 4, 8, 16, 33, 64):
+            r = torch.full((3, G), v, dtype=torch.float32)
+            r[1] = torch.linspace(-1, 1, G)
+            z = o.group_standardize(r)
+            assert torch.equal(z[0], torch.zeros(G)) and torch.equal(z[2], torch.zeros(G))
+            np.testing.assert_allclose(z.double().numpy(), brute.group_standardize(r.double()),
+                                       rtol=1e-6, atol=1e-6)
+
+
 def test_group_shift_invariance():
     """derivations-and-code.md:1168: adding a constant leaves centered advantages unchanged."""
 
