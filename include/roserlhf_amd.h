@@ -236,6 +236,23 @@ RRL_API int rrl_fused_logprob_policy(const rrl_policy_params* params, const void
                              int32_t dl_dtype, int64_t ds_b, int64_t ds_t,
                              int32_t* status, void* stream);
 
+/* rrl_fused_logprob_policy without the records workspace: no counterpart in
+ * the reference.  It is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The per-token records live in a static device array of
+ * RRL_NOALLOC_MAX_TOKENS x 16 bytes (16 MiB), one copy per GPU, held until the
+ * process ends; B*T above RRL_NOALLOC_MAX_TOKENS returns RRL_EINVAL.  Every
+ * call on one GPU shares that array: calls that overlap on one GPU (two
+ * streams, two threads) race and must be serialised by the caller.  Arguments
+ * and results are those of rrl_fused_logprob_policy; nothing is allocated. */
+#define RRL_NOALLOC_MAX_TOKENS (1 << 20)
+RRL_API int rrl_fused_logprob_policy_noalloc(const rrl_policy_params* params,
+                             const void* logits, int32_t logits_dtype, int64_t B, int64_t T,
+                             int64_t V, int64_t ls_b, int64_t ls_t, rrl_view targets,
+                             rrl_view old, rrl_view adv, rrl_view mask, const void* row_coef,
+                             void* logp_out, void* lse_out, void* dlogits, int32_t dl_dtype,
+                             int64_t ds_b, int64_t ds_t, int32_t* status, void* stream);
+
 /* ---- a4, a9: masked_mean (losses.py:41-50), sequence_log_ratio (:489-512)
  * masked_mean: out = acc[1] = sum(values * w) / sum(w), w = mask cast to the
  * value dtype; flags EMPTY_MASK.  The workspace keeps the denominator for the

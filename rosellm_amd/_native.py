@@ -97,6 +97,7 @@ SIGNATURES = {
     "rrl_fused_records_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "rrl_check_targets": (ctypes.c_int, [_PP, _I64, _I64, _I64, _V, _P, _P]),
     "rrl_fused_logprob_policy": (ctypes.c_int, [_PP, _P, _I32, _I64, _I64, _I64, _I64, _I64, _V, _V, _V, _V, _P, _P, _P, _P, _P, _I32, _I64, _I64, _P, _P]),
+    "rrl_fused_logprob_policy_noalloc": (ctypes.c_int, [_PP, _P, _I32, _I64, _I64, _I64, _I64, _I64, _V, _V, _V, _V, _P, _P, _P, _P, _I32, _I64, _I64, _P, _P]),
     "rrl_reduce_workspace_bytes": (ctypes.c_size_t, [_I64]),
     "rrl_masked_mean_fwd": (ctypes.c_int, [_I64, _I64, _V, _V, _I32, _P, _P, _P, _P]),
     "rrl_masked_mean_bwd": (ctypes.c_int, [_I64, _I64, _V, _I32, _P, _P, _P, _P]),

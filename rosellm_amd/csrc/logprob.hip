@@ -10,6 +10,8 @@
 // bf16, f16 and float32 rows up to 163840 (16-bit) or 81920 (float32) entries;
 // this file is the generic path for float64, longer rows, accumulation and
 // dlogits rows laid out differently from the logits rows.
+#include <mutex>
+
 #include "policy_math.hpp"
 #include "rrl_common.hpp"
 #include "row_common.hpp"
@@ -229,15 +231,14 @@ extern "C" int rrl_logprob_bwd(const void* logits, int32_t logits_dtype, int64_t
   return dispatch_row<MODE_BWD>(a, logits_dtype, as_stream(stream));
 }
 
-extern "C" int rrl_fused_logprob_policy(const rrl_policy_params* params, const void* logits,
-                                        int32_t logits_dtype, int64_t B, int64_t T, int64_t V,
-                                        int64_t ls_b, int64_t ls_t, rrl_view targets,
-                                        rrl_view old, rrl_view adv, rrl_view mask,
-                                        const void* row_coef, void* records, void* logp_out,
-                                        void* lse_out, void* dlogits, int32_t dl_dtype,
-                                        int64_t ds_b, int64_t ds_t, int32_t* status,
-                                        void* stream) {
-  clear_error();
+namespace {
+
+int fused_logprob_policy(const rrl_policy_params* params, const void* logits,
+                         int32_t logits_dtype, int64_t B, int64_t T, int64_t V, int64_t ls_b,
+                         int64_t ls_t, rrl_view targets, rrl_view old, rrl_view adv,
+                         rrl_view mask, const void* row_coef, void* records, void* logp_out,
+                         void* lse_out, void* dlogits, int32_t dl_dtype, int64_t ds_b,
+                         int64_t ds_t, int32_t* status, void* stream) {
   RRL_REQUIRE(params != nullptr, RRL_EINVAL, "params is null");
   RRL_REQUIRE(params->kind == RRL_OBJ_PPO || params->kind == RRL_OBJ_SAO ||
                   params->kind == RRL_OBJ_SAPO || params->kind == RRL_OBJ_NLL,
@@ -271,6 +272,73 @@ extern "C" int rrl_fused_logprob_policy(const rrl_policy_params* params, const v
   rc = maybe_launch_resident(a, 2, logits_dtype, as_stream(stream), &launched);
   if (rc || launched) return rc;
   return dispatch_row<MODE_FUSED>(a, logits_dtype, as_stream(stream));
+}
+
+// Records of rrl_fused_logprob_policy_noalloc: a file-scope device array, one
+// copy per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not a device
+// address); it passes the address hipGetSymbolAddress returns for the current
+// device, looked up once per device and kept in g_scratch_addr.
+static __device__ __align__(256) TokenRecord scratch[RRL_NOALLOC_MAX_TOKENS];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+int scratch_of_current_device(void** out) {
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  RRL_REQUIRE(e == hipSuccess, RRL_ELAUNCH,
+              std::string("hipGetDevice: ") + hipGetErrorString(e));
+  RRL_REQUIRE(dev >= 0 && dev < kMaxDevices, RRL_EINVAL, "device ordinal out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t se = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    RRL_REQUIRE(se == hipSuccess && p != nullptr, RRL_ELAUNCH,
+                std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(se));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return RRL_OK;
+}
+
+}  // namespace
+
+extern "C" int rrl_fused_logprob_policy(const rrl_policy_params* params, const void* logits,
+                                        int32_t logits_dtype, int64_t B, int64_t T, int64_t V,
+                                        int64_t ls_b, int64_t ls_t, rrl_view targets,
+                                        rrl_view old, rrl_view adv, rrl_view mask,
+                                        const void* row_coef, void* records, void* logp_out,
+                                        void* lse_out, void* dlogits, int32_t dl_dtype,
+                                        int64_t ds_b, int64_t ds_t, int32_t* status,
+                                        void* stream) {
+  clear_error();
+  return fused_logprob_policy(params, logits, logits_dtype, B, T, V, ls_b, ls_t, targets, old,
+                              adv, mask, row_coef, records, logp_out, lse_out, dlogits, dl_dtype,
+                              ds_b, ds_t, status, stream);
+}
+
+extern "C" int rrl_fused_logprob_policy_noalloc(
+    const rrl_policy_params* params, const void* logits, int32_t logits_dtype, int64_t B,
+    int64_t T, int64_t V, int64_t ls_b, int64_t ls_t, rrl_view targets, rrl_view old,
+    rrl_view adv, rrl_view mask, const void* row_coef, void* logp_out, void* lse_out,
+    void* dlogits, int32_t dl_dtype, int64_t ds_b, int64_t ds_t, int32_t* status,
+    void* stream) {
+  clear_error();
+  RRL_REQUIRE(B >= 0 && T >= 0, RRL_EINVAL, "negative size");
+  RRL_REQUIRE(B * T <= (int64_t)RRL_NOALLOC_MAX_TOKENS, RRL_EINVAL,
+              "rrl_fused_logprob_policy_noalloc: B*T = " + std::to_string(B * T) +
+                  " tokens exceeds the static scratch of " +
+                  std::to_string((int64_t)RRL_NOALLOC_MAX_TOKENS) +
+                  " tokens; call rrl_fused_logprob_policy with a records workspace");
+  void* records = nullptr;
+  if (int rc = scratch_of_current_device(&records)) return rc;
+  // Every record a sweep reads is written first by the same call's packing
+  // kernel, so nothing in the array needs clearing between calls.
+  return fused_logprob_policy(params, logits, logits_dtype, B, T, V, ls_b, ls_t, targets, old,
+                              adv, mask, row_coef, records, logp_out, lse_out, dlogits, dl_dtype,
+                              ds_b, ds_t, status, stream);
 }
 
 extern "C" size_t rrl_fused_records_bytes(int64_t B, int64_t T) {
