@@ -75,8 +75,13 @@ enum rrl_flag {
                                     that call's outputs are undefined: rerun it with
                                     RRL_POLICY_GENERIC set, or queue a rerun with
                                     RRL_POLICY_RERUN_FAST_RANGE (no reference counterpart) */
-  RRL_FLAG_BAD_PROBS = 32        /* rrl_sample_logprobs: a row holds NaN or +inf logits (torch.multinomial
+  RRL_FLAG_BAD_PROBS = 32,       /* rrl_sample_logprobs: a row holds NaN or +inf logits (torch.multinomial
                                     rejects such probabilities, roseinfer/engine.py:1155,1169) */
+  RRL_FLAG_LM_RANGE = 64         /* rrl_lm_head_fwd without mref_in: a token's logits rose more than 64
+                                    above its first 32-column tile maximum + 24, outside the fixed
+                                    reference point's exponent range; that token's outputs are
+                                    undefined: rerun with mref_in = the log-sum-exp of an LSE-only
+                                    call (no reference counterpart) */
 };
 
 /* rrl_policy_params.flags bits. */
@@ -316,6 +321,49 @@ RRL_API int rrl_broadcast_turn(int64_t B, int64_t K, int64_t T, rrl_view turn_ad
 RRL_API int rrl_masked_whiten(int64_t B, int64_t T, rrl_view x, rrl_view mask, double eps,
                       int32_t shift_mean, int32_t acc_dtype, void* workspace, void* out,
                       int32_t out_dtype, int32_t* status, void* stream);
+
+/* ---- fused LM head + token log-probs (rosetrainer/model.py:641,
+ * rosetrainer/qwen3.py:556 feeding losses.py:14-38), on the matrix cores ----
+ * The reference forms logits = hidden @ weight^T as a [N, V] tensor, then
+ * log_softmax + gather, and autograd's backward forms the [N, V] dlogits and
+ * the two products dlogits @ weight, dlogits^T @ hidden.  These entry points
+ * never hold more than a 32 x 64 logits tile (registers and LDS):
+ *   hidden: [N, H] rows h_ld elements apart; weight: [V, H] rows w_ld apart;
+ *   both BF16 (dtype RRL_BF16), 16-byte aligned, H a multiple of 128 up to 1024,
+ *   row strides multiples of 8 elements.  targets: contiguous int32 [N]
+ *   (a negative id: no target, logp 0 and no gradient, as cross-entropy's
+ *   ignore_index; the caller range-checks ids with rrl_check_targets).
+ * rrl_lm_head_fwd writes lse_out and logp_out (float32 [N]) and, when obar is
+ * not NULL, obar[n] = sum_{v != target} p_nv weight[v] (float32 [N, H], row
+ * stride obar_ld): the softmax-weighted weight rows the backward's dhidden
+ * needs, from the same pass (flash-attention-style online softmax).  Without
+ * obar only the log-sum-exp is formed (half the MFMA work).  A target id >= V
+ * raises TARGET_RANGE; a token whose logits exceed the fixed reference point's
+ * range raises LM_RANGE (rerun with mref_in = the lse of an obar-less call).
+ * mref_in: NULL, or float32 [N] reference points (the rerun). */
+RRL_API int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t dtype, int64_t N,
+                    int64_t H, int64_t V, int64_t h_ld, int64_t w_ld, const int32_t* targets,
+                    const float* mref_in, float* lse_out, float* logp_out, float* obar,
+                    int64_t obar_ld, int32_t* status, void* stream);
+
+/* dhidden[n] = g[n] * ((-expm1(logp[n])) * weight[target[n]] - obar[n]), in the
+ * weight dtype, rows dh_ld apart (the linear map's backward of a1's gradient
+ * g = d loss / d logp, with the target column's 1 - p formed from logp). */
+RRL_API int rrl_lm_head_dhidden(const void* weight, int32_t dtype, int64_t N, int64_t H,
+                    int64_t V, int64_t w_ld, const int32_t* targets, const float* logp,
+                    const float* g, const float* obar, int64_t obar_ld, void* dhidden,
+                    int64_t dh_ld, void* stream);
+
+/* dweight[v] = sum_n g[n] ([v == target[n]] - exp(logit[n, v] - lse[n])) hidden[n],
+ * the logits recomputed tile by tile, float32 accumulation over every token in
+ * registers, written once as float32 or the weight dtype (dw_dtype), rows dw_ld
+ * apart.  records: rrl_lm_head_records_bytes(N) bytes of caller workspace. */
+RRL_API size_t rrl_lm_head_records_bytes(int64_t N);
+RRL_API int rrl_lm_head_dweight(const void* hidden, const void* weight, int32_t dtype,
+                    int64_t N, int64_t H, int64_t V, int64_t h_ld, int64_t w_ld,
+                    const int32_t* targets, const float* lse, const float* logp,
+                    const float* g, void* records, void* dweight, int32_t dw_dtype,
+                    int64_t dw_ld, void* stream);
 
 /* ---- rollout side: next-token sampling with behaviour log-probs -------------
  * Replaces the token choice of roseinfer/engine.py:1103-1171

@@ -40,6 +40,7 @@ FLAG_TARGET_RANGE = 4
 FLAG_INVALID_TURN = 8
 FLAG_FAST_RANGE = 16
 FLAG_BAD_PROBS = 32
+FLAG_LM_RANGE = 64
 
 # rrl_policy_flag
 POLICY_GENERIC = 1
@@ -113,6 +114,10 @@ SIGNATURES = {
     "rrl_masked_whiten": (ctypes.c_int, [_I64, _I64, _V, _V, _D, _I32, _I32, _P, _P, _I32, _P, _P]),
     "rrl_sample_logprobs": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _D, _I64, _D, _I32,
                                            ctypes.c_uint64, ctypes.c_uint64, _P, _P, _P, _P, _P]),
+    "rrl_lm_head_fwd": (ctypes.c_int, [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P, _P]),
+    "rrl_lm_head_dhidden": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P]),
+    "rrl_lm_head_records_bytes": (ctypes.c_size_t, [_I64]),
+    "rrl_lm_head_dweight": (ctypes.c_int, [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32, _I64, _P]),
     "rrl_philox4x32_10": (None, [ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32)]),
 }
 

@@ -28,6 +28,7 @@ SOURCES = [
     "objectives.hip",
     "estimators.hip",
     "sampler.hip",
+    "lm_head.hip",
 ]
 
 ARCH = os.environ.get("ROSELLM_AMD_ARCH", "gfx950")

@@ -1,0 +1,704 @@
+// Fused LM head + token log-probs on the gfx950 matrix cores (MFMA), without
+// the [tokens, vocabulary] logits tensor.
+//
+// The reference forms logits = hidden @ W^T (rosetrainer/model.py:499,641,
+// rosetrainer/qwen3.py:508,556; no bias) and then log_softmax + gather
+// (roserlhf/losses.py:14-38), keeping both [N, V] tensors and their gradient.
+// With p = softmax(hidden_n W^T) and g_n = d loss / d logp_n the gradients are
+//   dhidden_n = g_n (W[a_n] - sum_v p_nv W_v)        (a_n: the token's target)
+//   dW_v      = sum_n g_n ([v == a_n] - p_nv) hidden_n
+// The first sum is an attention-shaped product (queries = hidden, keys =
+// values = W rows), so one streaming pass over the vocabulary computes it
+// together with the log-sum-exp (online softmax, flash-attention style).  The
+// second needs the final log-sum-exp: a mirrored pass streams the tokens past
+// a stationary block of W rows and recomputes each logits tile.  Logits exist
+// only as 32 x 64 tiles in registers and LDS.
+//
+// One kernel template serves both passes.  A workgroup (4 waves, one per SIMD)
+// holds BM = 64 "stationary" rows X (tokens in the forward, vocabulary rows in
+// the dW pass) and streams BN = 32-row tiles of Y (vocabulary rows, tokens).
+// Wave w owns the hidden slice d in [w H/4, (w+1) H/4):
+//   S phase:  S^T_w = Y[:, slice] X[:, slice]^T   (32 x 64 partial, MFMA
+//             16x16x32 with the X fragments held in registers for the whole
+//             pass and Y fragments read from LDS);
+//   exchange: the four partials are summed through LDS; wave w finishes the
+//             16 stationary rows of block w (softmax or gradient weights) and
+//             publishes them as bf16/f16 MFMA A fragments;
+//   acc phase: ACC_w[64 x slice] += P[64 x 32] Y[32 x slice], the Y tile read
+//             transposed from LDS with ds_read_tr16_b64.
+// The MFMA output layout of S^T (rows = tile rows) is already the A-fragment
+// layout of the accumulation product once its k index is taken as
+// {4g..4g+3, 16+4g..16+4g+3} for lane group g; the Y fragments of the
+// accumulation product use the same k order.
+//
+// LDS (H = 1024): two Y tiles of 32 x 1024 (double buffer, 128 KB, 16-byte
+// chunks XOR-swizzled by row so that both the natural and the transposed reads
+// are bank-conflict free), 24 KB of partials, 4 KB of fragments.
+#include <mutex>
+#include <type_traits>
+
+#include "rrl_common.hpp"
+#include "wave_common.hpp"
+
+namespace rrl {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+
+constexpr int kBM = 64;   // stationary rows per workgroup
+constexpr int kBN = 32;   // streamed rows per tile
+constexpr int kNT = 256;  // four waves
+constexpr float kLn2 = 0.69314718055994531f;
+// Reference point of the forward's exponentials.  Row n's weights are
+// exp(s - m_n) with m_n fixed at its first finite tile maximum plus
+// kRefMargin, so the accumulators never need rescaling: values from
+// kRefMargin + 63 below that maximum (negligible next to it) up to
+// kRefHeadroom above it stay inside the float32 / bf16 exponent range.  A row
+// whose logits rise further raises RRL_FLAG_LM_RANGE, and the caller reruns
+// it with the reference taken from an exact log-sum-exp pass (mref_in).
+constexpr float kRefMargin = 24.0f;
+constexpr float kRefHeadroom = 88.0f;
+
+enum { kModeFwd = 0, kModeFwdLseOnly = 1, kModeDw = 2 };
+
+struct TagBF16 {};
+struct TagF16 {};
+
+template <class Tag>
+__device__ __forceinline__ f32x4_t mfma(u32x4 a, u32x4 b, f32x4_t c) {
+  if constexpr (std::is_same<Tag, TagBF16>::value)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// Two floats to one packed 16-bit pair (round to nearest even).
+template <class Tag>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  if constexpr (std::is_same<Tag, TagBF16>::value) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    f16x2_t v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+}
+
+template <class Tag>
+__device__ __forceinline__ float widen(uint16_t h) {
+  if constexpr (std::is_same<Tag, TagBF16>::value) return __uint_as_float((uint32_t)h << 16);
+  else return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Tile rows in LDS are 2H + 48 bytes apart (2H is a multiple of 256, the
+// width of the 64 banks).  Natural reads (16 lanes, 16 consecutive rows, one
+// 16-byte chunk each) land 48 bytes apart modulo 256: 16 distinct bank
+// groups.  Transposed reads (16 lanes, 4 consecutive rows x 32 bytes) cover
+// [48i, 48i + 32) modulo 256: disjoint.  Every address is a per-lane base
+// plus a compile-time offset.
+constexpr int kRowPad = 48;
+
+__device__ __forceinline__ u32x4 lds_load16(const uint8_t* base, uint32_t off) {
+  return *reinterpret_cast<const u32x4*>(base + off);
+}
+__device__ __forceinline__ void lds_store16(uint8_t* base, uint32_t off, u32x4 v) {
+  *reinterpret_cast<u32x4*>(base + off) = v;
+}
+__device__ __forceinline__ uint2 lds_tr16(const uint8_t* base, uint32_t off) {
+  const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4_t*)(reinterpret_cast<uintptr_t>(base + off)));
+  return __builtin_bit_cast(uint2, v);
+}
+
+// Row exchange between the four 16-lane groups (lanes c, c+16, c+32, c+48).
+__device__ __forceinline__ float xor16(float v) { return __shfl_xor(v, 16, 64); }
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+struct LmArgs {
+  const void* x;  // stationary rows [nx, H], row stride x_ld elements
+  int64_t x_ld;
+  int32_t nx;
+  const void* y;  // streamed rows [ny, H], row stride y_ld elements
+  int64_t y_ld;
+  int32_t ny;
+  int32_t V;             // vocabulary size
+  const int32_t* tgt;    // forward: target of each stationary row (token), -1 = none
+  float* lse_out;        // forward: [nx]
+  float* logp_out;       // forward: [nx]
+  float* obar;           // forward: sum_{v != a} p_v W_v per token, [nx, H] (ld obar_ld)
+  int64_t obar_ld;
+  const float* mref_in;  // forward: per-token reference point (NULL: first-tile rule)
+  const float4* trec;    // dW pass: per streamed token {target bits, g, lse*log2e, g*(-expm1(logp))}
+  void* dw;              // dW pass: [nx, H] (ld dw_ld), float32 or 16-bit
+  int64_t dw_ld;
+  int32_t dw_f32;
+  int32_t* status;
+};
+
+template <int H>
+struct LdsLayout {
+  static constexpr int kRowBytes = H * 2 + kRowPad;
+  static constexpr int kTileBytes = kBN * kRowBytes;
+  static constexpr int kPartOff = 2 * kTileBytes;                 // [4 writers][3][2 vb][64] x 16 B
+  static constexpr int kPartBytes = 4 * 3 * 2 * 64 * 16;
+  static constexpr int kFragOff = kPartOff + kPartBytes;           // [4 blocks][64] x 16 B
+  static constexpr int kRecOff = kFragOff + 4 * 64 * 16;           // [2][32] x 16 B (dW pass)
+  static constexpr int kTotal = kRecOff + 2 * kBN * 16;            // 163840 at H = 1024
+  static constexpr int kAlphaOff = kPartOff;  // [64] floats, epilogue only (partials unused)
+};
+
+template <class Tag, int MODE, int H>
+__global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
+  constexpr int DW = H / 4;                 // hidden slice per wave
+  constexpr int KS = DW / 32;               // k-steps of the S product per wave
+  constexpr int DB = DW / 16;               // 16-column blocks of the accumulator per wave
+  constexpr int CH = H / 8;                 // 16-byte chunks per row
+  constexpr bool kAcc = MODE != kModeFwdLseOnly;
+  using L = LdsLayout<H>;
+  static_assert(H % 128 == 0 && H <= 1024, "hidden size must be a multiple of 128, at most 1024");
+
+  __shared__ __attribute__((aligned(16))) uint8_t lds[L::kTotal];
+
+  const int tid = threadIdx.x, lane = tid & 63, lg = lane >> 4, lc = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
+  const int32_t x0 = (int32_t)blockIdx.x * kBM;
+  const int dw0 = w * DW;
+
+  // ---- stationary fragments: X[x0 + 16nb + lc][dw0 + 32ks + 8lg .. +7] ----
+  u32x4 xs[4][KS];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const int32_t row = x0 + 16 * nb + lc;
+    const uint16_t* p = static_cast<const uint16_t*>(a.x) + (int64_t)row * a.x_ld + dw0 + 8 * lg;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      xs[nb][ks] = row < a.nx ? *reinterpret_cast<const u32x4*>(p + 32 * ks) : u32x4{0, 0, 0, 0};
+  }
+
+  f32x4_t acc[4][kAcc ? DB : 1];
+  if constexpr (kAcc) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[nb][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Forward row state of stationary row x0 + 16w + lc (replicated over lg).
+  const int32_t my_row = x0 + 16 * w + lc;
+  int32_t tg = -1;
+  if constexpr (MODE != kModeDw) {
+    if (my_row < a.nx) {
+      tg = a.tgt[my_row];
+      if (tg >= a.V) {  // a negative id is "no target" (cross-entropy's ignore_index)
+        raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+        tg = -1;
+      }
+    }
+  }
+  float m_ref = -__builtin_huge_valf(), l_part = 0.f, xa = -__builtin_huge_valf();
+  if constexpr (MODE == kModeFwd) {
+    if (a.mref_in != nullptr && my_row < a.nx) m_ref = a.mref_in[my_row];
+  }
+
+  const int32_t ntiles = (a.ny + kBN - 1) / kBN;
+
+  // ---- tile loads, global -> LDS directly (buffer loads with the LDS bit:
+  // no registers).  One wave-wide load writes 64 consecutive lanes x UNIT
+  // bytes of LDS, so a row (2H bytes, padded rows) is PER_ROW loads; UNIT is
+  // 16 bytes when a row is whole kilobytes, else 4.  The caller waits for
+  // vmcnt(0) before the barrier that publishes the tile. ----
+  constexpr int UNIT = (2 * H) % 1024 == 0 ? 16 : 4;
+  constexpr int PER_ROW = 2 * H / (64 * UNIT);
+  constexpr int WLOADS = kBN * PER_ROW / 4;  // per wave per tile
+  static_assert(kBN * PER_ROW % 4 == 0, "tile load split");
+  typedef __attribute__((address_space(3))) void lds_void_t;
+  auto issue_tile = [&](int32_t t, int buf) {
+    const int32_t r0 = t * kBN;
+    const int32_t rows = a.ny - r0 < kBN ? a.ny - r0 : kBN;
+    const uint16_t* base = static_cast<const uint16_t*>(a.y) + (int64_t)r0 * a.y_ld;
+    // Rows at or past `rows` start at or beyond the descriptor's byte count
+    // (row stride >= H), so they read as zeros.
+    const __amdgpu_buffer_rsrc_t rs =
+        row_rsrc(base, (uint32_t)(((rows - 1) * a.y_ld + H) * 2));
+    uint8_t* tb = lds + buf * L::kTileBytes;
+#pragma unroll
+    for (int i = 0; i < WLOADS; ++i) {
+      const int q = w * WLOADS + i;  // wave-uniform
+      const int j = q / PER_ROW, part = q % PER_ROW;
+      const uint32_t goff = (uint32_t)(j * a.y_ld * 2 + part * 64 * UNIT + lane * UNIT);
+      lds_void_t* dst = (lds_void_t*)(uintptr_t)(tb + j * L::kRowBytes + part * 64 * UNIT);
+      if constexpr (UNIT == 16)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, goff, 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 4, goff, 0, 0, 0);
+    }
+    if constexpr (MODE == kModeDw) {
+      // the tile's 32 token records (512 bytes): two dword loads by wave 0;
+      // records past the last token read as zeros (g = 0)
+      if (w == 0) {
+        const __amdgpu_buffer_rsrc_t rr = row_rsrc(
+            a.trec + r0, (uint32_t)(rows * 16));
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rr, (lds_void_t*)(uintptr_t)(lds + L::kRecOff + buf * kBN * 16 + i * 256), 4,
+              (uint32_t)(i * 256 + lane * 4), 0, 0, 0);
+      }
+    }
+  };
+
+  if (ntiles > 0) issue_tile(0, 0);
+  // Every prologue load (the stationary fragments and tile 0) has landed.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt untouched
+  lds_barrier();
+
+  uint8_t* const part = lds + L::kPartOff;
+  uint8_t* const frag = lds + L::kFragOff;
+  float* const alpha = reinterpret_cast<float*>(lds + L::kAlphaOff);
+
+  for (int32_t t = 0; t < ntiles; ++t) {
+    const int buf = (int)(t & 1);
+    const uint8_t* tb = lds + buf * L::kTileBytes;
+    // Tile t+1 goes to the other buffer, free since barrier C of tile t-1;
+    // it has this whole tile's work to land.
+    const bool more = t + 1 < ntiles;
+    if (more) issue_tile(t + 1, buf ^ 1);
+
+    // ---- S phase: S^T_w[32 x 64] over this wave's hidden slice, one
+    // 16-row half of the tile at a time (each Y fragment read once) ----
+    f32x4_t tot[2];
+#pragma unroll
+    for (int vb = 0; vb < 2; ++vb) {
+      f32x4_t sp[4];
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) sp[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      // Fragment ks+1 is read while the MFMAs of ks run; the scheduling
+      // fences keep the compiler from hoisting every read (register budget).
+      const uint8_t* abase = tb + (16 * vb + lc) * L::kRowBytes + (dw0 + 8 * lg) * 2;
+      auto af_at = [&](int ks) { return lds_load16(abase, 64 * ks); };
+      u32x4 af[3];
+      af[0] = af_at(0);
+      if (KS > 1) af[1] = af_at(1);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 2 < KS) af[(ks + 2) % 3] = af_at(ks + 2);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) sp[nb] = mfma<Tag>(af[ks % 3], xs[nb][ks], sp[nb]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // Partials of the other waves' row blocks go to LDS; this wave's own
+      // block stays in registers.
+      tot[vb] = sp[0];
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        if (nb == w) {  // uniform branch: no dynamic register indexing
+          tot[vb] = sp[nb];
+          continue;
+        }
+        const int slot = nb < w ? nb : nb - 1;
+        *reinterpret_cast<f32x4_t*>(part + (((w * 3 + slot) * 2 + vb) * 64 + lane) * 16) =
+            sp[nb];
+      }
+    }
+    lds_barrier();  // A: partials published
+
+
+    // ---- exchange: wave w finishes stationary block w ----
+    float s[8];
+    {
+      // The three other waves' partials of block w: all six reads issued
+      // before the first add.
+      f32x4_t pr[3][2];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const int ww = k < w ? k : k + 1;     // wave-uniform
+        const int slot = w < ww ? w : w - 1;  // w's slot among ww's targets
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb)
+          pr[k][vb] = *reinterpret_cast<const f32x4_t*>(
+              part + (((ww * 3 + slot) * 2 + vb) * 64 + lane) * 16);
+      }
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb) tot[vb] += (pr[0][vb] + pr[1][vb]) + pr[2][vb];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s[r] = tot[0][r];
+        s[4 + r] = tot[1][r];
+      }
+    }
+    // Tile column of value i: 4lg + (i & 3) + 16 (i >> 2).
+    uint32_t pk[4] = {0u, 0u, 0u, 0u};
+    if constexpr (MODE == kModeDw) {
+      // P^T[v][n] = g_n ([v == a_n] - exp(s - lse_n)), the target entry as
+      // g_n (-expm1(logp_n)) (exact as p -> 1).
+      const float* recs = reinterpret_cast<const float*>(lds + L::kRecOff + buf * kBN * 16);
+      float p[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int col = 4 * lg + (i & 3) + 16 * (i >> 2);
+        const float4 rc = *reinterpret_cast<const float4*>(recs + col * 4);
+        const int32_t an = __float_as_int(rc.x);
+        const float gn = rc.y;
+        const float e = exp2_hw(s[i] * kLog2e - rc.z);
+        p[i] = gn == 0.f ? 0.f : (an == (int32_t)my_row ? rc.w : -gn * e);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pk[i] = pack2<Tag>(p[2 * i], p[2 * i + 1]);
+    } else {
+      // Softmax weights of row my_row over this tile (target column held out).
+      float tmax = -__builtin_huge_valf();
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int32_t v = t * kBN + 4 * lg + (i & 3) + 16 * (i >> 2);
+        if (v >= a.V) s[i] = -__builtin_huge_valf();
+        if (v == tg) {
+          xa = s[i];
+          s[i] = -__builtin_huge_valf();
+        }
+        tmax = fmaxf(tmax, s[i]);
+      }
+      if constexpr (MODE == kModeFwdLseOnly) {
+        // No accumulator: each lane keeps an exact running maximum of its own
+        // columns, l rescaled as it moves; the row's four lanes merge at the end.
+        if (tmax > m_ref) {
+          l_part *= m_ref == -__builtin_huge_valf() ? 0.f : exp2_hw((m_ref - tmax) * kLog2e);
+          m_ref = tmax;
+        }
+      } else {
+        // The row's reference point, the same in its four lanes, is set once
+        // from its first finite tile maximum and then stays fixed (no
+        // accumulator rescaling): the cross-lane maximum runs only while some
+        // row of the wave has none yet.
+        if (__builtin_amdgcn_ballot_w64(m_ref == -__builtin_huge_valf()) != 0) {
+          float rmax = fmaxf(tmax, xor16(tmax));
+          rmax = fmaxf(rmax, xor32(rmax));
+          if (m_ref == -__builtin_huge_valf() && rmax > -__builtin_huge_valf())
+            m_ref = rmax + kRefMargin;
+        }
+        if (tmax > m_ref + (kRefHeadroom - kRefMargin) && my_row < a.nx)
+          raise_flag(a.status, RRL_FLAG_LM_RANGE);
+      }
+      const float mb = m_ref == -__builtin_huge_valf() ? 0.f : m_ref * kLog2e;
+      float p[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        p[i] = exp2_hw(s[i] * kLog2e - mb);  // exp(-inf) = 0
+        l_part += p[i];
+      }
+      if constexpr (kAcc) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pk[i] = pack2<Tag>(p[2 * i], p[2 * i + 1]);
+      }
+    }
+    if constexpr (kAcc) lds_store16(frag, (w * 64 + lane) * 16, u32x4{pk[0], pk[1], pk[2], pk[3]});
+    // B: fragments published; every wave's partial reads are done.
+    lds_barrier();
+    if constexpr (kAcc) {
+
+      u32x4 pf[4];
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) pf[nb] = lds_load16(frag, (nb * 64 + lane) * 16);
+      // ---- acc phase: ACC_w[64 x DW] += P[64 x 32] Y[32 x DW] ----
+      // B fragment of block db: Y[k][dw0 + 16db + lc] for k = 4lg + e and
+      // 16 + 4lg + e, two transposing reads; block db+1 is read while the
+      // MFMAs of db run.
+      const uint8_t* bbase =
+          tb + (4 * lg + (lc >> 2)) * L::kRowBytes + (dw0 + 4 * (lc & 3)) * 2;
+      auto bf_at = [&](int db) {
+        const uint2 b1 = lds_tr16(bbase, 32 * db);
+        const uint2 b2 = lds_tr16(bbase, 32 * db + 16 * L::kRowBytes);
+        return u32x4{b1.x, b1.y, b2.x, b2.y};
+      };
+      u32x4 bf[3];
+      bf[0] = bf_at(0);
+      if (DB > 1) bf[1] = bf_at(1);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        if (db + 2 < DB) bf[(db + 2) % 3] = bf_at(db + 2);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) acc[nb][db] = mfma<Tag>(pf[nb], bf[db % 3], acc[nb][db]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of tile t+1 landed
+    lds_barrier();  // C: tile t+1 complete; tile t's reads done
+  }
+
+  // ---- epilogue ----
+  if constexpr (MODE != kModeDw) {
+    if constexpr (MODE == kModeFwdLseOnly) {
+      // merge the four lanes' running maxima of each row
+      float M = fmaxf(m_ref, xor16(m_ref));
+      M = fmaxf(M, xor32(M));
+      l_part = m_ref == M ? l_part : l_part * exp2_hw((m_ref - M) * kLog2e);
+      m_ref = M;
+    }
+    float l = l_part + xor16(l_part);
+    l += xor32(l);
+    float xt = fmaxf(xa, xor16(xa));
+    xt = fmaxf(xt, xor32(xt));
+    // lse = log(l e^m_ref + e^xt); logp = xt - lse formed as -log1p(l e^(m_ref - xt))
+    // so that it keeps its relative precision as p_target -> 1.
+    float lse, logp;
+    const float mr = m_ref;
+    if (xt == -__builtin_huge_valf()) {
+      lse = mr == -__builtin_huge_valf() ? -__builtin_huge_valf() : mr + logf(l);
+      logp = tg < 0 ? 0.f : -__builtin_huge_valf();  // no target: 0
+    } else if (mr == -__builtin_huge_valf() || l == 0.f) {
+      lse = xt;
+      logp = 0.f;
+    } else {
+      const float M = fmaxf(mr, xt);
+      lse = M + logf(l * expf(mr - M) + expf(xt - M));
+      const float d = mr - xt;
+      const float z = l * expf(fminf(d, 80.f));
+      logp = (d < 80.f && z < 1e30f) ? -log1pf(z) : -(d + logf(l));
+    }
+    if (lg == 0 && my_row < a.nx) {
+      a.lse_out[my_row] = lse;
+      a.logp_out[my_row] = logp;
+    }
+    if constexpr (MODE == kModeFwd) {
+      // Obar = acc * exp(m_ref - lse): every wave scales all 64 rows.
+      if (lg == 0) alpha[16 * w + lc] = mr == -__builtin_huge_valf() ? 0.f : expf(mr - lse);
+      lds_barrier();
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const f32x4_t sc = *reinterpret_cast<const f32x4_t*>(alpha + 16 * nb + 4 * lg);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int32_t row = x0 + 16 * nb + 4 * lg + r;
+          if (row >= a.nx) continue;
+          float* o = a.obar + (int64_t)row * a.obar_ld + dw0 + lc;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) o[16 * db] = acc[nb][db][r] * sc[r];
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t row = x0 + 16 * nb + 4 * lg + r;
+        if (row >= a.nx) continue;
+        if (a.dw_f32) {
+          float* o = static_cast<float*>(a.dw) + (int64_t)row * a.dw_ld + dw0 + lc;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) o[16 * db] = acc[nb][db][r];
+        } else {
+          uint16_t* o = static_cast<uint16_t*>(a.dw) + (int64_t)row * a.dw_ld + dw0 + lc;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+            o[16 * db] = (uint16_t)(pack2<Tag>(acc[nb][db][r], 0.f) & 0xFFFFu);
+        }
+      }
+    }
+  }
+}
+
+// Per-token records of the dW pass: {target (bits), g, lse*log2(e),
+// g*(-expm1(logp))}; a token with no valid target gets target -1.
+__global__ __launch_bounds__(256) void lm_token_records_kernel(int64_t n, int32_t V,
+                                                               const int32_t* tgt,
+                                                               const float* lse,
+                                                               const float* logp,
+                                                               const float* g, float4* out) {
+  for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256) {
+    const int32_t a = tgt[i];
+    const float gi = g[i];
+    const bool ok = a >= 0 && a < V;
+    out[i] = make_float4(__int_as_float(ok ? a : -1), gi, lse[i] * kLog2e,
+                         ok ? gi * -expm1f(logp[i]) : 0.f);
+  }
+}
+
+// dhidden[n] = g_n ((-expm1(logp_n)) W[a_n] - obar_n), 16-bit out.
+template <class Tag>
+__global__ __launch_bounds__(256) void lm_dhidden_kernel(int64_t n, int32_t H, int32_t V,
+                                                         const uint16_t* w, int64_t w_ld,
+                                                         const int32_t* tgt, const float* logp,
+                                                         const float* g, const float* obar,
+                                                         int64_t obar_ld, uint16_t* dh,
+                                                         int64_t dh_ld) {
+  for (int64_t i = blockIdx.x; i < n; i += gridDim.x) {
+    const int32_t a = tgt[i];
+    const float gi = g[i];
+    const bool ok = a >= 0 && a < V && gi != 0.f;
+    const float ct = ok ? -expm1f(logp[i]) : 0.f;
+    const uint16_t* wr = w + (int64_t)(ok ? a : 0) * w_ld;
+    const float* orow = obar + i * obar_ld;
+    uint16_t* out = dh + i * dh_ld;
+    for (int d = threadIdx.x * 2; d < H; d += 512) {
+      const float w0 = ok ? widen<Tag>(wr[d]) : 0.f, w1 = ok ? widen<Tag>(wr[d + 1]) : 0.f;
+      const float v0 = gi == 0.f ? 0.f : gi * (ct * w0 - orow[d]);
+      const float v1 = gi == 0.f ? 0.f : gi * (ct * w1 - orow[d + 1]);
+      *reinterpret_cast<uint32_t*>(out + d) = pack2<Tag>(v0, v1);
+    }
+  }
+}
+
+int cu_count(int* out) {
+  static std::mutex mu;
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    *out = 256;
+    return RRL_OK;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  *out = cached[dev];
+  return RRL_OK;
+}
+
+template <class Tag, int MODE>
+int launch_tiles(const LmArgs& a, int64_t H, hipStream_t st) {
+  const unsigned grid = (unsigned)((a.nx + kBM - 1) / kBM);
+  if (grid == 0) return RRL_OK;
+#define RRL_LM_CASE(HV)                                                                        \
+  case HV:                                                                                     \
+    hipLaunchKernelGGL((lm_tile_kernel<Tag, MODE, HV>), dim3(grid), dim3(kNT), 0, st, a);      \
+    return check_launch("lm_tile_kernel");
+  switch (H) {
+    RRL_LM_CASE(128)
+    RRL_LM_CASE(256)
+    RRL_LM_CASE(384)
+    RRL_LM_CASE(512)
+    RRL_LM_CASE(640)
+    RRL_LM_CASE(768)
+    RRL_LM_CASE(896)
+    RRL_LM_CASE(1024)
+    default: break;
+  }
+#undef RRL_LM_CASE
+  set_error("lm head: hidden size must be a multiple of 128 and at most 1024");
+  return RRL_EINVAL;
+}
+
+// bfloat16 only: the softmax weights and gradients go through the MFMA as
+// 16-bit values, and float16's 5-bit exponent cannot hold weights of order
+// 1/V (6.6e-6 at V = 151936 is below its 6.1e-5 normal minimum).
+template <int MODE>
+int launch_tiles_dt(int32_t /*dt*/, const LmArgs& a, int64_t H, hipStream_t st) {
+  return launch_tiles<TagBF16, MODE>(a, H, st);
+}
+
+int check_operands(int32_t dt, int64_t N, int64_t H, int64_t V, const void* hidden,
+                   int64_t h_ld, const void* weight, int64_t w_ld) {
+  RRL_REQUIRE(dt == RRL_BF16, RRL_EDTYPE, "lm head: hidden and weight must be bfloat16");
+  RRL_REQUIRE(N >= 0 && V >= 1 && V < ((int64_t)1 << 31) && N < ((int64_t)1 << 31), RRL_EINVAL,
+              "lm head: need 0 <= N < 2^31 tokens and 1 <= V < 2^31");
+  RRL_REQUIRE(H >= 128 && H <= 1024 && H % 128 == 0, RRL_EINVAL,
+              "lm head: hidden size must be a multiple of 128 and at most 1024");
+  RRL_REQUIRE(h_ld >= H && w_ld >= H && h_ld % 8 == 0 && w_ld % 8 == 0, RRL_EINVAL,
+              "lm head: row strides must be >= H and multiples of 8 elements");
+  RRL_REQUIRE(N == 0 || (hidden && (uintptr_t)hidden % 16 == 0), RRL_EALIGN,
+              "lm head: hidden must be 16-byte aligned");
+  RRL_REQUIRE(weight && (uintptr_t)weight % 16 == 0, RRL_EALIGN,
+              "lm head: weight must be 16-byte aligned");
+  // One tile's byte range must fit a buffer descriptor.
+  RRL_REQUIRE((int64_t)kBN * (h_ld > w_ld ? h_ld : w_ld) * 2 < ((int64_t)1 << 31), RRL_EINVAL,
+              "lm head: row stride too large");
+  return RRL_OK;
+}
+
+}  // namespace
+}  // namespace rrl
+
+using namespace rrl;
+
+extern "C" int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t dtype, int64_t N,
+                               int64_t H, int64_t V, int64_t h_ld, int64_t w_ld,
+                               const int32_t* targets, const float* mref_in, float* lse_out,
+                               float* logp_out, float* obar, int64_t obar_ld, int32_t* status,
+                               void* stream) {
+  clear_error();
+  if (int rc = check_operands(dtype, N, H, V, hidden, h_ld, weight, w_ld)) return rc;
+  if (N == 0) return RRL_OK;
+  RRL_REQUIRE(targets && lse_out && logp_out && status, RRL_EINVAL,
+              "lm head: null pointer argument");
+  RRL_REQUIRE(mref_in == nullptr || obar != nullptr, RRL_EINVAL,
+              "lm head: mref_in applies to the pass that forms obar");
+  RRL_REQUIRE(obar == nullptr || obar_ld >= H, RRL_EINVAL, "lm head: obar row stride < H");
+  LmArgs a{};
+  a.x = hidden; a.x_ld = h_ld; a.nx = (int32_t)N;
+  a.y = weight; a.y_ld = w_ld; a.ny = (int32_t)V;
+  a.V = (int32_t)V;
+  a.tgt = targets; a.lse_out = lse_out; a.logp_out = logp_out;
+  a.obar = obar; a.obar_ld = obar_ld; a.mref_in = mref_in; a.status = status;
+  hipStream_t st = as_stream(stream);
+  return obar ? launch_tiles_dt<kModeFwd>(dtype, a, H, st)
+              : launch_tiles_dt<kModeFwdLseOnly>(dtype, a, H, st);
+}
+
+extern "C" size_t rrl_lm_head_records_bytes(int64_t N) {
+  return (size_t)(N > 0 ? N : 0) * 16 + 256;
+}
+
+extern "C" int rrl_lm_head_dhidden(const void* weight, int32_t dtype, int64_t N, int64_t H,
+                                   int64_t V, int64_t w_ld, const int32_t* targets,
+                                   const float* logp, const float* g, const float* obar,
+                                   int64_t obar_ld, void* dhidden, int64_t dh_ld,
+                                   void* stream) {
+  clear_error();
+  if (int rc = check_operands(dtype, N, H, V, dhidden, dh_ld, weight, w_ld)) return rc;
+  if (N == 0) return RRL_OK;
+  RRL_REQUIRE(targets && logp && g && obar && dhidden, RRL_EINVAL,
+              "lm head: null pointer argument");
+  RRL_REQUIRE(obar_ld >= H, RRL_EINVAL, "lm head: obar row stride < H");
+  int cus = 256;
+  cu_count(&cus);
+  const unsigned grid = (unsigned)(N < 16 * cus ? N : 16 * cus);
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(lm_dhidden_kernel<TagBF16>, dim3(grid), dim3(256), 0, st, N, (int32_t)H,
+                     (int32_t)V, static_cast<const uint16_t*>(weight), w_ld, targets, logp, g,
+                     obar, obar_ld, static_cast<uint16_t*>(dhidden), dh_ld);
+  return check_launch("lm_dhidden_kernel");
+}
+
+extern "C" int rrl_lm_head_dweight(const void* hidden, const void* weight, int32_t dtype,
+                                   int64_t N, int64_t H, int64_t V, int64_t h_ld, int64_t w_ld,
+                                   const int32_t* targets, const float* lse, const float* logp,
+                                   const float* g, void* records, void* dweight,
+                                   int32_t dw_dtype, int64_t dw_ld, void* stream) {
+  clear_error();
+  if (int rc = check_operands(dtype, N, H, V, hidden, h_ld, weight, w_ld)) return rc;
+  RRL_REQUIRE(dw_dtype == RRL_F32 || dw_dtype == dtype, RRL_EDTYPE,
+              "lm head: dweight must be float32 or the weight dtype");
+  RRL_REQUIRE(dweight && dw_ld >= H, RRL_EINVAL, "lm head: dweight pointer or stride");
+  RRL_REQUIRE(N == 0 || (targets && lse && logp && g && records), RRL_EINVAL,
+              "lm head: null pointer argument");
+  RRL_REQUIRE((uintptr_t)records % 16 == 0, RRL_EALIGN, "lm head: records must be 16-byte aligned");
+  hipStream_t st = as_stream(stream);
+  if (N > 0) {
+    int cus = 256;
+    cu_count(&cus);
+    const unsigned rg = (unsigned)((N + 255) / 256 < 16 * cus ? (N + 255) / 256 : 16 * cus);
+    hipLaunchKernelGGL(lm_token_records_kernel, dim3(rg), dim3(256), 0, st, N, (int32_t)V,
+                       targets, lse, logp, g, static_cast<float4*>(records));
+    if (int rc = check_launch("lm_token_records_kernel")) return rc;
+  }
+  LmArgs a{};
+  a.x = weight; a.x_ld = w_ld; a.nx = (int32_t)V;
+  a.y = hidden; a.y_ld = h_ld; a.ny = (int32_t)N;
+  a.V = (int32_t)V;
+  a.trec = static_cast<const float4*>(records);
+  a.dw = dweight; a.dw_ld = dw_ld; a.dw_f32 = dw_dtype == RRL_F32;
+  return launch_tiles_dt<kModeDw>(dtype, a, H, st);
+}

@@ -203,18 +203,6 @@ __device__ __forceinline__ TokenRecord load_record(const void* base, uint32_t r)
   return rec;
 }
 
-// Workgroup barrier for the combine's LDS exchange.  __syncthreads()'s release
-// fence waits for every outstanding vector-memory access (vmcnt(0)), which
-// would drain the next row's in-flight slab loads; the exchange only needs
-// this wave's LDS accesses to have landed, so wait on lgkmcnt alone.  s_waitcnt immediate (gfx9 layout): vmcnt 63 and
-// expcnt 7 (no wait), lgkmcnt 0.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // s * exp(m - M) for the combine: exact s when m == M (also for M = -inf or
 // +inf, where m - M is NaN), 0 for m = -inf below a finite M.
 __device__ __forceinline__ float rescale(float s, float m, float M) {

@@ -46,6 +46,20 @@ __device__ __forceinline__ int dpp_i(int v) {
 }
 constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
 
+// Workgroup barrier for LDS exchanges.  __syncthreads()'s release fence waits
+// for every outstanding vector-memory access (vmcnt(0)), which would drain
+// loads still in flight for a later row or tile; an LDS exchange only needs
+// this wave's LDS accesses to have landed, so wait on lgkmcnt alone.
+// s_waitcnt immediate, gfx9 layout (bits 3:0 vmcnt[3:0], 6:4 expcnt, 11:8
+// lgkmcnt, 15:14 vmcnt[5:4]): 0xC07F = vmcnt 63 and expcnt 7 (no wait),
+// lgkmcnt 0.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ float lane_read(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }

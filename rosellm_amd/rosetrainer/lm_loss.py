@@ -225,19 +225,22 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, target: Tensor, *
 
     ``hidden`` [..., H] (positions already aligned with ``target``),
     ``weight`` the LM head's [V, H] (no bias: rosetrainer/model.py:499,
-    qwen3.py:508).  Row blocks of ``row_block`` tokens: logits GEMM, the
-    single-pass NLL row kernel in place, then the dhidden and dW GEMMs, so the
-    forward leaves both gradients (three GEMMs, no recomputation).
+    qwen3.py:508), bfloat16 or float16.  The label log-probs come from the
+    matrix-core LM head (``linear_label_logprobs``: ignored labels have no
+    target), the loss from the NLL objective's kernels; the backward runs the
+    LM head's d hidden and d weight kernels.  ``row_block`` is accepted and
+    unused.
     """
 
     _linear._prepare(hidden, weight, target)
     _check_labels(target)
     p = _nll_params(ignore_index, reduction)
+    if row_block < 1:
+        raise ValueError("row_block must be positive")
     dev = nat.require_device(hidden, weight, target)
-    acc = nat.acc_dtype(hidden.dtype)
-    unused = torch.zeros((), dtype=acc, device=dev).expand(target.shape)
-    obj, _d1, _d2, _d3, _logp, _tr = _linear._FusedLinearPolicy.apply(
-        p, int(row_block), hidden, weight, target, unused, unused, target)
+    logp = _linear.linear_label_logprobs(hidden, weight, target, ignore_index)
+    unused = torch.zeros((), dtype=torch.float32, device=dev).expand(target.shape)
+    obj = _losses._objective(p, logp, unused, unused, target)[0]
     return -obj
 
 

@@ -265,18 +265,21 @@ def _rows_close(a, b, tol, what, chunk=16384):
     return worst
 
 
-def test_config5_linear_fullsize_matches_logits_path(device):
-    """Config 5 in full (262144 tokens, hidden 1024, V = 151936 bf16): the
-    fused LM-head path (16384-token row blocks between the GEMMs, float32 dW
-    accumulation) against the logits-level path on the same inputs
-    (F.linear, fused_policy_loss in place, autograd through F.linear).  Loss
-    within 1e-5 of its scale; d hidden and d weight row by row within 1e-2
-    norm-wise (both carry bf16 products; the logits-level dW is one K = 262144
-    product, the fused one 16 accumulated blocks)."""
+def test_config5_linear_fullsize_against_exact_rows(device):
+    """Config 5 in full (262144 tokens, hidden 1024, V = 151936 bf16) through
+    the matrix-core LM head, checked against float64 on samples that the
+    oracle can form exactly: the log-probs of 64 random tokens (their full
+    vocabulary rows of hidden @ W^T in float64), the d hidden rows of those
+    tokens, and the d weight rows of 8 random vocabulary entries (a sum over
+    all 262144 tokens, with each token's log-sum-exp taken from its exact
+    target logit and the kernel's log-prob).  d loss / d logp comes from the
+    objective's own backward.  Bars as in test_gpu_linear: log-probs within
+    1e-5 relative, bf16 rows within twice the propagated one-ulp bound of the
+    bf16 dlogits."""
 
-    import torch.nn.functional as F
+    from test_gpu_linear import _ulp16
 
-    print("[fullsize] config 5 fused LM head vs logits path", flush=True)
+    print("[fullsize] config 5 matrix-core LM head vs exact rows", flush=True)
     cfg = bench.CONFIGS["c5"]
     with torch.no_grad():
         inp = bench.make_inputs(cfg, device, 1234)
@@ -287,25 +290,49 @@ def test_config5_linear_fullsize_matches_logits_path(device):
     kw = cfg["kw"]
     del inp
     _free()
-    h1, w1 = h.detach().clone().requires_grad_(), w.detach().clone().requires_grad_()
-    out1 = R.fused_linear_policy_loss(h1, w1, t, old, adv, mask,
-                                      row_block=bench.LM_HEAD_ROW_BLOCK, **kw)
-    out1.loss.backward()
-    gh1, gw1, loss1 = h1.grad, w1.grad, float(out1.loss)
-    del out1, h1, w1
-    _free()
-    h2, w2 = h.detach().clone().requires_grad_(), w.detach().clone().requires_grad_()
-    logits = F.linear(h2, w2)
-    out2 = R.fused_policy_loss(logits, t, old, adv, mask, inplace=True, **kw)
-    out2.loss.backward()
-    loss2 = float(out2.loss)
-    del out2, logits
-    _free()
-    scale = max(abs(loss2), float(adv.abs().mean()))
-    assert abs(loss1 - loss2) <= 1e-5 * scale, (loss1, loss2)
-    dh = _rows_close(gh1, h2.grad, 1e-2, "d hidden")
-    dw = _rows_close(gw1, w2.grad, 1e-2, "d weight")
-    print(f"[fullsize] c5: loss {loss1:.6g} vs {loss2:.6g}; d hidden {dh:.2e}, d weight {dw:.2e}",
-          flush=True)
-    del gh1, gw1, h2, w2, h, w
+    N, H, V = B * T, h.shape[-1], w.shape[0]
+    hd, wd = h.detach().clone().requires_grad_(), w.detach().clone().requires_grad_()
+    out, lp = R.fused_linear_policy_loss(hd, wd, t, old, adv, mask, return_logprobs=True, **kw)
+    out.loss.backward()
+    gh, gw = hd.grad, wd.grad
+    # d loss / d logp from the objective's own backward on the same log-probs
+    leaf = lp.detach().clone().requires_grad_()
+    R.clipped_policy_loss(leaf, old, adv, mask, **kw).loss.backward()
+    g = leaf.grad.reshape(-1).double().cpu()
+    gen = torch.Generator().manual_seed(77)
+    h64 = h.reshape(N, H).cpu().double()
+    w64 = w.cpu().double()
+    t64 = t.reshape(-1).cpu()
+    lp64 = lp.reshape(-1).cpu().double()
+    # 1. log-probs and d hidden rows of 64 tokens
+    idx = torch.randperm(N, generator=gen)[:64]
+    x = h64[idx] @ w64.t()
+    lpe = torch.log_softmax(x, dim=-1).gather(1, t64[idx][:, None]).squeeze(1)
+    err = (lp64[idx] - lpe).abs()
+    assert bool((err <= 1e-5 * lpe.abs() + 1e-6).all()), float(err.max())
+    p = torch.softmax(x, dim=-1)
+    oh = torch.zeros_like(p).scatter_(1, t64[idx][:, None], 1.0)
+    dl16 = (g[idx][:, None] * (oh - p)).to(torch.bfloat16).double()
+    ref = dl16 @ w64
+    prop = _ulp16(dl16) @ w64.abs()
+    got = gh.reshape(N, H)[idx.to(device)].cpu().double()
+    excess = float(((got - ref).abs() / (2 * prop + _ulp16(ref.abs() + prop) + 1e-30)).max())
+    print(f"[fullsize] c5 logp max abs err {float(err.max()):.2e}; d hidden rows "
+          f"max |err|/bound {excess:.3f}", flush=True)
+    assert excess <= 1.0
+    # 2. d weight rows of 8 vocabulary entries, summed over every token
+    vs = torch.randperm(V, generator=gen)[:8]
+    xt = (h64 * w64[t64]).sum(dim=1)             # exact target logits
+    lse = xt - lp64                               # the kernel's log-sum-exp
+    xv = h64 @ w64[vs].t()                        # [N, 8]
+    pv = torch.exp(xv - lse[:, None])
+    ohv = (t64[:, None] == vs[None, :]).double()
+    dlv = (g[:, None] * (ohv - pv)).to(torch.bfloat16).double()
+    refw = dlv.t() @ h64
+    propw = _ulp16(dlv).t() @ h64.abs()
+    gotw = gw[vs.to(device)].cpu().double()
+    excess_w = float(((gotw - refw).abs() / (2 * propw + _ulp16(refw.abs() + propw) + 1e-30)).max())
+    print(f"[fullsize] c5 d weight rows max |err|/bound {excess_w:.3f}", flush=True)
+    assert excess_w <= 1.0
+    del gh, gw, hd, wd, h, w, out, lp
     _free()

@@ -1,34 +1,34 @@
-"""Fused LM-head path (config 5) vs the CPU oracle on identical seeded inputs.
+"""Matrix-core LM head (config 5) vs the CPU oracle on identical seeded inputs.
 
-The logits product is the GEMM library's (hipBLASLt through torch.mm): the
-oracle is fed the same rounded row-block products the path consumed, computed
-here with torch.mm over the same row blocks, and runs the rest of the chain in
-float64 (``lm_head_step``).  Bars, as for the logits-level path:
+The oracle runs the whole chain exactly: the float64 product of the bf16
+hidden states and weight (``hidden.double() @ weight.double().T``), then
+``lm_head_step`` in float64, whose dlogits are rounded to bf16 before the two
+backward products, as the reference's bf16 autograd rounds them.  Bars:
 
-* log-probs within 1e-5 relative of the float64 oracle;
+* log-probs within 1e-5 relative (+1e-6 absolute) of the float64 oracle: the
+  kernels accumulate the 16-bit products in float32;
 * the loss within 2e-3 of the objective's term scale (bf16 inputs);
-* d hidden and d weight (bf16): the reference's autograd feeds the linear
-  map's backward bf16 dlogits, and the row kernels hold each dlogit within
-  one ulp of the correctly rounded exact value (the logits-level bar).  So
-  every element of ``dlogits16 @ W`` / ``dlogits16.T @ hidden`` must lie
-  within what those one-ulp deviations can move it (``ulp(dlogits16) @ |W|``,
-  resp. ``ulp(dlogits16).T @ |hidden|``) plus one ulp of the bf16 output,
-  around the float64 product of the correctly rounded dlogits; and 99% of
-  the rows within 2e-3 norm-wise of that product rounded to bf16.  A row of
-  dW fed by a handful of dominant tokens moves by up to 2^-8 when one of
-  their dlogits sits one ulp away, so the bar is the propagated bound, not a
-  flat row-norm tolerance;
-* float32 inputs: every row of d hidden and d weight within 1e-5 norm-wise.
+* d hidden and d weight (bf16): every element within twice what one-ulp
+  deviations of the bf16 dlogits can move the product (``ulp(dlogits16) @
+  |W|``, resp. ``ulp(dlogits16).T @ |hidden|``) plus one ulp of the output,
+  around the float64 product of the correctly rounded dlogits.  The kernels
+  round the softmax weight p (forward) or g (onehot - p) (dW pass) to bf16
+  where the reference rounds g (onehot - p): each is within one ulp of the
+  reference's value.  Row-wise against the exact product: every row within
+  2^-7 (one bf16 ulp) norm-wise, and the 99th percentile within 2e-3 or
+  1.25x that of the reference's own bf16 chain (bf16 dlogits, product
+  rounded to bf16), whichever is larger.
 """
 
 from __future__ import annotations
+
+import math
 
 import pytest
 import torch
 
 from oracle import roserlhf_oracle as o
 from rosellm_amd import roserlhf as R
-from rosellm_amd.roserlhf import linear as LIN
 
 pytestmark = pytest.mark.gpu
 
@@ -41,55 +41,28 @@ def _gen(seed):
     return torch.Generator().manual_seed(seed)
 
 
-def _partition(B, T, row_block):
-    """The row blocks the path uses, restated: whole sequences per block when
-    a sequence fits, else stretches of one sequence."""
+def _inputs(seed, B, T, H, V, w_scale=None, hot=0.0):
+    """bf16 hidden ~ N(0, 1), weight ~ N(0, w_scale); the exact float64 logits;
+    targets sampled from the softmax (``hot``: that fraction of tokens gets
+    the arg-max as target, p_target near 1 when the weight is sharp)."""
 
-    if T <= row_block:
-        bc = max(1, row_block // T)
-        return [(b0, min(B, b0 + bc), 0, T) for b0 in range(0, B, bc)]
-    return [(b, b + 1, t0, min(T, t0 + row_block)) for b in range(B) for t0 in range(0, T, row_block)]
-
-
-def _block_logits(h, w, row_block):
-    """[B, T, V] products, one torch.mm per row block (as the path forms them)."""
-
-    B, T, H = h.shape
-    h2 = h.reshape(B * T, H)
-    parts = []
-    for b0, b1, t0, t1 in _partition(B, T, row_block):
-        r0, n = b0 * T + t0, (b1 - b0) * (t1 - t0)
-        parts.append(torch.mm(h2[r0:r0 + n], w.t()))
-    return torch.cat(parts).reshape(B, T, -1)
-
-
-def _inputs(seed, B, T, H, V, dtype, device, row_block):
     g = _gen(seed)
-    h = torch.randn(B, T, H, generator=g).to(dtype)
-    w = (torch.randn(V, H, generator=g) * (2.0 / H ** 0.5)).to(dtype)
-    hd, wd = h.to(device), w.to(device)
-    x = _block_logits(hd, wd, row_block).cpu()
-    probs = torch.softmax(x.double(), dim=-1)
+    h = torch.randn(B, T, H, generator=g).to(torch.bfloat16)
+    ws = (2.0 / H ** 0.5) if w_scale is None else w_scale
+    w = (torch.randn(V, H, generator=g) * ws).to(torch.bfloat16)
+    x = h.double() @ w.double().t()
+    probs = torch.softmax(x, dim=-1)
     t = torch.multinomial(probs.reshape(-1, V), 1, generator=g).reshape(B, T)
+    if hot > 0:
+        pick = torch.rand(B, T, generator=g) < hot
+        t = torch.where(pick, x.argmax(dim=-1), t)
     lp = o.token_logprobs(x, t, exact=True).float()
     old = lp + torch.randn(B, T, generator=g) * 0.1
     lengths = torch.randint(1, T + 1, (B,), generator=g)
     mask = torch.arange(T)[None, :] < lengths[:, None]
-    r = torch.randint(0, 2, (B // 4, 4), generator=g).float()
-    adv = o.group_standardize(r).reshape(-1)[:, None].expand(B, T).contiguous()
+    r = torch.randint(0, 2, (max(B // 4, 1), 4 if B >= 4 else B), generator=g).float()
+    adv = o.group_standardize(r).reshape(-1)[:B, None].expand(B, T).contiguous()
     return h, w, x, t, old, adv, mask
-
-
-def _rows_close(got, want, tol, what):
-    """Row-norm relative error against float64 rows (float32 outputs)."""
-
-    g = got.detach().cpu().double().reshape(-1, got.shape[-1])
-    w = want.detach().cpu().double().reshape(-1, got.shape[-1])
-    den = w.norm(dim=-1)
-    rel = torch.where(den > 0, (g - w).norm(dim=-1) / den.clamp_min(1e-300), (g - w).norm(dim=-1))
-    worst = float(rel.max())
-    print(f"{what}: worst row-norm rel err {worst:.3e}", flush=True)
-    assert worst <= tol, f"{what}: worst row-norm rel err {worst:.3e} > {tol}"
 
 
 def _ulp16(v):
@@ -99,139 +72,236 @@ def _ulp16(v):
     return torch.where(v != 0, torch.ldexp(torch.ones_like(m), e - 8), torch.zeros_like(m))
 
 
-def _product_check(got, dl16, other, what, transpose):
-    """got = bf16 GEMM of the kernel's dlogits with ``other``; dl16: the
-    correctly rounded exact dlogits [rows, V] (float64 copy)."""
+def _product_check(got, dl, other, what, transpose, factor=2.0):
+    """got: the kernel's d hidden (transpose=False: dl @ other) or d weight
+    (transpose=True: dl.T @ other); dl: the exact dlogits [rows, V] (float64).
 
-    a = dl16.t() if transpose else dl16
-    ref = a @ other.double()
+    Elementwise: within ``factor`` times the propagated one-ulp bound of the
+    bf16 dlogits the reference's autograd forms (plus one output ulp) around
+    the float64 product of those rounded dlogits.  Row-wise: 99% of the rows
+    within 2e-3 norm-wise of the exact product (bf16's own precision: the
+    kernels keep the target entry's 1 - p exact where the reference rounds
+    it)."""
+
+    dl16 = dl.to(torch.bfloat16).double()
+    a16 = dl16.t() if transpose else dl16
+    ref = a16 @ other.double()
     prop = (_ulp16(dl16).t() if transpose else _ulp16(dl16)) @ other.double().abs()
     g = got.detach().cpu().double().reshape(ref.shape)
-    bound = prop + _ulp16(ref.abs() + prop) + 1e-30
+    bound = factor * prop + _ulp16(ref.abs() + prop) + 1e-30
     excess = float(((g - ref).abs() / bound).max())
-    rounded = ref.float().to(torch.bfloat16).double()
-    den = rounded.norm(dim=-1)
-    rel = torch.where(den > 0, (g - rounded).norm(dim=-1) / den.clamp_min(1e-300),
-                      (g - rounded).norm(dim=-1))
-    q99 = float(torch.quantile(rel, 0.99))
-    print(f"{what}: max |err|/bound {excess:.3f}, row-norm rel err p99 {q99:.3e} "
-          f"max {float(rel.max()):.3e}", flush=True)
+    exact = (dl.t() if transpose else dl) @ other.double()
+    den = exact.norm(dim=-1)
+
+    def rowrel(v):
+        return torch.where(den > 0, (v - exact).norm(dim=-1) / den.clamp_min(1e-300),
+                           (v - exact).norm(dim=-1))
+
+    rel = rowrel(g)
+    # the reference's own chain: bf16 dlogits, their product rounded to bf16
+    rel_ref = rowrel(ref.float().to(torch.bfloat16).double())
+    q99, q99_ref = float(torch.quantile(rel, 0.99)), float(torch.quantile(rel_ref, 0.99))
+    print(f"{what}: max |err|/bound {excess:.3f}; row-norm rel err vs exact: p99 {q99:.3e} "
+          f"max {float(rel.max()):.3e} (the reference's bf16 chain: p99 {q99_ref:.3e} max "
+          f"{float(rel_ref.max()):.3e})", flush=True)
     assert excess <= 1.0, f"{what}: an element exceeds its propagated bound ({excess:.3f}x)"
-    assert q99 <= 2e-3, f"{what}: 99th percentile row-norm rel err {q99:.3e} > 2e-3"
+    assert float(rel.max()) <= 2.0 ** -7, f"{what}: a row beyond bf16 precision"
+    assert q99 <= max(2e-3, 1.25 * q99_ref), (
+        f"{what}: 99th percentile row-norm rel err {q99:.3e} (reference chain {q99_ref:.3e})")
 
 
-@pytest.mark.parametrize("V", [4099, 8256])
-@pytest.mark.parametrize("row_block", [64, 192, 4096])
-def test_linear_logprobs_and_grads(device, V, row_block):
-    print(f"[linear-logprobs] V={V} row_block={row_block}", flush=True)
-    B, T, H = 8, 96, 256
-    h, w, x, t, _old, _adv, _mask = _inputs(41, B, T, H, V, torch.bfloat16, device, row_block)
+def _exact_dlogits(x, t, g):
+    """g (onehot - softmax(x)) in float64 with the target entry formed as
+    g * sigmoid(logsumexp_{v != a}(x_v - x_a)) = g (1 - p_a), which keeps its
+    relative precision as p_a -> 1 (1 - p_a in float64 rounds to 0 once the
+    gap exceeds ~37)."""
+
+    V = x.shape[-1]
+    x2, t2, g2 = x.reshape(-1, V), t.reshape(-1), g.reshape(-1).double()
+    p = torch.softmax(x2, dim=-1)
+    dl = -g2[:, None] * p
+    xa = x2.gather(1, t2[:, None])
+    rest = (x2 - xa).scatter(1, t2[:, None], float("-inf"))
+    one_minus = torch.sigmoid(torch.logsumexp(rest, dim=-1))
+    dl.scatter_(1, t2[:, None], (g2 * one_minus)[:, None])
+    return dl
+
+
+def _logp_check(lp, lpo):
+    err = (lp.detach().cpu().double() - lpo).abs()
+    bad = err > 1e-5 * lpo.abs() + 1e-6
+    assert not bool(bad.any()), f"log-probs: worst abs err {float(err.max()):.3e}"
+
+
+@pytest.mark.parametrize("H,V", [(256, 4099), (1024, 8256), (384, 1000), (128, 33),
+                                 (768, 2050), (896, 301), (512, 1)])
+def test_linear_logprobs_and_grads(device, H, V):
+    """log-probs and, for a random upstream gradient, d hidden and d weight,
+    across hidden sizes (every instantiated one is a multiple of 128 up to
+    1024), vocabularies that are not tile multiples, and token counts that
+    are not 64-row block multiples."""
+
+    print(f"[linear-logprobs] H={H} V={V}", flush=True)
+    B, T = 3, 37
+    h, w, x, t, _old, _adv, _mask = _inputs(41, B, T, H, V)
     hd = h.to(device).requires_grad_()
     wd = w.to(device).requires_grad_()
-    lp = R.linear_token_logprobs(hd, wd, t.to(device), row_block=row_block)
+    lp = R.linear_token_logprobs(hd, wd, t.to(device))
     assert lp.dtype == torch.float32 and lp.shape == (B, T)
     lpo = o.token_logprobs(x, t, exact=True)
-    err = (lp.detach().cpu().double() - lpo).abs()
-    assert bool((err <= 1e-5 * lpo.abs() + 1e-7).all()), float(err.max())
+    _logp_check(lp, lpo)
     gw = torch.randn(B, T, generator=_gen(5))
     (lp * gw.to(device)).sum().backward()
-    p = torch.softmax(x.double(), dim=-1)
+    p = torch.softmax(x, dim=-1)
     oh = torch.zeros_like(p).scatter_(-1, t[..., None], 1.0)
-    # the reference's bf16 autograd rounds dlogits to bf16 before the linear
-    # map's backward
-    dl16 = (gw.double()[..., None] * (oh - p)).to(torch.bfloat16).double().reshape(-1, V)
-    _product_check(hd.grad.reshape(-1, H), dl16, w, "dhidden", transpose=False)
-    _product_check(wd.grad, dl16, h.reshape(-1, H), "dweight", transpose=True)
+    dl = (gw.double()[..., None] * (oh - p)).reshape(-1, V)
+    assert hd.grad.dtype == torch.bfloat16 and wd.grad.dtype == torch.bfloat16
+    _product_check(hd.grad.reshape(-1, H), dl, w, "dhidden", transpose=False)
+    _product_check(wd.grad, dl, h.reshape(-1, H), "dweight", transpose=True)
 
 
 @pytest.mark.parametrize("objective", ["clipped", "sao", "sapo", "gspo", "gspo_token"])
-@pytest.mark.parametrize("V,row_block", [(8256, 192), (4099, 64), (8256, 4096)])
-def test_fused_linear_matches_oracle(device, objective, V, row_block):
-    print(f"[fused-linear] objective={objective} V={V} row_block={row_block}", flush=True)
-    B, T, H = 8, 96, 256
-    h, w, x, t, old, adv, mask = _inputs(42, B, T, H, V, torch.bfloat16, device, row_block)
+def test_fused_linear_matches_oracle(device, objective):
+    print(f"[fused-linear] objective={objective}", flush=True)
+    B, T, H, V = 8, 96, 256, 8256
+    h, w, x, t, old, adv, mask = _inputs(42, B, T, H, V)
     kw = KW[objective]
     a = adv[:, 0].contiguous() if objective == "gspo" else adv
     hd = h.to(device).requires_grad_()
     wd = w.to(device).requires_grad_()
-    d = lambda z: z.to(device)
+    d = lambda z: z.to(device)  # noqa: E731
     out, lp = R.fused_linear_policy_loss(hd, wd, d(t), d(old), d(a), d(mask), objective=objective,
-                                         return_logprobs=True, row_block=row_block, **kw)
+                                         return_logprobs=True, **kw)
     out.loss.backward()
     kind = {"clipped": "ppo"}.get(objective, objective)
-    out_o, lpo, dho, dwo = o.lm_head_step(kind, h, w, x, t, old, a, mask, exact=True, **kw)
-    err = (lp.detach().cpu().double() - lpo).abs()
-    assert bool((err <= 1e-5 * lpo.abs() + 1e-7).all()), float(err.max())
+    # the whole chain in float64 on the exact products
+    out_o, lpo, _dho, _dwo = o.lm_head_step(kind, h, w, x, t, old, a, mask, exact=True, **kw)
+    _logp_check(lp, lpo)
     scale = max(abs(out_o["loss"].item()), a.abs().mean().item())
     assert abs(out.loss.item() - out_o["loss"].item()) <= 2e-3 * scale, (
         out.loss.item(), out_o["loss"].item())
-    assert hd.grad.dtype == torch.bfloat16 and wd.grad.dtype == torch.bfloat16
-    dl16 = out_o["dlogits"].double().reshape(-1, V)
-    _product_check(hd.grad.reshape(-1, H), dl16, w, "dhidden", transpose=False)
-    _product_check(wd.grad, dl16, h.reshape(-1, H), "dweight", transpose=True)
-    torch.testing.assert_close(dho.reshape(-1, H), dl16 @ w.double())  # the oracle's products
+    dl = out_o["dlogits"].double().reshape(-1, V)  # exact (float64 logits)
+    _product_check(hd.grad.reshape(-1, H), dl, w, "dhidden", transpose=False)
+    _product_check(wd.grad, dl, h.reshape(-1, H), "dweight", transpose=True)
 
 
-def test_fused_linear_float32(device):
-    B, T, H, V = 8, 32, 128, 3001
-    h, w, x, t, old, adv, mask = _inputs(43, B, T, H, V, torch.float32, device, 64)
+def test_dominant_targets_keep_precision(device):
+    """Sharp weights and arg-max targets: p_target -> 1, where 1 - p_target
+    must come from expm1(logp), not from 1 - p."""
+
+    B, T, H, V = 4, 64, 256, 4096
+    h, w, x, t, _old, _adv, _mask = _inputs(43, B, T, H, V, w_scale=2.0, hot=0.8)
     hd = h.to(device).requires_grad_()
     wd = w.to(device).requires_grad_()
-    d = lambda z: z.to(device)
-    out = R.fused_linear_policy_loss(hd, wd, d(t), d(old), d(adv), d(mask), row_block=64,
-                                     **KW["clipped"])
-    out.loss.backward()
-    out_o, _lpo, dho, dwo = o.lm_head_step("ppo", h, w, x, t, old, adv, mask, exact=True,
-                                           **KW["clipped"])
-    scale = max(abs(out_o["loss"].item()), adv.abs().mean().item())
-    assert abs(out.loss.item() - out_o["loss"].item()) <= 1e-5 * scale
-    _rows_close(hd.grad.reshape(-1, H), dho.reshape(-1, H), 1e-5, "dhidden f32")
-    _rows_close(wd.grad, dwo, 1e-5, "dweight f32")
+    lp = R.linear_token_logprobs(hd, wd, t.to(device))
+    lpo = o.token_logprobs(x, t, exact=True)
+    print(f"dominant: min p_target {float(lpo.exp().min()):.3e}, "
+          f"max p_target {float(lpo.exp().max()):.9f}", flush=True)
+    assert float(lpo.exp().max()) > 0.999
+    _logp_check(lp, lpo)
+    gw = torch.randn(B, T, generator=_gen(6))
+    (lp * gw.to(device)).sum().backward()
+    dl = _exact_dlogits(x, t, gw)
+    _product_check(hd.grad.reshape(-1, H), dl, w, "dhidden", transpose=False)
+    _product_check(wd.grad, dl, h.reshape(-1, H), "dweight", transpose=True)
+
+
+def test_logits_beyond_the_reference_range_rerun(device):
+    """One weight row that gives some tokens logits far above their first
+    tile's maximum (beyond the single pass's fixed reference range): the
+    path reruns around the exact log-sum-exp and still matches the oracle."""
+
+    B, T, H, V = 2, 64, 256, 2048
+    h, w, _x, _t, _old, _adv, _mask = _inputs(44, B, T, H, V)
+    w[1000] = (h[0, 0].float() * 0.6).to(torch.bfloat16)  # logit ~ 0.6 * |h|^2 ~ 150 for token 0
+    x = h.double() @ w.double().t()
+    t = torch.randint(0, V, (B, T), generator=_gen(7))
+    first = x[..., :32].max(dim=-1).values
+    assert float((x.max(dim=-1).values - first).max()) > 100.0
+    hd = h.to(device).requires_grad_()
+    wd = w.to(device).requires_grad_()
+    lp = R.linear_token_logprobs(hd, wd, t.to(device))
+    _logp_check(lp, o.token_logprobs(x, t, exact=True))
+    gw = torch.randn(B, T, generator=_gen(8))
+    (lp * gw.to(device)).sum().backward()
+    p = torch.softmax(x, dim=-1)
+    oh = torch.zeros_like(p).scatter_(-1, t[..., None], 1.0)
+    dl = (gw.double()[..., None] * (oh - p)).reshape(-1, V)
+    _product_check(hd.grad.reshape(-1, H), dl, w, "dhidden", transpose=False)
+    _product_check(wd.grad, dl, h.reshape(-1, H), "dweight", transpose=True)
+
+
+def test_strided_hidden_and_target_errors(device):
+    """A hidden view with a padded row stride is read in place (no copy);
+    out-of-range targets raise as torch.gather does; float32 is refused."""
+
+    B, T, H, V = 2, 40, 256, 1000
+    h, w, x, t, _old, _adv, _mask = _inputs(45, B, T, H, V)
+    big = torch.zeros(B, T, H + 64, dtype=torch.bfloat16)
+    big[..., :H] = h
+    hv = big.to(device)[..., :H]
+    lp = R.linear_token_logprobs(hv, w.to(device), t.to(device))
+    _logp_check(lp, o.token_logprobs(x, t, exact=True))
+    bad = t.clone()
+    bad[1, 3] = V
+    with pytest.raises(RuntimeError, match="out of bounds"):
+        R.linear_token_logprobs(h.to(device), w.to(device), bad.to(device))
+    bad[1, 3] = -1
+    with pytest.raises(RuntimeError, match="out of bounds"):
+        R.linear_token_logprobs(h.to(device), w.to(device), bad.to(device))
+    with pytest.raises(TypeError, match="bfloat16"):
+        R.linear_token_logprobs(h.float().to(device), w.float().to(device), t.to(device))
+    with pytest.raises(ValueError, match="multiple of 128"):
+        R.linear_token_logprobs(h[..., :200].to(device), w[:, :200].to(device), t.to(device))
 
 
 def test_fused_linear_grad_scale_and_diagnostic_grads(device):
     """3 * loss scales both gradients; a loss that also differentiates a
-    diagnostic (the KL term) takes the recomputing backward and equals the
-    composition linear_token_logprobs -> clipped_policy_loss."""
+    diagnostic (the KL term) equals the composition
+    linear_token_logprobs -> clipped_policy_loss."""
 
     B, T, H, V = 8, 48, 128, 4104
-    h, w, x, t, old, adv, mask = _inputs(44, B, T, H, V, torch.bfloat16, device, 128)
-    d = lambda z: z.to(device)
+    h, w, x, t, old, adv, mask = _inputs(46, B, T, H, V)
+    d = lambda z: z.to(device)  # noqa: E731
 
     def run(fused, f):
         hd = d(h).requires_grad_()
         wd = d(w).requires_grad_()
         if fused:
-            out = R.fused_linear_policy_loss(hd, wd, d(t), d(old), d(adv), d(mask), row_block=128,
+            out = R.fused_linear_policy_loss(hd, wd, d(t), d(old), d(adv), d(mask),
                                              **KW["clipped"])
         else:
-            lp = R.linear_token_logprobs(hd, wd, d(t), row_block=128)
+            lp = R.linear_token_logprobs(hd, wd, d(t))
             out = R.clipped_policy_loss(lp, d(old), d(adv), d(mask), **KW["clipped"])
         f(out).backward()
         return out, hd.grad, wd.grad
 
     o1, h1, w1 = run(True, lambda out: out.loss)
     o3, h3, w3 = run(True, lambda out: 3.0 * out.loss)
-    torch.testing.assert_close(h3.float(), 3.0 * h1.float(), rtol=8e-3, atol=1e-6)
-    torch.testing.assert_close(w3.float(), 3.0 * w1.float(), rtol=8e-3, atol=1e-6)
+    # d hidden: each side rounded to bf16 once, within two bf16 ulps; d weight
+    # sums per-token terms that the dW pass rounds to bf16 (3 g (onehot - p)
+    # against g (onehot - p)), so its rows agree norm-wise
+    torch.testing.assert_close(h3.float(), 3.0 * h1.float(), rtol=2.0 ** -6, atol=1e-6)
+    num = (w3.float() - 3.0 * w1.float()).norm(dim=-1)
+    den = (3.0 * w1.float()).norm(dim=-1)
+    assert bool((num <= 1e-2 * den + 1e-12).all()), float((num / den.clamp_min(1e-30)).max())
     _ok, hk, wk = run(True, lambda out: out.loss + 0.5 * out.approximate_kl)
     _oc, hc, wc = run(False, lambda out: out.loss + 0.5 * out.approximate_kl)
-    _rows_close(hk.reshape(-1, H), hc.reshape(-1, H).double(), 4e-3, "dhidden with kl")
-    _rows_close(wk, wc.double(), 4e-3, "dweight with kl")
+    assert torch.equal(hk, hc) and torch.equal(wk, wc)
 
 
 def test_fused_linear_equals_logits_level_path(device):
-    """The same row kernel as fused_policy_loss: log-probs bit-identical and
-    the loss equal when fed the same block products."""
+    """The loss of the LM-head path equals fused_policy_loss on the bf16
+    logits within the log-probs' float32 accumulation error."""
 
     B, T, H, V = 8, 64, 256, 8256
-    h, w, x, t, old, adv, mask = _inputs(45, B, T, H, V, torch.bfloat16, device, 128)
-    d = lambda z: z.to(device)
+    h, w, x, t, old, adv, mask = _inputs(47, B, T, H, V)
+    d = lambda z: z.to(device)  # noqa: E731
     out_l, lp_l = R.fused_linear_policy_loss(d(h), d(w).requires_grad_(), d(t), d(old), d(adv),
-                                             d(mask), return_logprobs=True, row_block=128,
-                                             **KW["clipped"])
-    xd = d(x).requires_grad_()
+                                             d(mask), return_logprobs=True, **KW["clipped"])
+    xd = d(x.float()).requires_grad_()
     out_x, lp_x = R.fused_policy_loss(xd, d(t), d(old), d(adv), d(mask), return_logprobs=True,
                                       **KW["clipped"])
-    assert torch.equal(lp_l, lp_x)
-    torch.testing.assert_close(out_l.loss, out_x.loss, rtol=1e-6, atol=1e-9)
+    assert float((lp_l - lp_x).abs().max()) < 1e-4
+    torch.testing.assert_close(out_l.loss, out_x.loss, rtol=1e-4, atol=1e-7)
+    assert math.isfinite(out_l.loss.item())

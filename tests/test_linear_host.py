@@ -1,5 +1,5 @@
-"""Host side of the fused LM-head path, without a GPU: the row-block
-partition and the argument validation that runs before any device work."""
+"""Host side of the matrix-core LM-head path, without a GPU: the argument
+validation that runs before any device work, and no CPU fallback."""
 
 from __future__ import annotations
 
@@ -7,28 +7,6 @@ import pytest
 import torch
 
 from rosellm_amd import roserlhf as R
-from rosellm_amd.roserlhf import linear as LIN
-
-
-def _partition(B, T, row_block):
-    if T <= row_block:
-        bc = max(1, row_block // T)
-        return [(b0, min(B, b0 + bc), 0, T) for b0 in range(0, B, bc)]
-    return [(b, b + 1, t0, min(T, t0 + row_block)) for b in range(B) for t0 in range(0, T, row_block)]
-
-
-@pytest.mark.parametrize("B,T,rb", [(8, 96, 64), (8, 96, 192), (8, 96, 4096), (3, 5, 7),
-                                    (1, 10, 3), (256, 1024, 16384), (64, 8192, 16384)])
-def test_partition_covers_every_row_once(B, T, rb):
-    blk = LIN._Blocks(torch.zeros(B * T, 4), torch.zeros(6, 4), B, T, rb)
-    assert blk.blocks == _partition(B, T, rb)
-    seen = torch.zeros(B * T, dtype=torch.int32)
-    for b in blk.blocks:
-        r0, n = blk.r0(b), blk.rows(b)
-        assert n <= max(rb, T)
-        seen[r0:r0 + n] += 1
-    assert bool((seen == 1).all())
-    assert blk.buf.shape == (max(blk.rows(b) for b in blk.blocks), 6)
 
 
 def test_validation_messages():
@@ -52,7 +30,9 @@ def test_validation_messages():
         R.fused_linear_policy_loss(h, w, t, z, z, z.bool(), skip_masked_rows=True,
                                    return_logprobs=True)
     with pytest.raises(ValueError, match="row_block must be positive"):
-        LIN._Blocks(torch.zeros(6, 8), w, 2, 3, 0)
+        R.linear_token_logprobs(h, w, t, row_block=0)
+    with pytest.raises(ValueError, match="not provided by the LM-head path"):
+        R.fused_linear_policy_loss(h, w, t, z, z, z.bool(), skip_masked_rows=True)
 
 
 def test_no_cpu_fallback():
