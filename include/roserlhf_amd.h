@@ -340,11 +340,16 @@ RRL_API int rrl_masked_whiten(int64_t B, int64_t T, rrl_view x, rrl_view mask, d
  * obar only the log-sum-exp is formed (half the MFMA work).  A target id >= V
  * raises TARGET_RANGE; a token whose logits exceed the fixed reference point's
  * range raises LM_RANGE (rerun with mref_in = the lse of an obar-less call).
- * mref_in: NULL, or float32 [N] reference points (the rerun). */
+ * mref_in: NULL, or float32 [N] reference points (the rerun).  need_obar:
+ * NULL, or uint8 [N] (nonzero: the token's obar is needed); a block of 64
+ * consecutive tokens none of which needs it takes the log-sum-exp-only pass
+ * and its obar rows are left unwritten (for tokens whose d loss / d logp is
+ * zero by construction, such as masked tokens). */
 RRL_API int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t dtype, int64_t N,
                     int64_t H, int64_t V, int64_t h_ld, int64_t w_ld, const int32_t* targets,
-                    const float* mref_in, float* lse_out, float* logp_out, float* obar,
-                    int64_t obar_ld, int32_t* status, void* stream);
+                    const uint8_t* need_obar, const float* mref_in, float* lse_out,
+                    float* logp_out, float* obar, int64_t obar_ld, int32_t* status,
+                    void* stream);
 
 /* dhidden[n] = g[n] * ((-expm1(logp[n])) * weight[target[n]] - obar[n]), in the
  * weight dtype, rows dh_ld apart (the linear map's backward of a1's gradient
@@ -357,7 +362,9 @@ RRL_API int rrl_lm_head_dhidden(const void* weight, int32_t dtype, int64_t N, in
 /* dweight[v] = sum_n g[n] ([v == target[n]] - exp(logit[n, v] - lse[n])) hidden[n],
  * the logits recomputed tile by tile, float32 accumulation over every token in
  * registers, written once as float32 or the weight dtype (dw_dtype), rows dw_ld
- * apart.  records: rrl_lm_head_records_bytes(N) bytes of caller workspace. */
+ * apart.  Tiles of 32 consecutive tokens whose g are all zero contribute
+ * exactly zero and are not visited.  records: rrl_lm_head_records_bytes(N)
+ * bytes of caller workspace (16-byte aligned). */
 RRL_API size_t rrl_lm_head_records_bytes(int64_t N);
 RRL_API int rrl_lm_head_dweight(const void* hidden, const void* weight, int32_t dtype,
                     int64_t N, int64_t H, int64_t V, int64_t h_ld, int64_t w_ld,

@@ -136,6 +136,9 @@ struct LmArgs {
   float* obar;           // forward: sum_{v != a} p_v W_v per token, [nx, H] (ld obar_ld)
   int64_t obar_ld;
   const float* mref_in;  // forward: per-token reference point (NULL: first-tile rule)
+  const uint8_t* need_obar;  // forward: per-token "obar needed" (NULL: every token)
+  const int32_t* tile_list;  // dW pass: indices of the streamed tiles to visit (NULL: all)
+  const int32_t* tile_count; // dW pass: number of entries of tile_list
   const float4* trec;    // dW pass: per streamed token {target bits, g, lse*log2e, g*(-expm1(logp))}
   void* dw;              // dW pass: [nx, H] (ld dw_ld), float32 or 16-bit
   int64_t dw_ld;
@@ -147,40 +150,36 @@ template <int H>
 struct LdsLayout {
   static constexpr int kRowBytes = H * 2 + kRowPad;
   static constexpr int kTileBytes = kBN * kRowBytes;
-  static constexpr int kPartOff = 2 * kTileBytes;                 // [4 writers][3][2 vb][64] x 16 B
-  static constexpr int kPartBytes = 4 * 3 * 2 * 64 * 16;
-  static constexpr int kFragOff = kPartOff + kPartBytes;           // [4 blocks][64] x 16 B
+  static constexpr int kFragOff = 2 * kTileBytes;                 // [4 blocks][64] x 16 B
   static constexpr int kRecOff = kFragOff + 4 * 64 * 16;           // [2][32] x 16 B (dW pass)
-  static constexpr int kTotal = kRecOff + 2 * kBN * 16;            // 163840 at H = 1024
-  static constexpr int kAlphaOff = kPartOff;  // [64] floats, epilogue only (partials unused)
+  static constexpr int kAlphaOff = kRecOff + 2 * kBN * 16;         // [64] floats (epilogue)
+  static constexpr int kTotal = kAlphaOff + 64 * 4;
 };
 
 template <class Tag, int MODE, int H>
-__global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
-  constexpr int DW = H / 4;                 // hidden slice per wave
-  constexpr int KS = DW / 32;               // k-steps of the S product per wave
+__device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds) {
+  constexpr int DW = H / 4;                 // hidden slice of each wave's accumulator
+  constexpr int KF = H / 32;                // k-steps of the S product (full hidden size)
   constexpr int DB = DW / 16;               // 16-column blocks of the accumulator per wave
   constexpr int CH = H / 8;                 // 16-byte chunks per row
   constexpr bool kAcc = MODE != kModeFwdLseOnly;
   using L = LdsLayout<H>;
   static_assert(H % 128 == 0 && H <= 1024, "hidden size must be a multiple of 128, at most 1024");
 
-  __shared__ __attribute__((aligned(16))) uint8_t lds[L::kTotal];
-
   const int tid = threadIdx.x, lane = tid & 63, lg = lane >> 4, lc = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int32_t x0 = (int32_t)blockIdx.x * kBM;
   const int dw0 = w * DW;
 
-  // ---- stationary fragments: X[x0 + 16nb + lc][dw0 + 32ks + 8lg .. +7] ----
-  u32x4 xs[4][KS];
+  // ---- stationary fragments of this wave's 16 rows over the whole hidden
+  // size: X[x0 + 16w + lc][32ks + 8lg .. +7] ----
+  u32x4 xs[KF];
+  {
+    const int32_t row = x0 + 16 * w + lc;
+    const uint16_t* p = static_cast<const uint16_t*>(a.x) + (int64_t)row * a.x_ld + 8 * lg;
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    const int32_t row = x0 + 16 * nb + lc;
-    const uint16_t* p = static_cast<const uint16_t*>(a.x) + (int64_t)row * a.x_ld + dw0 + 8 * lg;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      xs[nb][ks] = row < a.nx ? *reinterpret_cast<const u32x4*>(p + 32 * ks) : u32x4{0, 0, 0, 0};
+    for (int ks = 0; ks < KF; ++ks)
+      xs[ks] = row < a.nx ? *reinterpret_cast<const u32x4*>(p + 32 * ks) : u32x4{0, 0, 0, 0};
   }
 
   f32x4_t acc[4][kAcc ? DB : 1];
@@ -208,7 +207,8 @@ __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
     if (a.mref_in != nullptr && my_row < a.nx) m_ref = a.mref_in[my_row];
   }
 
-  const int32_t ntiles = (a.ny + kBN - 1) / kBN;
+  const int32_t ntiles = a.tile_count ? *a.tile_count : (a.ny + kBN - 1) / kBN;
+  auto tile_row0 = [&](int32_t t) { return (a.tile_list ? a.tile_list[t] : t) * kBN; };
 
   // ---- tile loads, global -> LDS directly (buffer loads with the LDS bit:
   // no registers).  One wave-wide load writes 64 consecutive lanes x UNIT
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
   static_assert(kBN * PER_ROW % 4 == 0, "tile load split");
   typedef __attribute__((address_space(3))) void lds_void_t;
   auto issue_tile = [&](int32_t t, int buf) {
-    const int32_t r0 = t * kBN;
+    const int32_t r0 = tile_row0(t);
     const int32_t rows = a.ny - r0 < kBN ? a.ny - r0 : kBN;
     const uint16_t* base = static_cast<const uint16_t*>(a.y) + (int64_t)r0 * a.y_ld;
     // Rows at or past `rows` start at or beyond the descriptor's byte count
@@ -260,7 +260,6 @@ __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt untouched
   lds_barrier();
 
-  uint8_t* const part = lds + L::kPartOff;
   uint8_t* const frag = lds + L::kFragOff;
   float* const alpha = reinterpret_cast<float*>(lds + L::kAlphaOff);
 
@@ -272,62 +271,45 @@ __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
     const bool more = t + 1 < ntiles;
     if (more) issue_tile(t + 1, buf ^ 1);
 
-    // ---- S phase: S^T_w[32 x 64] over this wave's hidden slice, one
-    // 16-row half of the tile at a time (each Y fragment read once) ----
+    // ---- S phase: S^T[32 x 16] of the tile against this wave's own 16 rows
+    // over the whole hidden size (no cross-wave reduction).  Two accumulator
+    // chains per tile half; the fragments of step ks+2 are read while step
+    // ks's MFMAs run (the scheduling fences keep the compiler from hoisting
+    // every read). ----
     f32x4_t tot[2];
-#pragma unroll
-    for (int vb = 0; vb < 2; ++vb) {
-      f32x4_t sp[4];
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) sp[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      // Fragment ks+1 is read while the MFMAs of ks run; the scheduling
-      // fences keep the compiler from hoisting every read (register budget).
-      const uint8_t* abase = tb + (16 * vb + lc) * L::kRowBytes + (dw0 + 8 * lg) * 2;
-      auto af_at = [&](int ks) { return lds_load16(abase, 64 * ks); };
-      u32x4 af[3];
-      af[0] = af_at(0);
-      if (KS > 1) af[1] = af_at(1);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (ks + 2 < KS) af[(ks + 2) % 3] = af_at(ks + 2);
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) sp[nb] = mfma<Tag>(af[ks % 3], xs[nb][ks], sp[nb]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // Partials of the other waves' row blocks go to LDS; this wave's own
-      // block stays in registers.
-      tot[vb] = sp[0];
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        if (nb == w) {  // uniform branch: no dynamic register indexing
-          tot[vb] = sp[nb];
-          continue;
-        }
-        const int slot = nb < w ? nb : nb - 1;
-        *reinterpret_cast<f32x4_t*>(part + (((w * 3 + slot) * 2 + vb) * 64 + lane) * 16) =
-            sp[nb];
-      }
-    }
-    lds_barrier();  // A: partials published
-
-
-    // ---- exchange: wave w finishes stationary block w ----
-    float s[8];
     {
-      // The three other waves' partials of block w: all six reads issued
-      // before the first add.
-      f32x4_t pr[3][2];
+      f32x4_t sa[2][2];
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        const int ww = k < w ? k : k + 1;     // wave-uniform
-        const int slot = w < ww ? w : w - 1;  // w's slot among ww's targets
+      for (int vb = 0; vb < 2; ++vb) sa[vb][0] = sa[vb][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const uint8_t* abase = tb + lc * L::kRowBytes + 16 * lg;
+      auto af_at = [&](int ks, int vb) {
+        return lds_load16(abase, 64 * ks + vb * 16 * L::kRowBytes);
+      };
+      u32x4 af[3][2];
+      af[0][0] = af_at(0, 0);
+      af[0][1] = af_at(0, 1);
+      if (KF > 1) {
+        af[1][0] = af_at(1, 0);
+        af[1][1] = af_at(1, 1);
+      }
+#pragma unroll
+      for (int ks = 0; ks < KF; ++ks) {
+        if (ks + 2 < KF) {
+          af[(ks + 2) % 3][0] = af_at(ks + 2, 0);
+          af[(ks + 2) % 3][1] = af_at(ks + 2, 1);
+        }
 #pragma unroll
         for (int vb = 0; vb < 2; ++vb)
-          pr[k][vb] = *reinterpret_cast<const f32x4_t*>(
-              part + (((ww * 3 + slot) * 2 + vb) * 64 + lane) * 16);
+          sa[vb][ks & 1] = mfma<Tag>(af[ks % 3][vb], xs[ks], sa[vb][ks & 1]);
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int vb = 0; vb < 2; ++vb) tot[vb] += (pr[0][vb] + pr[1][vb]) + pr[2][vb];
+      for (int vb = 0; vb < 2; ++vb) tot[vb] = sa[vb][0] + sa[vb][1];
+    }
+
+    // ---- this wave's 16 rows: softmax weights or gradient weights ----
+    float s[8];
+    {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         s[r] = tot[0][r];
@@ -357,7 +339,7 @@ __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
       float tmax = -__builtin_huge_valf();
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int32_t v = t * kBN + 4 * lg + (i & 3) + 16 * (i >> 2);
+        const int32_t v = tile_row0(t) + 4 * lg + (i & 3) + 16 * (i >> 2);
         if (v >= a.V) s[i] = -__builtin_huge_valf();
         if (v == tg) {
           xa = s[i];
@@ -398,10 +380,9 @@ __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
         for (int i = 0; i < 4; ++i) pk[i] = pack2<Tag>(p[2 * i], p[2 * i + 1]);
       }
     }
-    if constexpr (kAcc) lds_store16(frag, (w * 64 + lane) * 16, u32x4{pk[0], pk[1], pk[2], pk[3]});
-    // B: fragments published; every wave's partial reads are done.
-    lds_barrier();
     if constexpr (kAcc) {
+      lds_store16(frag, (w * 64 + lane) * 16, u32x4{pk[0], pk[1], pk[2], pk[3]});
+      lds_barrier();  // B: every wave's fragments published
 
       u32x4 pf[4];
 #pragma unroll
@@ -503,6 +484,74 @@ __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
       }
     }
   }
+}
+
+template <class Tag, int MODE, int H>
+__global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LdsLayout<H>::kTotal];
+  if constexpr (MODE == kModeFwd) {
+    // A block of 64 tokens none of which needs obar (masked tokens, whose
+    // d loss / d logp is zero) takes the log-sum-exp-only pass: half the
+    // MFMA work.  Every wave reads the same 64 flags, so the branch is
+    // uniform across the workgroup.
+    if (a.need_obar != nullptr) {
+      const int32_t row = (int32_t)blockIdx.x * kBM + (int32_t)(threadIdx.x & 63);
+      const bool need = row < a.nx && a.need_obar[row] != 0;
+      if (__builtin_amdgcn_ballot_w64(need) == 0) {
+        lm_tile_body<Tag, kModeFwdLseOnly, H>(a, lds);
+        return;
+      }
+    }
+  }
+  lm_tile_body<Tag, MODE, H>(a, lds);
+}
+
+// Tiles of 32 streamed tokens that hold a token with g != 0 (the others
+// contribute exactly zero to dW): flags, then one workgroup lists them in
+// ascending order.
+__global__ __launch_bounds__(256) void lm_tile_flags_kernel(int32_t n, const float* g,
+                                                            uint8_t* flags) {
+  const int32_t ntiles = (n + kBN - 1) / kBN;
+  for (int32_t tile = blockIdx.x * 256 + threadIdx.x; tile < ntiles;
+       tile += gridDim.x * 256) {
+    const int32_t b = tile * kBN, e = n - b < kBN ? n : b + kBN;
+    bool act = false;
+    if (e - b == kBN && ((uintptr_t)(g + b) & 15) == 0) {
+      const float4* q = reinterpret_cast<const float4*>(g + b);
+#pragma unroll
+      for (int i = 0; i < kBN / 4; ++i) {
+        const float4 v = q[i];
+        act |= (v.x != 0.f) | (v.y != 0.f) | (v.z != 0.f) | (v.w != 0.f);
+      }
+    } else {
+      for (int32_t i = b; i < e; ++i) act |= g[i] != 0.f;
+    }
+    flags[tile] = act ? 1 : 0;
+  }
+}
+
+__global__ __launch_bounds__(1024) void lm_tile_list_kernel(int32_t n, const uint8_t* flags,
+                                                            int32_t* list, int32_t* count) {
+  __shared__ int32_t wcount[16];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int32_t ntiles = (n + kBN - 1) / kBN;
+  int32_t base = 0;
+  for (int32_t c0 = 0; c0 < ntiles; c0 += 1024) {
+    const int32_t tile = c0 + tid;
+    const bool act = tile < ntiles && flags[tile] != 0;
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(act);
+    if (lane == 0) wcount[wv] = __popcll(bal);
+    __syncthreads();
+    int32_t before = base, total = base;
+    for (int k = 0; k < 16; ++k) {
+      if (k < wv) before += wcount[k];
+      total += wcount[k];
+    }
+    if (act) list[before + __popcll(bal & ((1ull << lane) - 1ull))] = tile;
+    base = total;
+    __syncthreads();
+  }
+  if (tid == 0) *count = base;
 }
 
 // Per-token records of the dW pass: {target (bits), g, lse*log2(e),
@@ -625,9 +674,9 @@ using namespace rrl;
 
 extern "C" int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t dtype, int64_t N,
                                int64_t H, int64_t V, int64_t h_ld, int64_t w_ld,
-                               const int32_t* targets, const float* mref_in, float* lse_out,
-                               float* logp_out, float* obar, int64_t obar_ld, int32_t* status,
-                               void* stream) {
+                               const int32_t* targets, const uint8_t* need_obar,
+                               const float* mref_in, float* lse_out, float* logp_out, float* obar,
+                               int64_t obar_ld, int32_t* status, void* stream) {
   clear_error();
   if (int rc = check_operands(dtype, N, H, V, hidden, h_ld, weight, w_ld)) return rc;
   if (N == 0) return RRL_OK;
@@ -641,14 +690,25 @@ extern "C" int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t d
   a.y = weight; a.y_ld = w_ld; a.ny = (int32_t)V;
   a.V = (int32_t)V;
   a.tgt = targets; a.lse_out = lse_out; a.logp_out = logp_out;
-  a.obar = obar; a.obar_ld = obar_ld; a.mref_in = mref_in; a.status = status;
+  a.obar = obar; a.obar_ld = obar_ld; a.mref_in = mref_in; a.need_obar = need_obar;
+  a.status = status;
   hipStream_t st = as_stream(stream);
   return obar ? launch_tiles_dt<kModeFwd>(dtype, a, H, st)
               : launch_tiles_dt<kModeFwdLseOnly>(dtype, a, H, st);
 }
 
+// Workspace of rrl_lm_head_dweight: 16-byte token records, then the tile
+// flags, then the active tile list and its count.
+namespace {
+size_t records_part(int64_t N) { return ((size_t)(N > 0 ? N : 0) * 16 + 255) & ~(size_t)255; }
+size_t flags_part(int64_t N) {
+  return ((size_t)((N > 0 ? N : 0) + kBN - 1) / kBN + 255) & ~(size_t)255;
+}
+}  // namespace
+
 extern "C" size_t rrl_lm_head_records_bytes(int64_t N) {
-  return (size_t)(N > 0 ? N : 0) * 16 + 256;
+  const size_t ntiles = (size_t)((N > 0 ? N : 0) + kBN - 1) / kBN;
+  return records_part(N) + flags_part(N) + (ntiles + 64) * 4 + 256;
 }
 
 extern "C" int rrl_lm_head_dhidden(const void* weight, int32_t dtype, int64_t N, int64_t H,
@@ -686,15 +746,30 @@ extern "C" int rrl_lm_head_dweight(const void* hidden, const void* weight, int32
               "lm head: null pointer argument");
   RRL_REQUIRE((uintptr_t)records % 16 == 0, RRL_EALIGN, "lm head: records must be 16-byte aligned");
   hipStream_t st = as_stream(stream);
+  uint8_t* ws = static_cast<uint8_t*>(records);
+  uint8_t* flags = ws + records_part(N);
+  int32_t* list = reinterpret_cast<int32_t*>(flags + flags_part(N));
+  const int64_t ntiles = (N + kBN - 1) / kBN;
+  int32_t* count = list + ntiles + 32;
   if (N > 0) {
     int cus = 256;
     cu_count(&cus);
     const unsigned rg = (unsigned)((N + 255) / 256 < 16 * cus ? (N + 255) / 256 : 16 * cus);
     hipLaunchKernelGGL(lm_token_records_kernel, dim3(rg), dim3(256), 0, st, N, (int32_t)V,
-                       targets, lse, logp, g, static_cast<float4*>(records));
+                       targets, lse, logp, g, reinterpret_cast<float4*>(ws));
     if (int rc = check_launch("lm_token_records_kernel")) return rc;
+    const unsigned fg = (unsigned)((ntiles + 255) / 256 < 4 * cus ? (ntiles + 255) / 256 : 4 * cus);
+    hipLaunchKernelGGL(lm_tile_flags_kernel, dim3(fg), dim3(256), 0, st, (int32_t)N, g, flags);
+    if (int rc = check_launch("lm_tile_flags_kernel")) return rc;
+    hipLaunchKernelGGL(lm_tile_list_kernel, dim3(1), dim3(1024), 0, st, (int32_t)N, flags, list,
+                       count);
+    if (int rc = check_launch("lm_tile_list_kernel")) return rc;
   }
   LmArgs a{};
+  if (N > 0) {
+    a.tile_list = list;
+    a.tile_count = count;
+  }
   a.x = weight; a.x_ld = w_ld; a.nx = (int32_t)V;
   a.y = hidden; a.y_ld = h_ld; a.ny = (int32_t)N;
   a.V = (int32_t)V;

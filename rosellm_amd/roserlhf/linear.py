@@ -92,13 +92,15 @@ def _targets_i32(target_ids: Tensor, n: int) -> Tensor:
     return target_ids.reshape(n).to(torch.int32).contiguous()
 
 
-def lm_head_forward(h2: Tensor, w: Tensor, tgt32: Tensor, want_obar: bool, status: Tensor
+def lm_head_forward(h2: Tensor, w: Tensor, tgt32: Tensor, want_obar: bool, status: Tensor,
+                    need: Optional[Tensor] = None
                     ) -> Tuple[Tensor, Tensor, Optional[Tensor], int]:
     """(lse, logp, obar, status flags): lse and logp float32 [N], obar float32
     [N, H] when ``want_obar`` (else None).  Reads the status word once (one
     host synchronisation).  If a token's logits leave the single pass's fixed
     reference range (flag LM_RANGE), the pass is redone around the exact
-    log-sum-exp of a second, log-sum-exp-only pass."""
+    log-sum-exp of a second, log-sum-exp-only pass.  ``need``: optional uint8
+    [N]; 64-token blocks with no needed token skip obar (left unwritten)."""
 
     dev = h2.device
     N, H = h2.shape
@@ -108,19 +110,20 @@ def lm_head_forward(h2: Tensor, w: Tensor, tgt32: Tensor, want_obar: bool, statu
     lse = torch.empty(N, dtype=torch.float32, device=dev)
     logp = torch.empty(N, dtype=torch.float32, device=dev)
     obar = torch.empty((N, H), dtype=torch.float32, device=dev) if want_obar else None
+    need_p = nat.ptr(need) if (want_obar and need is not None) else None
     nat.call("rrl_lm_head_fwd", h2.data_ptr(), w.data_ptr(), dt, N, H, V, h2.stride(0),
-             w.stride(0), tgt32.data_ptr(), None, lse.data_ptr(), logp.data_ptr(), nat.ptr(obar),
-             H, status.data_ptr(), stream)
+             w.stride(0), tgt32.data_ptr(), need_p, None, lse.data_ptr(), logp.data_ptr(),
+             nat.ptr(obar), H, status.data_ptr(), stream)
     flags = nat.read_status(status)
     if flags & nat.FLAG_LM_RANGE and want_obar:
         # Exact log-sum-exp first, then the single pass around it.
         mref = torch.empty(N, dtype=torch.float32, device=dev)
         nat.call("rrl_lm_head_fwd", h2.data_ptr(), w.data_ptr(), dt, N, H, V, h2.stride(0),
-                 w.stride(0), tgt32.data_ptr(), None, mref.data_ptr(), logp.data_ptr(), None, H,
-                 status.data_ptr(), stream)
+                 w.stride(0), tgt32.data_ptr(), None, None, mref.data_ptr(), logp.data_ptr(),
+                 None, H, status.data_ptr(), stream)
         nat.call("rrl_lm_head_fwd", h2.data_ptr(), w.data_ptr(), dt, N, H, V, h2.stride(0),
-                 w.stride(0), tgt32.data_ptr(), mref.data_ptr(), lse.data_ptr(), logp.data_ptr(),
-                 nat.ptr(obar), H, status.data_ptr(), stream)
+                 w.stride(0), tgt32.data_ptr(), need_p, mref.data_ptr(), lse.data_ptr(),
+                 logp.data_ptr(), nat.ptr(obar), H, status.data_ptr(), stream)
         flags = nat.read_status(status) & ~nat.FLAG_LM_RANGE
     return lse, logp, obar, flags
 
@@ -159,7 +162,7 @@ class _LinearLogprobs(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, check: nat.RrlPolicyParams, hidden: Tensor, weight: Tensor,
-                target_ids: Tensor):
+                target_ids: Tensor, weight_mask: Optional[Tensor] = None):
         dev = nat.require_device(hidden, weight, target_ids)
         B, T = _prepare(hidden, weight, target_ids)
         _check_mfma(hidden)
@@ -176,7 +179,12 @@ class _LinearLogprobs(torch.autograd.Function):
         nat.call("rrl_check_targets", L.ctypes_ref(check), B, T, V, tv, status.data_ptr(),
                  nat.stream_ptr(dev))
         need = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
-        lse, logp, obar, flags = lm_head_forward(h2, w, tgt32, need, status)
+        # Tokens whose mask weight is zero get d loss / d logp = 0 from every
+        # objective here, so their obar (the d hidden term) is never read.
+        need_rows = None
+        if need and weight_mask is not None:
+            need_rows = (weight_mask.reshape(N) != 0).to(torch.uint8).contiguous()
+        lse, logp, obar, flags = lm_head_forward(h2, w, tgt32, need, status, need_rows)
         if flags & nat.FLAG_TARGET_RANGE:
             L._raise_flags(nat.FLAG_TARGET_RANGE, check.kind)
         ctx.save_for_backward(h2, w, tgt32, lse, logp, obar)
@@ -188,11 +196,11 @@ class _LinearLogprobs(torch.autograd.Function):
     def backward(ctx, g):
         need_h, need_w = ctx.needs_input_grad[1], ctx.needs_input_grad[2]
         if g is None or not (need_h or need_w):
-            return None, None, None, None
+            return None, None, None, None, None
         h2, w, tgt32, lse, logp, obar = ctx.saved_tensors
         gc = g.reshape(-1).to(torch.float32).contiguous()
         dh, dw = lm_head_backward(h2, w, tgt32, lse, logp, obar, gc, need_h, need_w)
-        return None, (dh.view(ctx.hidden_shape) if dh is not None else None), dw, None
+        return None, (dh.view(ctx.hidden_shape) if dh is not None else None), dw, None, None
 
 
 def linear_token_logprobs(hidden: Tensor, weight: Tensor, target_ids: Tensor, *,
@@ -222,7 +230,7 @@ def linear_label_logprobs(hidden: Tensor, weight: Tensor, labels: Tensor,
     p = nat.RrlPolicyParams()
     p.kind = nat.OBJ_NLL
     p.ignore_index = int(ignore_index)
-    return _LinearLogprobs.apply(p, hidden, weight, labels)
+    return _LinearLogprobs.apply(p, hidden, weight, labels, labels != int(ignore_index))
 
 
 def fused_linear_policy_loss(
@@ -270,8 +278,10 @@ def fused_linear_policy_loss(
                          "every token's log-prob")
     if row_block < 1:
         raise ValueError("row_block must be positive")
+    mask = L._on_device(action_mask, hidden)
+    ppo = L._params(nat.OBJ_PPO)
     if kind in (nat.OBJ_GSPO, nat.OBJ_GSPO_TOKEN):
-        logp = linear_token_logprobs(hidden, weight, target_ids)
+        logp = _LinearLogprobs.apply(ppo, hidden, weight, target_ids, mask)
         fn = L.gspo_policy_loss if kind == nat.OBJ_GSPO else L.gspo_token_policy_loss
         out = fn(logp, old_logprobs, advantages, action_mask, clip_low=clip_low,
                  clip_high=clip_low if clip_high is None else clip_high,
@@ -282,8 +292,7 @@ def fused_linear_policy_loss(
                               clip_low=clip_low, clip_high=clip_high,
                               max_log_ratio=max_log_ratio, detach_ratio=detach_ratio,
                               tau_positive=tau_positive, tau_negative=tau_negative)
-    logp = linear_token_logprobs(hidden, weight, target_ids)
-    obj, d1, d2, d3, _seq, trusted = L._objective(p, logp, old_logprobs, advantages,
-                                                   action_mask)
+    logp = _LinearLogprobs.apply(ppo, hidden, weight, target_ids, mask)
+    obj, d1, d2, d3, _seq, trusted = L._objective(p, logp, old_logprobs, advantages, mask)
     out = L._token_local_output(kind, obj, d1, d2, d3, trusted)
     return (out, logp.detach()) if return_logprobs else out
