@@ -113,9 +113,34 @@ __device__ __forceinline__ void lds_store16(uint8_t* base, uint32_t off, u32x4 v
   *reinterpret_cast<u32x4*>(base + off) = v;
 }
 __device__ __forceinline__ uint2 lds_tr16(const uint8_t* base, uint32_t off) {
-  const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_i16x4_t*)(reinterpret_cast<uintptr_t>(base + off)));
+  const i16x4_t v =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(const_cast<uint8_t*>(base + off)));
   return __builtin_bit_cast(uint2, v);
+}
+
+// The dW pass's token records of tile columns 4g + {0..3} and 16 + 4g + {0..3}
+// (lane group g; `base` = the tile's records + 64 g bytes), with the wait for
+// them.  The compiler models a 16-byte LDS-DMA load as a 4-byte store, and its
+// alias analysis cannot place these reads apart from the next tile's loads
+// still in flight into the other buffer: written as plain loads they get a
+// vmcnt(0) wait, which would wait for the whole next tile.
+__device__ __forceinline__ void lds_read_records(const uint8_t* base, f32x4_t (&r)[8]) {
+  const uint32_t addr = (uint32_t)reinterpret_cast<uintptr_t>(base);
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %8 offset:16\n\t"
+      "ds_read_b128 %2, %8 offset:32\n\t"
+      "ds_read_b128 %3, %8 offset:48\n\t"
+      "ds_read_b128 %4, %8 offset:256\n\t"
+      "ds_read_b128 %5, %8 offset:272\n\t"
+      "ds_read_b128 %6, %8 offset:288\n\t"
+      "ds_read_b128 %7, %8 offset:304\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      // early-clobber outputs: the address must outlive the first read
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]),
+        "=&v"(r[6]), "=&v"(r[7])
+      : "v"(addr)
+      : "memory");
 }
 
 // Row exchange between the four 16-lane groups (lanes c, c+16, c+32, c+48).
@@ -151,15 +176,17 @@ struct LdsLayout {
   static constexpr int kRowBytes = H * 2 + kRowPad;
   static constexpr int kTileBytes = kBN * kRowBytes;
   static constexpr int kFragOff = 2 * kTileBytes;                 // [4 blocks][64] x 16 B
-  static constexpr int kRecOff = kFragOff + 4 * 64 * 16;           // [2][32] x 16 B (dW pass)
-  static constexpr int kAlphaOff = kRecOff + 2 * kBN * 16;         // [64] floats (epilogue)
-  static constexpr int kTotal = kAlphaOff + 64 * 4;
+  static constexpr int kPartOff = kFragOff + 4 * 64 * 16;          // [12 slots][2][64] x 16 B
+  static constexpr int kRecOff = kPartOff + 12 * 2 * 64 * 16;      // [2][32] x 16 B (dW pass)
+  static constexpr int kAlphaOff = kPartOff;                       // [64] floats (epilogue only)
+  static constexpr int kTotal = kRecOff + 2 * kBN * 16;
+  static_assert(kTotal <= 160 * 1024, "LDS budget of one workgroup");
 };
 
 template <class Tag, int MODE, int H>
 __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds) {
-  constexpr int DW = H / 4;                 // hidden slice of each wave's accumulator
-  constexpr int KF = H / 32;                // k-steps of the S product (full hidden size)
+  constexpr int DW = H / 4;                 // hidden slice of each wave (S depth and accumulator)
+  constexpr int KQ = DW / 32;               // k-steps of the S product over one slice
   constexpr int DB = DW / 16;               // 16-column blocks of the accumulator per wave
   constexpr int CH = H / 8;                 // 16-byte chunks per row
   constexpr bool kAcc = MODE != kModeFwdLseOnly;
@@ -171,15 +198,17 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds) {
   const int32_t x0 = (int32_t)blockIdx.x * kBM;
   const int dw0 = w * DW;
 
-  // ---- stationary fragments of this wave's 16 rows over the whole hidden
-  // size: X[x0 + 16w + lc][32ks + 8lg .. +7] ----
-  u32x4 xs[KF];
-  {
-    const int32_t row = x0 + 16 * w + lc;
-    const uint16_t* p = static_cast<const uint16_t*>(a.x) + (int64_t)row * a.x_ld + 8 * lg;
+  // ---- stationary fragments of all 64 rows over this wave's hidden slice,
+  // row blocks rotated so that slot 0 is the wave's own block:
+  // xs[j][ks] = X[x0 + 16((w + j) mod 4) + lc][dw0 + 32ks + 8lg .. +7] ----
+  u32x4 xs[4][KQ];
 #pragma unroll
-    for (int ks = 0; ks < KF; ++ks)
-      xs[ks] = row < a.nx ? *reinterpret_cast<const u32x4*>(p + 32 * ks) : u32x4{0, 0, 0, 0};
+  for (int j = 0; j < 4; ++j) {
+    const int32_t row = x0 + 16 * ((w + j) & 3) + lc;
+    const uint16_t* p = static_cast<const uint16_t*>(a.x) + (int64_t)row * a.x_ld + dw0 + 8 * lg;
+#pragma unroll
+    for (int ks = 0; ks < KQ; ++ks)
+      xs[j][ks] = row < a.nx ? *reinterpret_cast<const u32x4*>(p + 32 * ks) : u32x4{0, 0, 0, 0};
   }
 
   f32x4_t acc[4][kAcc ? DB : 1];
@@ -208,103 +237,157 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds) {
   }
 
   const int32_t ntiles = a.tile_count ? *a.tile_count : (a.ny + kBN - 1) / kBN;
-  auto tile_row0 = [&](int32_t t) { return (a.tile_list ? a.tile_list[t] : t) * kBN; };
+  // First streamed row of tile t, wave-uniform (a scalar register).
+  auto tile_row0 = [&](int32_t t) {
+    return __builtin_amdgcn_readfirstlane((a.tile_list ? a.tile_list[t] : t) * kBN);
+  };
 
   // ---- tile loads, global -> LDS directly (buffer loads with the LDS bit:
   // no registers).  One wave-wide load writes 64 consecutive lanes x UNIT
   // bytes of LDS, so a row (2H bytes, padded rows) is PER_ROW loads; UNIT is
-  // 16 bytes when a row is whole kilobytes, else 4.  The caller waits for
-  // vmcnt(0) before the barrier that publishes the tile. ----
+  // 16 bytes when a row is whole kilobytes, else 4.  Each wave issues WLOADS
+  // of them per tile, spread over the S phase's k-steps (CHUNK per step): a
+  // wave that issued them all at once would stall on the full load queue
+  // before its first MFMA.  The caller waits for vmcnt(0) before the barrier
+  // that publishes the tile. ----
   constexpr int UNIT = (2 * H) % 1024 == 0 ? 16 : 4;
   constexpr int PER_ROW = 2 * H / (64 * UNIT);
   constexpr int WLOADS = kBN * PER_ROW / 4;  // per wave per tile
   static_assert(kBN * PER_ROW % 4 == 0, "tile load split");
   typedef __attribute__((address_space(3))) void lds_void_t;
-  auto issue_tile = [&](int32_t t, int buf) {
-    const int32_t r0 = tile_row0(t);
+  // dW pass: the 32 token records of the next tile go through registers of
+  // wave 0's first 32 lanes (a plain load issued ahead of the tile's loads)
+  // and are written to LDS at the end of the current tile.
+  float4 rec_next = make_float4(0.f, 0.f, 0.f, 0.f);
+  constexpr int CHUNK = (WLOADS + KQ - 1) / KQ;
+  // Descriptor of the tile starting at streamed row r0 (and, in the dW pass,
+  // the load of its token records).
+  auto tile_src = [&](int32_t r0) {
     const int32_t rows = a.ny - r0 < kBN ? a.ny - r0 : kBN;
+    if constexpr (MODE == kModeDw) {
+      // records past the last token read as zeros (g = 0)
+      if (w == 0 && lane < kBN)
+        rec_next = lane < rows ? a.trec[r0 + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     const uint16_t* base = static_cast<const uint16_t*>(a.y) + (int64_t)r0 * a.y_ld;
     // Rows at or past `rows` start at or beyond the descriptor's byte count
     // (row stride >= H), so they read as zeros.
-    const __amdgpu_buffer_rsrc_t rs =
-        row_rsrc(base, (uint32_t)(((rows - 1) * a.y_ld + H) * 2));
-    uint8_t* tb = lds + buf * L::kTileBytes;
+    return row_rsrc(base, (uint32_t)(((rows - 1) * a.y_ld + H) * 2));
+  };
+  // This wave's loads i0 .. i1-1 of a tile into buffer tb (i0, i1 constant
+  // after unrolling).
+  auto issue_loads = [&](const __amdgpu_buffer_rsrc_t& rs, uint8_t* tb, int i0, int i1) {
 #pragma unroll
-    for (int i = 0; i < WLOADS; ++i) {
+    for (int i = i0; i < i1; ++i) {
       const int q = w * WLOADS + i;  // wave-uniform
       const int j = q / PER_ROW, part = q % PER_ROW;
       const uint32_t goff = (uint32_t)(j * a.y_ld * 2 + part * 64 * UNIT + lane * UNIT);
-      lds_void_t* dst = (lds_void_t*)(uintptr_t)(tb + j * L::kRowBytes + part * 64 * UNIT);
+      lds_void_t* dst = (lds_void_t*)(tb + j * L::kRowBytes + part * 64 * UNIT);
       if constexpr (UNIT == 16)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, goff, 0, 0, 0);
       else
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 4, goff, 0, 0, 0);
     }
+  };
+  auto publish_records = [&](int buf) {
     if constexpr (MODE == kModeDw) {
-      // the tile's 32 token records (512 bytes): two dword loads by wave 0;
-      // records past the last token read as zeros (g = 0)
-      if (w == 0) {
-        const __amdgpu_buffer_rsrc_t rr = row_rsrc(
-            a.trec + r0, (uint32_t)(rows * 16));
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rr, (lds_void_t*)(uintptr_t)(lds + L::kRecOff + buf * kBN * 16 + i * 256), 4,
-              (uint32_t)(i * 256 + lane * 4), 0, 0, 0);
-      }
+      if (w == 0 && lane < kBN)
+        *reinterpret_cast<float4*>(lds + L::kRecOff + buf * kBN * 16 + lane * 16) = rec_next;
     }
   };
 
-  if (ntiles > 0) issue_tile(0, 0);
+  int32_t r0_next = ntiles > 0 ? tile_row0(0) : 0;
+  if (ntiles > 0) issue_loads(tile_src(r0_next), lds, 0, WLOADS);
   // Every prologue load (the stationary fragments and tile 0) has landed.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt untouched
+  publish_records(0);
   lds_barrier();
 
   uint8_t* const frag = lds + L::kFragOff;
   float* const alpha = reinterpret_cast<float*>(lds + L::kAlphaOff);
 
-  for (int32_t t = 0; t < ntiles; ++t) {
-    const int buf = (int)(t & 1);
-    const uint8_t* tb = lds + buf * L::kTileBytes;
+  // One tile: tb is the tile being computed on, tn the buffer its successor
+  // is loaded into.  The two are distinct LDS objects for the compiler
+  // (restrict): without that, its alias analysis cannot tell the transposed
+  // reads of tb from the in-flight loads into tn and waits for all of them
+  // (vmcnt(0)) before the first transposed read.
+  auto tile_step = [&](const uint8_t* __restrict__ tb, uint8_t* __restrict__ tn, const int buf,
+                       const int32_t t) __attribute__((always_inline)) {
     // Tile t+1 goes to the other buffer, free since barrier C of tile t-1;
     // it has this whole tile's work to land.
     const bool more = t + 1 < ntiles;
-    if (more) issue_tile(t + 1, buf ^ 1);
+    // The first row of tile t was read when its loads were issued; reading
+    // tile_list here, before tile t+1's loads are in flight, keeps the wait
+    // for that read from also waiting for them.
+    const int32_t r0 = r0_next;
+    __amdgpu_buffer_rsrc_t rs_next;
+    if (more) {
+      r0_next = tile_row0(t + 1);
+      rs_next = tile_src(r0_next);
+    }
 
-    // ---- S phase: S^T[32 x 16] of the tile against this wave's own 16 rows
-    // over the whole hidden size (no cross-wave reduction).  Two accumulator
-    // chains per tile half; the fragments of step ks+2 are read while step
-    // ks's MFMAs run (the scheduling fences keep the compiler from hoisting
-    // every read). ----
+    // ---- S phase: partial S^T[32 x 64] of the tile against all 64 rows over
+    // this wave's hidden slice; each tile fragment read from LDS feeds four
+    // MFMAs (one per 16-row block).  The fragments of step ks+2 are read while
+    // step ks's MFMAs run (the scheduling fences keep the compiler from
+    // hoisting every read). ----
     f32x4_t tot[2];
     {
-      f32x4_t sa[2][2];
+      f32x4_t sa[4][2];
 #pragma unroll
-      for (int vb = 0; vb < 2; ++vb) sa[vb][0] = sa[vb][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      const uint8_t* abase = tb + lc * L::kRowBytes + 16 * lg;
+      for (int j = 0; j < 4; ++j) sa[j][0] = sa[j][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const uint8_t* abase = tb + lc * L::kRowBytes + 2 * dw0 + 16 * lg;
       auto af_at = [&](int ks, int vb) {
         return lds_load16(abase, 64 * ks + vb * 16 * L::kRowBytes);
       };
       u32x4 af[3][2];
       af[0][0] = af_at(0, 0);
       af[0][1] = af_at(0, 1);
-      if (KF > 1) {
+      if (KQ > 1) {
         af[1][0] = af_at(1, 0);
         af[1][1] = af_at(1, 1);
       }
 #pragma unroll
-      for (int ks = 0; ks < KF; ++ks) {
-        if (ks + 2 < KF) {
+      for (int ks = 0; ks < KQ; ++ks) {
+        if (more && ks * CHUNK < WLOADS)
+          issue_loads(rs_next, tn, ks * CHUNK,
+                      ks * CHUNK + CHUNK < WLOADS ? ks * CHUNK + CHUNK : WLOADS);
+        if (ks + 2 < KQ) {
           af[(ks + 2) % 3][0] = af_at(ks + 2, 0);
           af[(ks + 2) % 3][1] = af_at(ks + 2, 1);
         }
 #pragma unroll
         for (int vb = 0; vb < 2; ++vb)
-          sa[vb][ks & 1] = mfma<Tag>(af[ks % 3][vb], xs[ks], sa[vb][ks & 1]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            sa[j][vb] = mfma<Tag>(af[ks % 3][vb], xs[j][ks], sa[j][vb]);
         __builtin_amdgcn_sched_barrier(0);
       }
+
+      // ---- exchange: wave w sends its partials of the other three row blocks
+      // to their owners (slot 3d + s' holds source s' of the other sources
+      // of destination block d, in source order), then adds them to its own
+      // partial in that order. ----
+      uint8_t* const part = lds + L::kPartOff;
 #pragma unroll
-      for (int vb = 0; vb < 2; ++vb) tot[vb] = sa[vb][0] + sa[vb][1];
+      for (int j = 1; j < 4; ++j) {
+        const int d = (w + j) & 3;  // wave-uniform
+        const int sl = 3 * d + (w < d ? w : w - 1);
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb)
+          lds_store16(part, (uint32_t)((2 * sl + vb) * 1024 + lane * 16),
+                      __builtin_bit_cast(u32x4, sa[j][vb]));
+      }
+      lds_barrier();  // A: partials published
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb) {
+        f32x4_t o[3];
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+          o[q] = __builtin_bit_cast(
+              f32x4_t, lds_load16(part, (uint32_t)((2 * (3 * w + q) + vb) * 1024 + lane * 16)));
+        tot[vb] = ((sa[0][vb] + o[0]) + o[1]) + o[2];
+      }
     }
 
     // ---- this wave's 16 rows: softmax weights or gradient weights ----
@@ -321,12 +404,12 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds) {
     if constexpr (MODE == kModeDw) {
       // P^T[v][n] = g_n ([v == a_n] - exp(s - lse_n)), the target entry as
       // g_n (-expm1(logp_n)) (exact as p -> 1).
-      const float* recs = reinterpret_cast<const float*>(lds + L::kRecOff + buf * kBN * 16);
+      f32x4_t rcs[8];
+      lds_read_records(lds + L::kRecOff + buf * kBN * 16 + 64 * lg, rcs);
       float p[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int col = 4 * lg + (i & 3) + 16 * (i >> 2);
-        const float4 rc = *reinterpret_cast<const float4*>(recs + col * 4);
+        const f32x4_t rc = rcs[i];
         const int32_t an = __float_as_int(rc.x);
         const float gn = rc.y;
         const float e = exp2_hw(s[i] * kLog2e - rc.z);
@@ -336,17 +419,24 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds) {
       for (int i = 0; i < 4; ++i) pk[i] = pack2<Tag>(p[2 * i], p[2 * i + 1]);
     } else {
       // Softmax weights of row my_row over this tile (target column held out).
+      // Columns past the vocabulary (last tile only) and a row's target column
+      // (in a tile holding some row's target) take the per-column path; the
+      // test is wave-uniform.
+      const bool tgt_here = tg >= r0 && tg < r0 + kBN;
+      if (r0 + kBN > a.V || __builtin_amdgcn_ballot_w64(tgt_here) != 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int32_t v = r0 + 4 * lg + (i & 3) + 16 * (i >> 2);
+          if (v >= a.V) s[i] = -__builtin_huge_valf();
+          if (v == tg) {
+            xa = s[i];
+            s[i] = -__builtin_huge_valf();
+          }
+        }
+      }
       float tmax = -__builtin_huge_valf();
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int32_t v = tile_row0(t) + 4 * lg + (i & 3) + 16 * (i >> 2);
-        if (v >= a.V) s[i] = -__builtin_huge_valf();
-        if (v == tg) {
-          xa = s[i];
-          s[i] = -__builtin_huge_valf();
-        }
-        tmax = fmaxf(tmax, s[i]);
-      }
+      for (int i = 0; i < 8; ++i) tmax = fmaxf(tmax, s[i]);
       if constexpr (MODE == kModeFwdLseOnly) {
         // No accumulator: each lane keeps an exact running maximum of its own
         // columns, l rescaled as it moves; the row's four lanes merge at the end.
@@ -410,7 +500,12 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds) {
       }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of tile t+1 landed
+    if (more) publish_records(buf ^ 1);  // tile t's records were read before barrier B
     lds_barrier();  // C: tile t+1 complete; tile t's reads done
+  };
+  for (int32_t t = 0; t < ntiles; ++t) {
+    const int buf = (int)(t & 1);
+    tile_step(lds + buf * L::kTileBytes, lds + (buf ^ 1) * L::kTileBytes, buf, t);
   }
 
   // ---- epilogue ----
