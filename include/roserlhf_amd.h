@@ -344,12 +344,15 @@ RRL_API int rrl_masked_whiten(int64_t B, int64_t T, rrl_view x, rrl_view mask, d
  * NULL, or uint8 [N] (nonzero: the token's obar is needed); a block of 64
  * consecutive tokens none of which needs it takes the log-sum-exp-only pass
  * and its obar rows are left unwritten (for tokens whose d loss / d logp is
- * zero by construction, such as masked tokens). */
+ * zero by construction, such as masked tokens).  workspace: with need_obar
+ * and obar, rrl_lm_head_fwd_workspace_bytes(N) bytes of caller device memory
+ * (16-byte aligned; the order in which the blocks are taken), else ignored. */
+RRL_API size_t rrl_lm_head_fwd_workspace_bytes(int64_t N);
 RRL_API int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t dtype, int64_t N,
                     int64_t H, int64_t V, int64_t h_ld, int64_t w_ld, const int32_t* targets,
                     const uint8_t* need_obar, const float* mref_in, float* lse_out,
-                    float* logp_out, float* obar, int64_t obar_ld, int32_t* status,
-                    void* stream);
+                    float* logp_out, float* obar, int64_t obar_ld, void* workspace,
+                    int32_t* status, void* stream);
 
 /* dhidden[n] = g[n] * ((-expm1(logp[n])) * weight[target[n]] - obar[n]), in the
  * weight dtype, rows dh_ld apart (the linear map's backward of a1's gradient

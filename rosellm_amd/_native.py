@@ -114,7 +114,8 @@ SIGNATURES = {
     "rrl_masked_whiten": (ctypes.c_int, [_I64, _I64, _V, _V, _D, _I32, _I32, _P, _P, _I32, _P, _P]),
     "rrl_sample_logprobs": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _D, _I64, _D, _I32,
                                            ctypes.c_uint64, ctypes.c_uint64, _P, _P, _P, _P, _P]),
-    "rrl_lm_head_fwd": (ctypes.c_int, [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _P, _P]),
+    "rrl_lm_head_fwd_workspace_bytes": (ctypes.c_size_t, [_I64]),
+    "rrl_lm_head_fwd": (ctypes.c_int, [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P]),
     "rrl_lm_head_dhidden": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P]),
     "rrl_lm_head_records_bytes": (ctypes.c_size_t, [_I64]),
     "rrl_lm_head_dweight": (ctypes.c_int, [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32, _I64, _P]),

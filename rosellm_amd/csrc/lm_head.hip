@@ -162,6 +162,8 @@ struct LmArgs {
   int64_t obar_ld;
   const float* mref_in;  // forward: per-token reference point (NULL: first-tile rule)
   const uint8_t* need_obar;  // forward: per-token "obar needed" (NULL: every token)
+  const int32_t* block_order;  // forward with need_obar: workgroup i takes 64-token block
+                               // block_order[i] (the blocks that need obar first)
   const int32_t* tile_list;  // dW pass: indices of the streamed tiles to visit (NULL: all)
   const int32_t* tile_count; // dW pass: number of entries of tile_list
   const float4* trec;    // dW pass: per streamed token {target bits, g, lse*log2e, g*(-expm1(logp))}
@@ -184,7 +186,7 @@ struct LdsLayout {
 };
 
 template <class Tag, int MODE, int H>
-__device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds) {
+__device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, const int32_t x0) {
   constexpr int DW = H / 4;                 // hidden slice of each wave (S depth and accumulator)
   constexpr int KQ = DW / 32;               // k-steps of the S product over one slice
   constexpr int DB = DW / 16;               // 16-column blocks of the accumulator per wave
@@ -195,7 +197,6 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds) {
 
   const int tid = threadIdx.x, lane = tid & 63, lg = lane >> 4, lc = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
-  const int32_t x0 = (int32_t)blockIdx.x * kBM;
   const int dw0 = w * DW;
 
   // ---- stationary fragments of all 64 rows over this wave's hidden slice,
@@ -588,17 +589,25 @@ __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
     // A block of 64 tokens none of which needs obar (masked tokens, whose
     // d loss / d logp is zero) takes the log-sum-exp-only pass: half the
     // MFMA work.  Every wave reads the same 64 flags, so the branch is
-    // uniform across the workgroup.
+    // uniform across the workgroup.  Workgroups take the blocks in
+    // block_order, those that need obar first: consecutive workgroups go to
+    // the eight XCDs in turn, so this spreads both kinds evenly over them,
+    // and the workgroups resident at one time stream the weight at one speed
+    // and share its tiles in L2.  (In token order, masks that end each
+    // sequence's response in a run of masked blocks load the XCDs unevenly:
+    // measured as slow as obar for every block.)
     if (a.need_obar != nullptr) {
-      const int32_t row = (int32_t)blockIdx.x * kBM + (int32_t)(threadIdx.x & 63);
+      const int32_t blk = __builtin_amdgcn_readfirstlane(a.block_order[blockIdx.x]);
+      const int32_t row = blk * kBM + (int32_t)(threadIdx.x & 63);
       const bool need = row < a.nx && a.need_obar[row] != 0;
-      if (__builtin_amdgcn_ballot_w64(need) == 0) {
-        lm_tile_body<Tag, kModeFwdLseOnly, H>(a, lds);
-        return;
-      }
+      if (__builtin_amdgcn_ballot_w64(need) == 0)
+        lm_tile_body<Tag, kModeFwdLseOnly, H>(a, lds, blk * kBM);
+      else
+        lm_tile_body<Tag, MODE, H>(a, lds, blk * kBM);
+      return;
     }
   }
-  lm_tile_body<Tag, MODE, H>(a, lds);
+  lm_tile_body<Tag, MODE, H>(a, lds, (int32_t)blockIdx.x * kBM);
 }
 
 // Tiles of 32 streamed tokens that hold a token with g != 0 (the others
@@ -647,6 +656,47 @@ __global__ __launch_bounds__(1024) void lm_tile_list_kernel(int32_t n, const uin
     __syncthreads();
   }
   if (tid == 0) *count = base;
+}
+
+// Order of the forward's 64-token blocks: those with a token whose obar is
+// needed first, then the others, each in ascending order (one workgroup).
+__global__ __launch_bounds__(1024) void lm_block_order_kernel(int32_t n, const uint8_t* need,
+                                                              int32_t* order) {
+  __shared__ int32_t wcount[16];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int32_t nblocks = (n + kBM - 1) / kBM;
+  int32_t base = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int32_t c0 = 0; c0 < nblocks; c0 += 1024) {
+      const int32_t blk = c0 + tid;
+      bool any = false;
+      if (blk < nblocks) {
+        const int32_t b = blk * kBM, e = n - b < kBM ? n : b + kBM;
+        if (e - b == kBM && ((uintptr_t)(need + b) & 15) == 0) {
+          const uint4* q = reinterpret_cast<const uint4*>(need + b);
+#pragma unroll
+          for (int i = 0; i < kBM / 16; ++i) {
+            const uint4 v = q[i];
+            any |= (v.x | v.y | v.z | v.w) != 0u;
+          }
+        } else {
+          for (int32_t i = b; i < e; ++i) any |= need[i] != 0;
+        }
+      }
+      const bool take = blk < nblocks && any == (pass == 0);
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(take);
+      if (lane == 0) wcount[wv] = __popcll(bal);
+      __syncthreads();
+      int32_t before = base, total = base;
+      for (int k = 0; k < 16; ++k) {
+        if (k < wv) before += wcount[k];
+        total += wcount[k];
+      }
+      if (take) order[before + __popcll(bal & ((1ull << lane) - 1ull))] = blk;
+      base = total;
+      __syncthreads();
+    }
+  }
 }
 
 // Per-token records of the dW pass: {target (bits), g, lse*log2(e),
@@ -771,7 +821,7 @@ extern "C" int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t d
                                int64_t H, int64_t V, int64_t h_ld, int64_t w_ld,
                                const int32_t* targets, const uint8_t* need_obar,
                                const float* mref_in, float* lse_out, float* logp_out, float* obar,
-                               int64_t obar_ld, int32_t* status, void* stream) {
+                               int64_t obar_ld, void* workspace, int32_t* status, void* stream) {
   clear_error();
   if (int rc = check_operands(dtype, N, H, V, hidden, h_ld, weight, w_ld)) return rc;
   if (N == 0) return RRL_OK;
@@ -788,8 +838,26 @@ extern "C" int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t d
   a.obar = obar; a.obar_ld = obar_ld; a.mref_in = mref_in; a.need_obar = need_obar;
   a.status = status;
   hipStream_t st = as_stream(stream);
-  return obar ? launch_tiles_dt<kModeFwd>(dtype, a, H, st)
-              : launch_tiles_dt<kModeFwdLseOnly>(dtype, a, H, st);
+  if (!obar) {
+    a.need_obar = nullptr;
+    return launch_tiles_dt<kModeFwdLseOnly>(dtype, a, H, st);
+  }
+  if (need_obar) {
+    RRL_REQUIRE(workspace != nullptr && ((uintptr_t)workspace & 15) == 0, RRL_EINVAL,
+                "lm head: need_obar requires a 16-byte aligned workspace of "
+                "rrl_lm_head_fwd_workspace_bytes(N) bytes");
+    int32_t* order = static_cast<int32_t*>(workspace);
+    hipLaunchKernelGGL(lm_block_order_kernel, dim3(1), dim3(1024), 0, st, (int32_t)N, need_obar,
+                       order);
+    if (int rc = check_launch("lm_block_order_kernel")) return rc;
+    a.block_order = order;
+  }
+  return launch_tiles_dt<kModeFwd>(dtype, a, H, st);
+}
+
+extern "C" size_t rrl_lm_head_fwd_workspace_bytes(int64_t N) {
+  if (N <= 0) return 0;
+  return (size_t)(((N + kBM - 1) / kBM) * 4 + 255) / 256 * 256;
 }
 
 // Workspace of rrl_lm_head_dweight: 16-byte token records, then the tile

@@ -111,19 +111,23 @@ def lm_head_forward(h2: Tensor, w: Tensor, tgt32: Tensor, want_obar: bool, statu
     logp = torch.empty(N, dtype=torch.float32, device=dev)
     obar = torch.empty((N, H), dtype=torch.float32, device=dev) if want_obar else None
     need_p = nat.ptr(need) if (want_obar and need is not None) else None
+    ws = None
+    if need_p is not None:
+        ws = torch.empty(nat.lib().rrl_lm_head_fwd_workspace_bytes(N), dtype=torch.uint8,
+                         device=dev)
     nat.call("rrl_lm_head_fwd", h2.data_ptr(), w.data_ptr(), dt, N, H, V, h2.stride(0),
              w.stride(0), tgt32.data_ptr(), need_p, None, lse.data_ptr(), logp.data_ptr(),
-             nat.ptr(obar), H, status.data_ptr(), stream)
+             nat.ptr(obar), H, nat.ptr(ws), status.data_ptr(), stream)
     flags = nat.read_status(status)
     if flags & nat.FLAG_LM_RANGE and want_obar:
         # Exact log-sum-exp first, then the single pass around it.
         mref = torch.empty(N, dtype=torch.float32, device=dev)
         nat.call("rrl_lm_head_fwd", h2.data_ptr(), w.data_ptr(), dt, N, H, V, h2.stride(0),
                  w.stride(0), tgt32.data_ptr(), None, None, mref.data_ptr(), logp.data_ptr(),
-                 None, H, status.data_ptr(), stream)
+                 None, H, None, status.data_ptr(), stream)
         nat.call("rrl_lm_head_fwd", h2.data_ptr(), w.data_ptr(), dt, N, H, V, h2.stride(0),
                  w.stride(0), tgt32.data_ptr(), need_p, mref.data_ptr(), lse.data_ptr(),
-                 logp.data_ptr(), nat.ptr(obar), H, status.data_ptr(), stream)
+                 logp.data_ptr(), nat.ptr(obar), H, nat.ptr(ws), status.data_ptr(), stream)
         flags = nat.read_status(status) & ~nat.FLAG_LM_RANGE
     return lse, logp, obar, flags
 
