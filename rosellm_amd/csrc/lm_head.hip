@@ -31,9 +31,9 @@
 // {4g..4g+3, 16+4g..16+4g+3} for lane group g; the Y fragments of the
 // accumulation product use the same k order.
 //
-// LDS (H = 1024): two Y tiles of 32 x 1024 (double buffer, 128 KB, 16-byte
-// chunks XOR-swizzled by row so that both the natural and the transposed reads
-// are bank-conflict free), 24 KB of partials, 4 KB of fragments.
+// LDS (H = 1024): two Y tiles of 32 x 1024 (double buffer, 130 KB with rows
+// padded so that both the natural and the transposed reads are bank-conflict
+// free), 24 KB of partials, 4 KB of fragments, 1 KB of token records.
 #include <mutex>
 #include <type_traits>
 
@@ -98,13 +98,14 @@ __device__ __forceinline__ float widen(uint16_t h) {
   else return (float)__builtin_bit_cast(_Float16, h);
 }
 
-// Tile rows in LDS are 2H + 48 bytes apart (2H is a multiple of 256, the
-// width of the 64 banks).  Natural reads (16 lanes, 16 consecutive rows, one
-// 16-byte chunk each) land 48 bytes apart modulo 256: 16 distinct bank
-// groups.  Transposed reads (16 lanes, 4 consecutive rows x 32 bytes) cover
-// [48i, 48i + 32) modulo 256: disjoint.  Every address is a per-lane base
-// plus a compile-time offset.
-constexpr int kRowPad = 48;
+// Tile rows in LDS are 2H + 32 bytes apart.  Both read patterns of the tile
+// (natural: 16 lanes on 16 consecutive rows, one 16-byte chunk each;
+// transposed: ds_read_b64_tr_b16 over 4 consecutive rows x 32 bytes) are
+// bank-conflict free at that pitch for H = 1024 (measured with the
+// SQ_LDS_BANK_CONFLICT counter on gfx950: zero at 2H + 32, two extra cycles
+// per transposed read at 2H + 16, 2H + 48 and 2H + 64).  Every address is a
+// per-lane base plus a compile-time offset.
+constexpr int kRowPad = 32;
 
 __device__ __forceinline__ u32x4 lds_load16(const uint8_t* base, uint32_t off) {
   return *reinterpret_cast<const u32x4*>(base + off);
