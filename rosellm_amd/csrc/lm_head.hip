@@ -148,6 +148,28 @@ __device__ __forceinline__ void lds_read_records(const uint8_t* base, f32x4_t (&
 __device__ __forceinline__ float xor16(float v) { return __shfl_xor(v, 16, 64); }
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
+// lse and logp of one row from its merged state: l = the sum of exp(s - mr)
+// over its non-target columns, xt = the target column's logit (-inf: not
+// seen), tg < 0: no target (logp 0).  lse = log(l e^mr + e^xt); logp = xt - lse
+// is formed as -log1p(l e^(mr - xt)) so that it keeps its relative precision
+// as p_target -> 1.
+__device__ __forceinline__ void finish_row(float mr, float l, float xt, int32_t tg, float& lse,
+                                           float& logp) {
+  if (xt == -__builtin_huge_valf()) {
+    lse = mr == -__builtin_huge_valf() ? -__builtin_huge_valf() : mr + logf(l);
+    logp = tg < 0 ? 0.f : -__builtin_huge_valf();  // no target: 0
+  } else if (mr == -__builtin_huge_valf() || l == 0.f) {
+    lse = xt;
+    logp = 0.f;
+  } else {
+    const float M = fmaxf(mr, xt);
+    lse = M + logf(l * expf(mr - M) + expf(xt - M));
+    const float d = mr - xt;
+    const float z = l * expf(fminf(d, 80.f));
+    logp = (d < 80.f && z < 1e30f) ? -log1pf(z) : -(d + logf(l));
+  }
+}
+
 struct LmArgs {
   const void* x;  // stationary rows [nx, H], row stride x_ld elements
   int64_t x_ld;
@@ -163,8 +185,9 @@ struct LmArgs {
   int64_t obar_ld;
   const float* mref_in;  // forward: per-token reference point (NULL: first-tile rule)
   const uint8_t* need_obar;  // forward: per-token "obar needed" (NULL: every token)
-  const int32_t* block_order;  // forward with need_obar: workgroup i takes 64-token block
-                               // block_order[i] (the blocks that need obar first)
+  const int32_t* block_order;  // forward with need_obar: the 64-token blocks, those that
+                               // need obar first
+  const int32_t* block_count;  // forward with need_obar: how many blocks need obar
   const int32_t* tile_list;  // dW pass: indices of the streamed tiles to visit (NULL: all)
   const int32_t* tile_count; // dW pass: number of entries of tile_list
   const float4* trec;    // dW pass: per streamed token {target bits, g, lse*log2e, g*(-expm1(logp))}
@@ -523,23 +546,9 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, cons
     l += xor32(l);
     float xt = fmaxf(xa, xor16(xa));
     xt = fmaxf(xt, xor32(xt));
-    // lse = log(l e^m_ref + e^xt); logp = xt - lse formed as -log1p(l e^(m_ref - xt))
-    // so that it keeps its relative precision as p_target -> 1.
     float lse, logp;
     const float mr = m_ref;
-    if (xt == -__builtin_huge_valf()) {
-      lse = mr == -__builtin_huge_valf() ? -__builtin_huge_valf() : mr + logf(l);
-      logp = tg < 0 ? 0.f : -__builtin_huge_valf();  // no target: 0
-    } else if (mr == -__builtin_huge_valf() || l == 0.f) {
-      lse = xt;
-      logp = 0.f;
-    } else {
-      const float M = fmaxf(mr, xt);
-      lse = M + logf(l * expf(mr - M) + expf(xt - M));
-      const float d = mr - xt;
-      const float z = l * expf(fminf(d, 80.f));
-      logp = (d < 80.f && z < 1e30f) ? -log1pf(z) : -(d + logf(l));
-    }
+    finish_row(mr, l, xt, tg, lse, logp);
     if (lg == 0 && my_row < a.nx) {
       a.lse_out[my_row] = lse;
       a.logp_out[my_row] = logp;
@@ -587,28 +596,212 @@ template <class Tag, int MODE, int H>
 __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[LdsLayout<H>::kTotal];
   if constexpr (MODE == kModeFwd) {
-    // A block of 64 tokens none of which needs obar (masked tokens, whose
-    // d loss / d logp is zero) takes the log-sum-exp-only pass: half the
-    // MFMA work.  Every wave reads the same 64 flags, so the branch is
-    // uniform across the workgroup.  Workgroups take the blocks in
-    // block_order, those that need obar first: consecutive workgroups go to
-    // the eight XCDs in turn, so this spreads both kinds evenly over them,
-    // and the workgroups resident at one time stream the weight at one speed
-    // and share its tiles in L2.  (In token order, masks that end each
-    // sequence's response in a run of masked blocks load the XCDs unevenly:
-    // measured as slow as obar for every block.)
-    if (a.need_obar != nullptr) {
+    // With need_obar, workgroup i takes block block_order[i] of the blocks
+    // that need obar (listed first); the blocks that do not are left to the
+    // log-sum-exp kernel.  Listing them first, rather than taking blocks in
+    // token order, spreads them evenly over the eight XCDs (consecutive
+    // workgroups go to the XCDs in turn): masks that end each sequence in a
+    // run of masked blocks otherwise load some XCDs with most of the obar
+    // work (measured: as slow as obar for every block).
+    if (a.block_order != nullptr) {
+      if ((int32_t)blockIdx.x >= *a.block_count) return;
       const int32_t blk = __builtin_amdgcn_readfirstlane(a.block_order[blockIdx.x]);
-      const int32_t row = blk * kBM + (int32_t)(threadIdx.x & 63);
-      const bool need = row < a.nx && a.need_obar[row] != 0;
-      if (__builtin_amdgcn_ballot_w64(need) == 0)
-        lm_tile_body<Tag, kModeFwdLseOnly, H>(a, lds, blk * kBM);
-      else
-        lm_tile_body<Tag, MODE, H>(a, lds, blk * kBM);
+      lm_tile_body<Tag, MODE, H>(a, lds, blk * kBM);
       return;
     }
   }
   lm_tile_body<Tag, MODE, H>(a, lds, (int32_t)blockIdx.x * kBM);
+}
+
+// ---- log-sum-exp-only pass (no obar), 128 stationary rows per workgroup ----
+// Without the accumulator a wave has the registers for 32 rows over the whole
+// hidden size (xs: 256 registers, in the accumulation registers), so the
+// score product needs no cross-wave exchange and each tile fetched from L2
+// serves twice the rows of the obar pass.  Wave w holds rows
+// xb + 32 (w & 1) + [0, 32) of block xb = (w < 2 ? x_a : x_b) (x_b < 0: none).
+template <class Tag, int H>
+__device__ __forceinline__ void lm_lse_body(const LmArgs& a, uint8_t* lds, const int32_t x_a,
+                                            const int32_t x_b) {
+  constexpr int KF = H / 32;  // k-steps over the whole hidden size
+  using L = LdsLayout<H>;
+  static_assert(H % 128 == 0 && H <= 1024, "hidden size must be a multiple of 128, at most 1024");
+
+  const int tid = threadIdx.x, lane = tid & 63, lg = lane >> 4, lc = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int32_t xb = w < 2 ? x_a : x_b;
+  int32_t row[2];
+  bool ok[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    row[rb] = xb + 32 * (w & 1) + 16 * rb + lc;
+    ok[rb] = xb >= 0 && row[rb] < a.nx;
+  }
+  u32x4 xs[2][KF];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const uint16_t* p =
+        static_cast<const uint16_t*>(a.x) + (int64_t)(ok[rb] ? row[rb] : 0) * a.x_ld + 8 * lg;
+#pragma unroll
+    for (int ks = 0; ks < KF; ++ks)
+      xs[rb][ks] = ok[rb] ? *reinterpret_cast<const u32x4*>(p + 32 * ks) : u32x4{0, 0, 0, 0};
+  }
+  int32_t tg[2];
+  float m[2], l[2], xa[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    tg[rb] = -1;
+    if (ok[rb]) {
+      tg[rb] = a.tgt[row[rb]];
+      if (tg[rb] >= a.V) {
+        raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+        tg[rb] = -1;
+      }
+    }
+    m[rb] = -__builtin_huge_valf();
+    l[rb] = 0.f;
+    xa[rb] = -__builtin_huge_valf();
+  }
+
+  const int32_t ntiles = (a.ny + kBN - 1) / kBN;
+  constexpr int UNIT = (2 * H) % 1024 == 0 ? 16 : 4;
+  constexpr int PER_ROW = 2 * H / (64 * UNIT);
+  constexpr int WLOADS = kBN * PER_ROW / 4;
+  constexpr int CHUNK = (WLOADS + KF - 1) / KF;
+  typedef __attribute__((address_space(3))) void lds_void_t;
+  auto tile_src = [&](int32_t r0) {
+    const int32_t rows = a.ny - r0 < kBN ? a.ny - r0 : kBN;
+    const uint16_t* base = static_cast<const uint16_t*>(a.y) + (int64_t)r0 * a.y_ld;
+    return row_rsrc(base, (uint32_t)(((rows - 1) * a.y_ld + H) * 2));
+  };
+  auto issue_loads = [&](const __amdgpu_buffer_rsrc_t& rs, uint8_t* tb, int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i) {
+      const int q = w * WLOADS + i;
+      const int j = q / PER_ROW, part = q % PER_ROW;
+      const uint32_t goff = (uint32_t)(j * a.y_ld * 2 + part * 64 * UNIT + lane * UNIT);
+      lds_void_t* dst = (lds_void_t*)(tb + j * L::kRowBytes + part * 64 * UNIT);
+      if constexpr (UNIT == 16)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 16, goff, 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst, 4, goff, 0, 0, 0);
+    }
+  };
+  if (ntiles > 0) issue_loads(tile_src(0), lds, 0, WLOADS);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the prologue loads landed
+  lds_barrier();
+
+  auto tile_step = [&](const uint8_t* __restrict__ tb, uint8_t* __restrict__ tn,
+                       const int32_t t) __attribute__((always_inline)) {
+    const bool more = t + 1 < ntiles;
+    const int32_t r0 = t * kBN;
+    __amdgpu_buffer_rsrc_t rs_next;
+    if (more) rs_next = tile_src(r0 + kBN);
+    f32x4_t sa[2][2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) sa[rb][0] = sa[rb][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const uint8_t* abase = tb + lc * L::kRowBytes + 16 * lg;
+    auto af_at = [&](int ks, int vb) { return lds_load16(abase, 64 * ks + vb * 16 * L::kRowBytes); };
+    u32x4 af[3][2];
+    af[0][0] = af_at(0, 0);
+    af[0][1] = af_at(0, 1);
+    if (KF > 1) {
+      af[1][0] = af_at(1, 0);
+      af[1][1] = af_at(1, 1);
+    }
+#pragma unroll
+    for (int ks = 0; ks < KF; ++ks) {
+      if (more && ks * CHUNK < WLOADS)
+        issue_loads(rs_next, tn, ks * CHUNK,
+                    ks * CHUNK + CHUNK < WLOADS ? ks * CHUNK + CHUNK : WLOADS);
+      if (ks + 2 < KF) {
+        af[(ks + 2) % 3][0] = af_at(ks + 2, 0);
+        af[(ks + 2) % 3][1] = af_at(ks + 2, 1);
+      }
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+          sa[rb][vb] = mfma<Tag>(af[ks % 3][vb], xs[rb][ks], sa[rb][vb]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Per row block: the target column held out, columns past the vocabulary
+    // dropped (both on a wave-uniform slow path), then each lane's exact
+    // running maximum and sum of its own columns (merged at the end).
+    const bool slow = r0 + kBN > a.V ||
+                      __builtin_amdgcn_ballot_w64((tg[0] >= r0 && tg[0] < r0 + kBN) ||
+                                                  (tg[1] >= r0 && tg[1] < r0 + kBN)) != 0;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      float sv[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sv[r] = sa[rb][0][r];
+        sv[4 + r] = sa[rb][1][r];
+      }
+      if (slow) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int32_t v = r0 + 4 * lg + (i & 3) + 16 * (i >> 2);
+          if (v >= a.V) sv[i] = -__builtin_huge_valf();
+          if (v == tg[rb]) {
+            xa[rb] = sv[i];
+            sv[i] = -__builtin_huge_valf();
+          }
+        }
+      }
+      float tmax = sv[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, sv[i]);
+      if (tmax > m[rb]) {
+        l[rb] *= m[rb] == -__builtin_huge_valf() ? 0.f : exp2_hw((m[rb] - tmax) * kLog2e);
+        m[rb] = tmax;
+      }
+      const float mb = m[rb] == -__builtin_huge_valf() ? 0.f : m[rb] * kLog2e;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) l[rb] += exp2_hw(sv[i] * kLog2e - mb);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of tile t+1 landed
+    lds_barrier();                       // tile t+1 complete; tile t's reads done
+  };
+  for (int32_t t = 0; t < ntiles; ++t) {
+    const int buf = (int)(t & 1);
+    tile_step(lds + buf * L::kTileBytes, lds + (buf ^ 1) * L::kTileBytes, t);
+  }
+
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    float M = fmaxf(m[rb], xor16(m[rb]));
+    M = fmaxf(M, xor32(M));
+    float lr = m[rb] == M ? l[rb] : l[rb] * exp2_hw((m[rb] - M) * kLog2e);
+    lr += xor16(lr);
+    lr += xor32(lr);
+    float xt = fmaxf(xa[rb], xor16(xa[rb]));
+    xt = fmaxf(xt, xor32(xt));
+    float lse, logp;
+    finish_row(M, lr, xt, tg[rb], lse, logp);
+    if (lg == 0 && ok[rb]) {
+      a.lse_out[row[rb]] = lse;
+      a.logp_out[row[rb]] = logp;
+    }
+  }
+}
+
+template <class Tag, int H>
+__global__ __launch_bounds__(kNT, 1) void lm_lse_kernel(LmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * LdsLayout<H>::kTileBytes];
+  int32_t x_a, x_b;
+  if (a.block_order != nullptr) {
+    // blocks block_order[count + 2i], [count + 2i + 1]: those that need no obar
+    const int32_t nblocks = (a.nx + kBM - 1) / kBM;
+    const int32_t e = *a.block_count + 2 * (int32_t)blockIdx.x;
+    if (e >= nblocks) return;
+    x_a = __builtin_amdgcn_readfirstlane(a.block_order[e]) * kBM;
+    x_b = e + 1 < nblocks ? __builtin_amdgcn_readfirstlane(a.block_order[e + 1]) * kBM : -1;
+  } else {
+    x_a = (int32_t)blockIdx.x * 2 * kBM;
+    x_b = x_a + kBM < a.nx ? x_a + kBM : -1;
+  }
+  lm_lse_body<Tag, H>(a, lds, x_a, x_b);
 }
 
 // Tiles of 32 streamed tokens that hold a token with g != 0 (the others
@@ -697,6 +890,7 @@ __global__ __launch_bounds__(1024) void lm_block_order_kernel(int32_t n, const u
       base = total;
       __syncthreads();
     }
+    if (pass == 0 && tid == 0) order[nblocks] = base;  // blocks that need obar
   }
 }
 
@@ -794,6 +988,29 @@ int launch_tiles_dt(int32_t /*dt*/, const LmArgs& a, int64_t H, hipStream_t st) 
   return launch_tiles<TagBF16, MODE>(a, H, st);
 }
 
+int launch_lse(const LmArgs& a, int64_t H, hipStream_t st) {
+  const unsigned grid = (unsigned)((a.nx + 2 * kBM - 1) / (2 * kBM));
+  if (grid == 0) return RRL_OK;
+#define RRL_LSE_CASE(HV)                                                                      \
+  case HV:                                                                                    \
+    hipLaunchKernelGGL((lm_lse_kernel<TagBF16, HV>), dim3(grid), dim3(kNT), 0, st, a);        \
+    return check_launch("lm_lse_kernel");
+  switch (H) {
+    RRL_LSE_CASE(128)
+    RRL_LSE_CASE(256)
+    RRL_LSE_CASE(384)
+    RRL_LSE_CASE(512)
+    RRL_LSE_CASE(640)
+    RRL_LSE_CASE(768)
+    RRL_LSE_CASE(896)
+    RRL_LSE_CASE(1024)
+    default: break;
+  }
+#undef RRL_LSE_CASE
+  set_error("lm head: hidden size must be a multiple of 128 and at most 1024");
+  return RRL_EINVAL;
+}
+
 int check_operands(int32_t dt, int64_t N, int64_t H, int64_t V, const void* hidden,
                    int64_t h_ld, const void* weight, int64_t w_ld) {
   RRL_REQUIRE(dt == RRL_BF16, RRL_EDTYPE, "lm head: hidden and weight must be bfloat16");
@@ -841,24 +1058,28 @@ extern "C" int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t d
   hipStream_t st = as_stream(stream);
   if (!obar) {
     a.need_obar = nullptr;
-    return launch_tiles_dt<kModeFwdLseOnly>(dtype, a, H, st);
+    return launch_lse(a, H, st);
   }
-  if (need_obar) {
-    RRL_REQUIRE(workspace != nullptr && ((uintptr_t)workspace & 15) == 0, RRL_EINVAL,
-                "lm head: need_obar requires a 16-byte aligned workspace of "
-                "rrl_lm_head_fwd_workspace_bytes(N) bytes");
-    int32_t* order = static_cast<int32_t*>(workspace);
-    hipLaunchKernelGGL(lm_block_order_kernel, dim3(1), dim3(1024), 0, st, (int32_t)N, need_obar,
-                       order);
-    if (int rc = check_launch("lm_block_order_kernel")) return rc;
-    a.block_order = order;
-  }
-  return launch_tiles_dt<kModeFwd>(dtype, a, H, st);
+  if (!need_obar) return launch_tiles_dt<kModeFwd>(dtype, a, H, st);
+  RRL_REQUIRE(workspace != nullptr && ((uintptr_t)workspace & 15) == 0, RRL_EINVAL,
+              "lm head: need_obar requires a 16-byte aligned workspace of "
+              "rrl_lm_head_fwd_workspace_bytes(N) bytes");
+  // Blocks that need obar (listed first) take the obar pass, the others the
+  // log-sum-exp pass; each launch covers every block that could be its and
+  // its surplus workgroups return at once.
+  int32_t* order = static_cast<int32_t*>(workspace);
+  hipLaunchKernelGGL(lm_block_order_kernel, dim3(1), dim3(1024), 0, st, (int32_t)N, need_obar,
+                     order);
+  if (int rc = check_launch("lm_block_order_kernel")) return rc;
+  a.block_order = order;
+  a.block_count = order + (N + kBM - 1) / kBM;
+  if (int rc = launch_tiles_dt<kModeFwd>(dtype, a, H, st)) return rc;
+  return launch_lse(a, H, st);
 }
 
 extern "C" size_t rrl_lm_head_fwd_workspace_bytes(int64_t N) {
   if (N <= 0) return 0;
-  return (size_t)(((N + kBM - 1) / kBM) * 4 + 255) / 256 * 256;
+  return (size_t)(((N + kBM - 1) / kBM + 1) * 4 + 255) / 256 * 256;
 }
 
 // Workspace of rrl_lm_head_dweight: 16-byte token records, then the tile

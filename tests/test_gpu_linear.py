@@ -235,6 +235,53 @@ def test_logits_beyond_the_reference_range_rerun(device):
     _product_check(wd.grad, dl, h.reshape(-1, H), "dweight", transpose=True)
 
 
+@pytest.mark.parametrize("H,V,B,T,hot", [(1024, 8256, 3, 67, 0.0), (128, 33, 2, 32, 0.0),
+                                         (384, 1000, 2, 129, 0.0), (768, 2050, 2, 1, 0.0),
+                                         (256, 4096, 4, 64, 0.8)])
+def test_logprobs_without_grad_lse_pass(device, H, V, B, T, hot):
+    """Without a gradient the log-probs come from the log-sum-exp-only kernel
+    (128 tokens per workgroup: token counts that fill one, two or three
+    64-token halves of it, vocabularies off the 32-column tile, targets that
+    dominate their row)."""
+
+    print(f"[lse-pass] H={H} V={V} N={B * T} hot={hot}", flush=True)
+    h, w, x, t, _old, _adv, _mask = _inputs(47, B, T, H, V, w_scale=2.0 if hot else None,
+                                           hot=hot)
+    with torch.no_grad():
+        lp = R.linear_token_logprobs(h.to(device), w.to(device), t.to(device))
+    assert lp.dtype == torch.float32 and lp.shape == (B, T)
+    _logp_check(lp, o.token_logprobs(x, t, exact=True), scale=x.abs().max())
+
+
+def test_fused_linear_masked_blocks_interleaved(device):
+    """Masks whose fully masked 64-token blocks alternate with needed ones:
+    the needed blocks take the obar pass, the others the log-sum-exp pass
+    (two per workgroup, not adjacent in memory), and every log-prob, the loss
+    and both gradients match the oracle."""
+
+    B, T, H, V = 8, 192, 256, 4099
+    h, w, x, t, old, adv, _mask = _inputs(48, B, T, H, V)
+    lengths = torch.tensor([64, 192, 0, 130, 1, 65, 128, 0])
+    mask = torch.arange(T)[None, :] < lengths[:, None]
+    blocks = mask.reshape(-1, 64).any(dim=1)
+    assert bool(blocks.any()) and not bool(blocks.all())
+    kw = KW["clipped"]
+    hd = h.to(device).requires_grad_()
+    wd = w.to(device).requires_grad_()
+    d = lambda z: z.to(device)  # noqa: E731
+    out, lp = R.fused_linear_policy_loss(hd, wd, d(t), d(old), d(adv), d(mask),
+                                         objective="clipped", return_logprobs=True, **kw)
+    out.loss.backward()
+    out_o, lpo, _dho, _dwo = o.lm_head_step("ppo", h, w, x, t, old, adv, mask, exact=True, **kw)
+    _logp_check(lp, lpo)
+    scale = max(abs(out_o["loss"].item()), adv.abs().mean().item())
+    assert abs(out.loss.item() - out_o["loss"].item()) <= 2e-3 * scale
+    dl = out_o["dlogits"].double().reshape(-1, V)
+    _product_check(hd.grad.reshape(-1, H), dl, w, "dhidden", transpose=False)
+    _product_check(wd.grad, dl, h.reshape(-1, H), "dweight", transpose=True)
+    assert bool((hd.grad.reshape(-1, H)[~mask.reshape(-1).to(device)] == 0).all())
+
+
 def test_strided_hidden_and_target_errors(device):
     """A hidden view with a padded row stride is read in place (no copy);
     out-of-range targets raise as torch.gather does; float32 is refused."""
