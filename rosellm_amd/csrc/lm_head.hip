@@ -262,10 +262,9 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, cons
   }
 
   const int32_t ntiles = a.tile_count ? *a.tile_count : (a.ny + kBN - 1) / kBN;
-  // First streamed row of tile t, wave-uniform (a scalar register).
-  auto tile_row0 = [&](int32_t t) {
-    return __builtin_amdgcn_readfirstlane((a.tile_list ? a.tile_list[t] : t) * kBN);
-  };
+  // Index of tile t (tile_list read one tile ahead of its use: the wait for
+  // the read is then the end-of-tile wait that precedes it).
+  auto tile_index = [&](int32_t t) { return a.tile_list ? a.tile_list[t] : t; };
 
   // ---- tile loads, global -> LDS directly (buffer loads with the LDS bit:
   // no registers).  One wave-wide load writes 64 consecutive lanes x UNIT
@@ -321,7 +320,8 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, cons
     }
   };
 
-  int32_t r0_next = ntiles > 0 ? tile_row0(0) : 0;
+  int32_t r0_next = ntiles > 0 ? __builtin_amdgcn_readfirstlane(tile_index(0) * kBN) : 0;
+  int32_t idx_ahead = ntiles > 1 ? tile_index(1) : 0;
   if (ntiles > 0) issue_loads(tile_src(r0_next), lds, 0, WLOADS);
   // Every prologue load (the stationary fragments and tile 0) has landed.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt untouched
@@ -341,14 +341,12 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, cons
     // Tile t+1 goes to the other buffer, free since barrier C of tile t-1;
     // it has this whole tile's work to land.
     const bool more = t + 1 < ntiles;
-    // The first row of tile t was read when its loads were issued; reading
-    // tile_list here, before tile t+1's loads are in flight, keeps the wait
-    // for that read from also waiting for them.
     const int32_t r0 = r0_next;
     __amdgpu_buffer_rsrc_t rs_next;
     if (more) {
-      r0_next = tile_row0(t + 1);
+      r0_next = __builtin_amdgcn_readfirstlane(idx_ahead * kBN);
       rs_next = tile_src(r0_next);
+      if (t + 2 < ntiles) idx_ahead = tile_index(t + 2);
     }
 
     // ---- S phase: partial S^T[32 x 64] of the tile against all 64 rows over
@@ -592,21 +590,38 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, cons
   }
 }
 
+template <class Tag, int H>
+__device__ __forceinline__ void lm_lse_body(const LmArgs& a, uint8_t* lds, const int32_t x_a,
+                                            const int32_t x_b);
+
 template <class Tag, int MODE, int H>
 __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[LdsLayout<H>::kTotal];
   if constexpr (MODE == kModeFwd) {
-    // With need_obar, workgroup i takes block block_order[i] of the blocks
-    // that need obar (listed first); the blocks that do not are left to the
-    // log-sum-exp kernel.  Listing them first, rather than taking blocks in
-    // token order, spreads them evenly over the eight XCDs (consecutive
-    // workgroups go to the XCDs in turn): masks that end each sequence in a
-    // run of masked blocks otherwise load some XCDs with most of the obar
-    // work (measured: as slow as obar for every block).
+    // With need_obar the launch covers both kinds of 64-token block, in
+    // block_order: workgroup i < count takes block block_order[i], which
+    // needs obar; the following workgroups take the remaining blocks two at
+    // a time through the log-sum-exp pass; surplus workgroups return at once.
+    // Listing the obar blocks first, rather than taking blocks in token
+    // order, spreads them evenly over the eight XCDs (consecutive workgroups
+    // go to the XCDs in turn): masks that end each sequence in a run of
+    // masked blocks otherwise load some XCDs with most of the obar work
+    // (measured: as slow as obar for every block).  One launch rather than
+    // two lets the log-sum-exp workgroups fill the obar pass's last round.
     if (a.block_order != nullptr) {
-      if ((int32_t)blockIdx.x >= *a.block_count) return;
-      const int32_t blk = __builtin_amdgcn_readfirstlane(a.block_order[blockIdx.x]);
-      lm_tile_body<Tag, MODE, H>(a, lds, blk * kBM);
+      const int32_t count = *a.block_count, i = (int32_t)blockIdx.x;
+      if (i < count) {
+        const int32_t blk = __builtin_amdgcn_readfirstlane(a.block_order[i]);
+        lm_tile_body<Tag, MODE, H>(a, lds, blk * kBM);
+        return;
+      }
+      const int32_t nblocks = (a.nx + kBM - 1) / kBM;
+      const int32_t e = count + 2 * (i - count);
+      if (e >= nblocks) return;
+      const int32_t x_a = __builtin_amdgcn_readfirstlane(a.block_order[e]) * kBM;
+      const int32_t x_b =
+          e + 1 < nblocks ? __builtin_amdgcn_readfirstlane(a.block_order[e + 1]) * kBM : -1;
+      lm_lse_body<Tag, H>(a, lds, x_a, x_b);
       return;
     }
   }
@@ -789,19 +804,8 @@ __device__ __forceinline__ void lm_lse_body(const LmArgs& a, uint8_t* lds, const
 template <class Tag, int H>
 __global__ __launch_bounds__(kNT, 1) void lm_lse_kernel(LmArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * LdsLayout<H>::kTileBytes];
-  int32_t x_a, x_b;
-  if (a.block_order != nullptr) {
-    // blocks block_order[count + 2i], [count + 2i + 1]: those that need no obar
-    const int32_t nblocks = (a.nx + kBM - 1) / kBM;
-    const int32_t e = *a.block_count + 2 * (int32_t)blockIdx.x;
-    if (e >= nblocks) return;
-    x_a = __builtin_amdgcn_readfirstlane(a.block_order[e]) * kBM;
-    x_b = e + 1 < nblocks ? __builtin_amdgcn_readfirstlane(a.block_order[e + 1]) * kBM : -1;
-  } else {
-    x_a = (int32_t)blockIdx.x * 2 * kBM;
-    x_b = x_a + kBM < a.nx ? x_a + kBM : -1;
-  }
-  lm_lse_body<Tag, H>(a, lds, x_a, x_b);
+  const int32_t x_a = (int32_t)blockIdx.x * 2 * kBM;
+  lm_lse_body<Tag, H>(a, lds, x_a, x_a + kBM < a.nx ? x_a + kBM : -1);
 }
 
 // Tiles of 32 streamed tokens that hold a token with g != 0 (the others
@@ -958,7 +962,9 @@ int cu_count(int* out) {
 
 template <class Tag, int MODE>
 int launch_tiles(const LmArgs& a, int64_t H, hipStream_t st) {
-  const unsigned grid = (unsigned)((a.nx + kBM - 1) / kBM);
+  const int64_t nblocks = (a.nx + kBM - 1) / kBM;
+  const unsigned grid =
+      (unsigned)(a.block_order != nullptr ? nblocks + (nblocks + 1) / 2 : nblocks);
   if (grid == 0) return RRL_OK;
 #define RRL_LM_CASE(HV)                                                                        \
   case HV:                                                                                     \
@@ -1065,16 +1071,14 @@ extern "C" int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t d
               "lm head: need_obar requires a 16-byte aligned workspace of "
               "rrl_lm_head_fwd_workspace_bytes(N) bytes");
   // Blocks that need obar (listed first) take the obar pass, the others the
-  // log-sum-exp pass; each launch covers every block that could be its and
-  // its surplus workgroups return at once.
+  // log-sum-exp pass, in one launch.
   int32_t* order = static_cast<int32_t*>(workspace);
   hipLaunchKernelGGL(lm_block_order_kernel, dim3(1), dim3(1024), 0, st, (int32_t)N, need_obar,
                      order);
   if (int rc = check_launch("lm_block_order_kernel")) return rc;
   a.block_order = order;
   a.block_count = order + (N + kBM - 1) / kBM;
-  if (int rc = launch_tiles_dt<kModeFwd>(dtype, a, H, st)) return rc;
-  return launch_lse(a, H, st);
+  return launch_tiles_dt<kModeFwd>(dtype, a, H, st);
 }
 
 extern "C" size_t rrl_lm_head_fwd_workspace_bytes(int64_t N) {
