@@ -366,13 +366,16 @@ RRL_API int rrl_lm_head_dhidden(const void* weight, int32_t dtype, int64_t N, in
  * the logits recomputed tile by tile, float32 accumulation over every token in
  * registers, written once as float32 or the weight dtype (dw_dtype), rows dw_ld
  * apart.  Tiles of 32 consecutive tokens whose g are all zero contribute
- * exactly zero and are not visited.  records: rrl_lm_head_records_bytes(N)
- * bytes of caller workspace (16-byte aligned). */
-RRL_API size_t rrl_lm_head_records_bytes(int64_t N);
+ * exactly zero and are not visited.  workspace:
+ * rrl_lm_head_dweight_workspace_bytes(N, H, V) bytes of caller device memory
+ * (16-byte aligned; token records, the visited tiles, and float32 partial rows
+ * of the weight blocks that a last partial round of workgroups splits over
+ * token ranges; the size depends on the current device's CU count). */
+RRL_API size_t rrl_lm_head_dweight_workspace_bytes(int64_t N, int64_t H, int64_t V);
 RRL_API int rrl_lm_head_dweight(const void* hidden, const void* weight, int32_t dtype,
                     int64_t N, int64_t H, int64_t V, int64_t h_ld, int64_t w_ld,
                     const int32_t* targets, const float* lse, const float* logp,
-                    const float* g, void* records, void* dweight, int32_t dw_dtype,
+                    const float* g, void* workspace, void* dweight, int32_t dw_dtype,
                     int64_t dw_ld, void* stream);
 
 /* ---- rollout side: next-token sampling with behaviour log-probs -------------

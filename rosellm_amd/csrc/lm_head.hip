@@ -194,6 +194,9 @@ struct LmArgs {
   void* dw;              // dW pass: [nx, H] (ld dw_ld), float32 or 16-bit
   int64_t dw_ld;
   int32_t dw_f32;
+  int32_t dw_full;       // dW pass: workgroups that take a whole 64-row block
+  int32_t dw_split;      // dW pass: parts each later block is split into (tile ranges)
+  float* dw_part;        // dW pass: float32 [parts][64][H] partial rows of the split blocks
   int32_t* status;
 };
 
@@ -210,7 +213,9 @@ struct LdsLayout {
 };
 
 template <class Tag, int MODE, int H>
-__device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, const int32_t x0) {
+__device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, const int32_t x0,
+                                             const int32_t t_lo, const int32_t t_hi,
+                                             float* const part_out) {
   constexpr int DW = H / 4;                 // hidden slice of each wave (S depth and accumulator)
   constexpr int KQ = DW / 32;               // k-steps of the S product over one slice
   constexpr int DB = DW / 16;               // 16-column blocks of the accumulator per wave
@@ -261,7 +266,7 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, cons
     if (a.mref_in != nullptr && my_row < a.nx) m_ref = a.mref_in[my_row];
   }
 
-  const int32_t ntiles = a.tile_count ? *a.tile_count : (a.ny + kBN - 1) / kBN;
+  // Streamed tiles t_lo .. t_hi - 1 (of tile_list when given).
   // Index of tile t (tile_list read one tile ahead of its use: the wait for
   // the read is then the end-of-tile wait that precedes it).
   auto tile_index = [&](int32_t t) { return a.tile_list ? a.tile_list[t] : t; };
@@ -320,9 +325,9 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, cons
     }
   };
 
-  int32_t r0_next = ntiles > 0 ? __builtin_amdgcn_readfirstlane(tile_index(0) * kBN) : 0;
-  int32_t idx_ahead = ntiles > 1 ? tile_index(1) : 0;
-  if (ntiles > 0) issue_loads(tile_src(r0_next), lds, 0, WLOADS);
+  int32_t r0_next = t_lo < t_hi ? __builtin_amdgcn_readfirstlane(tile_index(t_lo) * kBN) : 0;
+  int32_t idx_ahead = t_lo + 1 < t_hi ? tile_index(t_lo + 1) : 0;
+  if (t_lo < t_hi) issue_loads(tile_src(r0_next), lds, 0, WLOADS);
   // Every prologue load (the stationary fragments and tile 0) has landed.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt, lgkmcnt untouched
   publish_records(0);
@@ -340,13 +345,13 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, cons
                        const int32_t t) __attribute__((always_inline)) {
     // Tile t+1 goes to the other buffer, free since barrier C of tile t-1;
     // it has this whole tile's work to land.
-    const bool more = t + 1 < ntiles;
+    const bool more = t + 1 < t_hi;
     const int32_t r0 = r0_next;
     __amdgpu_buffer_rsrc_t rs_next;
     if (more) {
       r0_next = __builtin_amdgcn_readfirstlane(idx_ahead * kBN);
       rs_next = tile_src(r0_next);
-      if (t + 2 < ntiles) idx_ahead = tile_index(t + 2);
+      if (t + 2 < t_hi) idx_ahead = tile_index(t + 2);
     }
 
     // ---- S phase: partial S^T[32 x 64] of the tile against all 64 rows over
@@ -526,8 +531,8 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, cons
     if (more) publish_records(buf ^ 1);  // tile t's records were read before barrier B
     lds_barrier();  // C: tile t+1 complete; tile t's reads done
   };
-  for (int32_t t = 0; t < ntiles; ++t) {
-    const int buf = (int)(t & 1);
+  for (int32_t t = t_lo; t < t_hi; ++t) {
+    const int buf = (int)((t - t_lo) & 1);
     tile_step(lds + buf * L::kTileBytes, lds + (buf ^ 1) * L::kTileBytes, buf, t);
   }
 
@@ -575,7 +580,11 @@ __device__ __forceinline__ void lm_tile_body(const LmArgs& a, uint8_t* lds, cons
       for (int r = 0; r < 4; ++r) {
         const int32_t row = x0 + 16 * nb + 4 * lg + r;
         if (row >= a.nx) continue;
-        if (a.dw_f32) {
+        if (part_out != nullptr) {  // a part of a split block: float32 partial rows
+          float* o = part_out + (int64_t)(16 * nb + 4 * lg + r) * H + dw0 + lc;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) o[16 * db] = acc[nb][db][r];
+        } else if (a.dw_f32) {
           float* o = static_cast<float*>(a.dw) + (int64_t)row * a.dw_ld + dw0 + lc;
 #pragma unroll
           for (int db = 0; db < DB; ++db) o[16 * db] = acc[nb][db][r];
@@ -612,7 +621,7 @@ __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
       const int32_t count = *a.block_count, i = (int32_t)blockIdx.x;
       if (i < count) {
         const int32_t blk = __builtin_amdgcn_readfirstlane(a.block_order[i]);
-        lm_tile_body<Tag, MODE, H>(a, lds, blk * kBM);
+        lm_tile_body<Tag, MODE, H>(a, lds, blk * kBM, 0, (a.ny + kBN - 1) / kBN, nullptr);
         return;
       }
       const int32_t nblocks = (a.nx + kBM - 1) / kBM;
@@ -625,7 +634,26 @@ __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
       return;
     }
   }
-  lm_tile_body<Tag, MODE, H>(a, lds, (int32_t)blockIdx.x * kBM);
+  if constexpr (MODE == kModeDw) {
+    // Blocks past dw_full are split into dw_split ranges of the tile list
+    // (the last, partial round of workgroups then has dw_split times as many,
+    // each with 1 / dw_split of the work); their float32 partial rows are
+    // summed by lm_dw_reduce_kernel.
+    const int32_t nt = a.tile_count ? *a.tile_count : (a.ny + kBN - 1) / kBN;
+    const int32_t i = (int32_t)blockIdx.x;
+    if (i < a.dw_full) {
+      lm_tile_body<Tag, MODE, H>(a, lds, i * kBM, 0, nt, nullptr);
+    } else {
+      const int32_t j = i - a.dw_full, part = j % a.dw_split;
+      const int32_t lo = (int32_t)((int64_t)part * nt / a.dw_split);
+      const int32_t hi = (int32_t)((int64_t)(part + 1) * nt / a.dw_split);
+      lm_tile_body<Tag, MODE, H>(a, lds, (a.dw_full + j / a.dw_split) * kBM, lo, hi,
+                                 a.dw_part + (int64_t)j * kBM * H);
+    }
+    return;
+  }
+  lm_tile_body<Tag, MODE, H>(a, lds, (int32_t)blockIdx.x * kBM, 0, (a.ny + kBN - 1) / kBN,
+                             nullptr);
 }
 
 // ---- log-sum-exp-only pass (no obar), 128 stationary rows per workgroup ----
@@ -915,6 +943,30 @@ __global__ __launch_bounds__(256) void lm_token_records_kernel(int64_t n, int32_
   }
 }
 
+// Rows of the split dW blocks (blocks full, full + 1, ...): dw[row] = the sum
+// over the parts, in part order, of their float32 partial rows.
+template <class Tag>
+__global__ __launch_bounds__(256) void lm_dw_reduce_kernel(int32_t nrows, int32_t parts,
+                                                           int32_t full, int32_t H, int32_t nx,
+                                                           const float* part, void* dw,
+                                                           int64_t dw_ld, int32_t dw_f32) {
+  for (int32_t rr = blockIdx.x; rr < nrows; rr += gridDim.x) {
+    const int32_t blk = rr / kBM, r = rr % kBM;
+    const int32_t row = full * kBM + rr;
+    if (row >= nx) continue;
+    for (int32_t c = threadIdx.x; c < H; c += 256) {
+      float v = 0.f;
+      for (int32_t q = 0; q < parts; ++q)
+        v += part[((int64_t)(blk * parts + q) * kBM + r) * H + c];
+      if (dw_f32)
+        static_cast<float*>(dw)[(int64_t)row * dw_ld + c] = v;
+      else
+        static_cast<uint16_t*>(dw)[(int64_t)row * dw_ld + c] =
+            (uint16_t)(pack2<Tag>(v, 0.f) & 0xFFFFu);
+    }
+  }
+}
+
 // dhidden[n] = g_n ((-expm1(logp_n)) W[a_n] - obar_n), 16-bit out.
 template <class Tag>
 __global__ __launch_bounds__(256) void lm_dhidden_kernel(int64_t n, int32_t H, int32_t V,
@@ -963,8 +1015,9 @@ int cu_count(int* out) {
 template <class Tag, int MODE>
 int launch_tiles(const LmArgs& a, int64_t H, hipStream_t st) {
   const int64_t nblocks = (a.nx + kBM - 1) / kBM;
-  const unsigned grid =
-      (unsigned)(a.block_order != nullptr ? nblocks + (nblocks + 1) / 2 : nblocks);
+  unsigned grid = (unsigned)(a.block_order != nullptr ? nblocks + (nblocks + 1) / 2 : nblocks);
+  if (MODE == kModeDw && a.dw_split > 1)
+    grid = (unsigned)(a.dw_full + (nblocks - a.dw_full) * a.dw_split);
   if (grid == 0) return RRL_OK;
 #define RRL_LM_CASE(HV)                                                                        \
   case HV:                                                                                     \
@@ -1087,17 +1140,39 @@ extern "C" size_t rrl_lm_head_fwd_workspace_bytes(int64_t N) {
 }
 
 // Workspace of rrl_lm_head_dweight: 16-byte token records, then the tile
-// flags, then the active tile list and its count.
+// flags, then the active tile list and its count, then the float32 partial
+// rows of the blocks split over tile ranges.
 namespace {
 size_t records_part(int64_t N) { return ((size_t)(N > 0 ? N : 0) * 16 + 255) & ~(size_t)255; }
 size_t flags_part(int64_t N) {
   return ((size_t)((N > 0 ? N : 0) + kBN - 1) / kBN + 255) & ~(size_t)255;
 }
+size_t list_part(int64_t N) {
+  const size_t ntiles = (size_t)((N > 0 ? N : 0) + kBN - 1) / kBN;
+  return ((ntiles + 64) * 4 + 255) & ~(size_t)255;
+}
+// The dW grid: whole blocks, then the blocks of a last partial round of
+// workgroups (at most half a round) split into `split` tile ranges each.
+struct DwGrid {
+  int32_t full, split, rest;
+};
+DwGrid dw_grid(int64_t V) {
+  int cus = 256;
+  cu_count(&cus);
+  const int64_t nvb = (V + kBM - 1) / kBM;
+  const int64_t rest = nvb % cus;
+  if (rest == 0 || 2 * rest > cus || nvb < cus) return DwGrid{(int32_t)nvb, 1, 0};
+  int64_t split = cus / rest;
+  if (split > 8) split = 8;
+  return DwGrid{(int32_t)(nvb - rest), (int32_t)split, (int32_t)rest};
+}
 }  // namespace
 
-extern "C" size_t rrl_lm_head_records_bytes(int64_t N) {
-  const size_t ntiles = (size_t)((N > 0 ? N : 0) + kBN - 1) / kBN;
-  return records_part(N) + flags_part(N) + (ntiles + 64) * 4 + 256;
+extern "C" size_t rrl_lm_head_dweight_workspace_bytes(int64_t N, int64_t H, int64_t V) {
+  const DwGrid gd = dw_grid(V > 0 ? V : 0);
+  const size_t parts =
+      gd.split > 1 ? (size_t)gd.rest * gd.split * kBM * (size_t)(H > 0 ? H : 0) * 4 : 0;
+  return records_part(N) + flags_part(N) + list_part(N) + parts;
 }
 
 extern "C" int rrl_lm_head_dhidden(const void* weight, int32_t dtype, int64_t N, int64_t H,
@@ -1124,20 +1199,22 @@ extern "C" int rrl_lm_head_dhidden(const void* weight, int32_t dtype, int64_t N,
 extern "C" int rrl_lm_head_dweight(const void* hidden, const void* weight, int32_t dtype,
                                    int64_t N, int64_t H, int64_t V, int64_t h_ld, int64_t w_ld,
                                    const int32_t* targets, const float* lse, const float* logp,
-                                   const float* g, void* records, void* dweight,
+                                   const float* g, void* workspace, void* dweight,
                                    int32_t dw_dtype, int64_t dw_ld, void* stream) {
   clear_error();
   if (int rc = check_operands(dtype, N, H, V, hidden, h_ld, weight, w_ld)) return rc;
   RRL_REQUIRE(dw_dtype == RRL_F32 || dw_dtype == dtype, RRL_EDTYPE,
               "lm head: dweight must be float32 or the weight dtype");
   RRL_REQUIRE(dweight && dw_ld >= H, RRL_EINVAL, "lm head: dweight pointer or stride");
-  RRL_REQUIRE(N == 0 || (targets && lse && logp && g && records), RRL_EINVAL,
+  RRL_REQUIRE(N == 0 || (targets && lse && logp && g && workspace), RRL_EINVAL,
               "lm head: null pointer argument");
-  RRL_REQUIRE((uintptr_t)records % 16 == 0, RRL_EALIGN, "lm head: records must be 16-byte aligned");
+  RRL_REQUIRE((uintptr_t)workspace % 16 == 0, RRL_EALIGN,
+              "lm head: workspace must be 16-byte aligned");
   hipStream_t st = as_stream(stream);
-  uint8_t* ws = static_cast<uint8_t*>(records);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
   uint8_t* flags = ws + records_part(N);
   int32_t* list = reinterpret_cast<int32_t*>(flags + flags_part(N));
+  float* parts = reinterpret_cast<float*>(flags + flags_part(N) + list_part(N));
   const int64_t ntiles = (N + kBN - 1) / kBN;
   int32_t* count = list + ntiles + 32;
   if (N > 0) {
@@ -1162,7 +1239,19 @@ extern "C" int rrl_lm_head_dweight(const void* hidden, const void* weight, int32
   a.x = weight; a.x_ld = w_ld; a.nx = (int32_t)V;
   a.y = hidden; a.y_ld = h_ld; a.ny = (int32_t)N;
   a.V = (int32_t)V;
-  a.trec = static_cast<const float4*>(records);
+  a.trec = reinterpret_cast<const float4*>(ws);
   a.dw = dweight; a.dw_ld = dw_ld; a.dw_f32 = dw_dtype == RRL_F32;
-  return launch_tiles_dt<kModeDw>(dtype, a, H, st);
+  const DwGrid gd = dw_grid(V);
+  a.dw_full = gd.full;
+  a.dw_split = gd.split;
+  a.dw_part = gd.split > 1 ? parts : nullptr;
+  if (int rc = launch_tiles_dt<kModeDw>(dtype, a, H, st)) return rc;
+  if (gd.split > 1) {
+    const int32_t nrows = gd.rest * kBM;
+    hipLaunchKernelGGL(lm_dw_reduce_kernel<TagBF16>, dim3((unsigned)nrows), dim3(256), 0, st,
+                       nrows, gd.split, gd.full, (int32_t)H, (int32_t)V, parts, dweight, dw_ld,
+                       (int32_t)a.dw_f32);
+    return check_launch("lm_dw_reduce_kernel");
+  }
+  return RRL_OK;
 }

@@ -149,7 +149,8 @@ def lm_head_backward(h2: Tensor, w: Tensor, tgt32: Tensor, lse: Tensor, logp: Te
                  logp.data_ptr(), g.data_ptr(), obar.data_ptr(), H, dh.data_ptr(), H, stream)
     if need_w:
         dw = torch.empty((V, H), dtype=w.dtype, device=dev)
-        rec = torch.empty(nat.lib().rrl_lm_head_records_bytes(N), dtype=torch.uint8, device=dev)
+        rec = torch.empty(nat.lib().rrl_lm_head_dweight_workspace_bytes(N, H, V),
+                          dtype=torch.uint8, device=dev)
         nat.call("rrl_lm_head_dweight", h2.data_ptr(), w.data_ptr(), dt, N, H, V, h2.stride(0),
                  w.stride(0), tgt32.data_ptr(), lse.data_ptr(), logp.data_ptr(), g.data_ptr(),
                  rec.data_ptr(), dw.data_ptr(), dt, H, stream)

@@ -138,12 +138,14 @@ def _logp_check(lp, lpo, scale=None):
 
 
 @pytest.mark.parametrize("H,V", [(256, 4099), (1024, 8256), (384, 1000), (128, 33),
-                                 (768, 2050), (896, 301), (512, 1)])
+                                 (768, 2050), (896, 301), (512, 1), (128, 19201)])
 def test_linear_logprobs_and_grads(device, H, V):
     """log-probs and, for a random upstream gradient, d hidden and d weight,
     across hidden sizes (every instantiated one is a multiple of 128 up to
     1024), vocabularies that are not tile multiples, and token counts that
-    are not 64-row block multiples."""
+    are not 64-row block multiples.  V = 19201 has 301 weight blocks: on a
+    256-CU device the dW pass splits the last 45 over token ranges and sums
+    their partial rows."""
 
     print(f"[linear-logprobs] H={H} V={V}", flush=True)
     B, T = 3, 37
