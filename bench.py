@@ -17,11 +17,20 @@ backward to bf16 dlogits.  ``--path fused`` (default) runs it through
 ``clipped_policy_loss`` and autograd (two reads, one write).  Inputs are
 resident in HBM before the timed region.
 
+After the headline the same run times every other configuration and reports
+it under ``variants`` (each in its own try/except; an error string replaces a
+failed one): C1, C3 with GSPO and with GSPO-token, C4 (GAE + whitening + SAPO,
+dlogits in place: its logits are regenerated from their seed before every
+step, outside the step's events, so every step runs on the config's data),
+SFT, the rollout sampler and C5.
+
 ``--config c5`` is the fused LM-head step: hidden [256x1024, 1024] bf16 and
 an LM-head weight [151936, 1024] bf16 -> log-probs -> clipped objective ->
-d hidden and d weight, through ``fused_linear_policy_loss`` (``--path
-composed``: F.linear, gather_token_logprobs, clipped_policy_loss, autograd);
-its roofline is MFMA-bound (3 x 2*N*H*V flops per step).
+d hidden and d weight, through ``fused_linear_policy_loss`` on the
+hand-written MFMA kernels (``--path composed``: F.linear,
+gather_token_logprobs, clipped_policy_loss, autograd).  Its roofline is
+MFMA-bound: the reference's three products, 3 x 2*N*H*V = 244.7 TFLOP per
+step, against the dense bf16 peak.
 
 ``--config sample`` is the rollout side: one decode step of 256 rows x
 151936 bf16 logits -> next token + behaviour log-probs
@@ -33,11 +42,15 @@ forwards (rosetrainer/model.py:643-649) on config 2's logits, labels = the
 sampled tokens: ``rosellm_amd.rosetrainer.causal_lm_loss`` (the same
 single-pass row kernel, objective NLL) -> backward to bf16 dlogits.
 
-Prints one JSON line (rank 0): value = tokens/s over all B*T positions, plus
-``roofline`` for the dominant kernel (HIP events around its entry point over
-the timed steps; algorithmic bytes N*(V*(2+2) + 21)) and ``cpu_baseline``, the
-oracle's PyTorch-CPU composition timed on a bounded sub-batch of the same
-tensors.
+Prints one JSON line (rank 0): value = tokens/s over all B*T positions (the
+wall clock over the timed steps; the median of the per-step event times is
+beside it), ``roofline`` for the dominant kernel (HIP events around its
+entry point over a second pass of the timed steps; algorithmic bytes
+N*(V*(2+2) + 21) for the row kernels) and ``cpu_baseline``: the oracle's
+PyTorch-CPU composition timed on the sub-batch BASELINE's CPU plan names
+(C1 whole, C2/C3/SFT 16 sequences = 2 groups of 8, C4 2 x 8192, C5 16
+sequences), with the same sub-batch run through the HIP path in the same run
+as its parity batch.
 """
 
 from __future__ import annotations
@@ -88,8 +101,13 @@ CONFIGS["sft"] = dict(CONFIGS["c2"], objective="nll", kw={}, sft=True,
                       workload="SFT: next-token cross-entropy fwd+bwd (rosetrainer/model.py:"
                                "643-649), 256x1024 tokens, V=151936 bf16")
 SFT_SIDE_BYTES = 12  # per row: 8 label + 4 logp out
-LM_HEAD_ROW_BLOCK = 16384
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# Sequences of the CPU plan's sub-batch per config (C1 whole; C4's are 8192 long).
+CPU_SEQS = {"c1": 32, "c2": 16, "c3": 16, "sft": 16, "c4": 2, "c5": 16}
+# Configurations timed after the headline, reported under "variants".
+VARIANTS = ["c1", "c3", "c3_gspo_token", "c4", "sft", "sample", "c5"]
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -107,16 +125,35 @@ def parse_args():
     p.add_argument("--path", choices=["fused", "composed"], default="fused")
     p.add_argument("--objective", choices=["gspo", "gspo_token"], default=None,
                    help="config c3 only: GSPO (default) or GSPO-token")
-    p.add_argument("--cpu-sample-seqs", type=int, default=2,
-                   help="sequences of the batch timed on the CPU oracle")
+    p.add_argument("--cpu-sample-seqs", type=int, default=None,
+                   help="sequences of the batch timed on the CPU oracle (default: the CPU "
+                        "plan's sub-batch of the config)")
     p.add_argument("--cpu-runs", type=int, default=3)
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--no-variants", action="store_true",
-                   help="do not also time the skip_masked_rows variant of the fused path")
+                   help="time the headline configuration only")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also launch one device copy of known size (HBM counter calibration)")
     p.add_argument("--seed", type=int, default=1234)
     return p.parse_args()
+
+
+def fill_logits(logits, cfg, device, seed):
+    """The config's logits, written into ``logits`` [B, T, V] from generators
+    seeded seed + 0, 1, 2 (the same values on every call)."""
+
+    import torch
+
+    V = logits.shape[-1]
+    gens = [torch.Generator(device=device).manual_seed(seed + i) for i in range(3)]
+    torch.randn(logits.shape, dtype=logits.dtype, device=device, generator=gens[0], out=logits)
+    logits.mul_(cfg["sigma"])
+    if cfg["hot"] > 0:
+        flat = logits.view(-1, V)
+        hot_rows = torch.nonzero(torch.rand(flat.shape[0], device=device, generator=gens[1])
+                                 < cfg["hot"]).reshape(-1)
+        hot_cols = torch.randint(0, V, (hot_rows.numel(),), device=device, generator=gens[2])
+        flat[hot_rows, hot_cols] = (flat[hot_rows, hot_cols].float() + 15.0).to(logits.dtype)
 
 
 def make_inputs(cfg, device, seed):
@@ -141,16 +178,9 @@ def make_inputs(cfg, device, seed):
         h2 = hidden.view(-1, H)
         row_logits = lambda r0, r1: torch.mm(h2[r0:r1], weight.t())
     else:
-        logits = torch.randn(B, T, V, dtype=dtype, device=device, generator=gens[0])
-        logits.mul_(cfg["sigma"])
+        logits = torch.empty(B, T, V, dtype=dtype, device=device)
+        fill_logits(logits, cfg, device, seed)
         flat = logits.view(-1, V)
-        if cfg["hot"] > 0:
-            hot_rows = torch.nonzero(torch.rand(B * T, device=device, generator=gens[1])
-                                     < cfg["hot"])
-            hot_rows = hot_rows.reshape(-1)
-            hot_cols = torch.randint(0, V, (hot_rows.numel(),), device=device,
-                                     generator=gens[2])
-            flat[hot_rows, hot_cols] = (flat[hot_rows, hot_cols].float() + 15.0).to(dtype)
         row_logits = lambda r0, r1: flat[r0:r1]
     # Actions ~ softmax(logits) by Gumbel-max; reference log-probs by
     # log_softmax in float32, chunked so no [N, V] float32 tensor is built.
@@ -217,8 +247,7 @@ def make_step(inp, cfg, path, objective, skip_masked=False, probe=None):
             weight.grad = None
             a = R.group_standardized_advantages(rewards).reshape(-1)[:, None].expand(B, T)
             if path == "fused":
-                out = R.fused_linear_policy_loss(hidden, weight, actions, old, a, mask,
-                                                 row_block=LM_HEAD_ROW_BLOCK, **kw)
+                out = R.fused_linear_policy_loss(hidden, weight, actions, old, a, mask, **kw)
             else:
                 lp = R.gather_token_logprobs(F.linear(hidden, weight), actions)
                 _watch(lp, probe)
@@ -244,9 +273,9 @@ def make_step(inp, cfg, path, objective, skip_masked=False, probe=None):
 
     if objective == "sapo":
         # Config 4: GAE over the valid tokens, whitened, then SAPO.  dlogits
-        # overwrite the logits (logits + dlogits would need 318.6 GB), so each
-        # step after the first runs on the previous step's dlogits: the same
-        # work on different values.
+        # overwrite the logits (logits + dlogits would need 318.6 GB); the
+        # timing loops regenerate the logits from their seed before every
+        # step (prepare_step), outside the step's events.
         def step():
             logits.grad = None
             adv, _ = R.generalized_advantage_estimation(rewards, inp["values"], gamma=1.0,
@@ -283,24 +312,78 @@ def make_step(inp, cfg, path, objective, skip_masked=False, probe=None):
     return step
 
 
-def cpu_baseline(inp, cfg, n_seq, runs):
-    """The oracle's PyTorch-CPU composition (log_softmax -> gather -> clip ->
-    autograd), op for op the reference's, timed on the first n_seq sequences."""
+def cpu_info():
+    """Host facts recorded beside every CPU figure."""
+
+    import torch
+
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "cpu_model": model}
+
+
+def _median_runs(fn, runs, what):
+    """Run fn() 1 + runs times (the first a warm-up): (median seconds, last output)."""
+
+    times, out = [], None
+    for i in range(runs + 1):
+        t0 = time.perf_counter()
+        out = fn()
+        dt = time.perf_counter() - t0
+        if i > 0:
+            times.append(dt)
+        log(f"[bench] cpu oracle {what} run {i}: {dt:.2f} s")
+    return statistics.median(times), out
+
+
+def _err(got, want, chunk=1024):
+    """Largest absolute difference, largest |want|, and the relative L2 norm of
+    the difference, accumulated in float64 over row chunks (host memory stays
+    a few chunks)."""
+
+    g2 = got.detach().reshape(-1, got.shape[-1])
+    w2 = want.detach().reshape(-1, want.shape[-1])
+    mx = mw = ss_d = ss_w = 0.0
+    for r0 in range(0, g2.shape[0], chunk):
+        g = g2[r0:r0 + chunk].cpu().double()
+        w = w2[r0:r0 + chunk].cpu().double()
+        d = g - w
+        mx = max(mx, float(d.abs().max()))
+        mw = max(mw, float(w.abs().max()))
+        ss_d += float((d * d).sum())
+        ss_w += float((w * w).sum())
+    return {"max_abs_err": mx, "max_abs": mw,
+            "rel_l2": math.sqrt(ss_d / ss_w) if ss_w > 0 else math.sqrt(ss_d)}
+
+
+def cpu_baseline(inp, cfg, name, objective, path, n_seq, runs):
+    """The oracle's PyTorch-CPU composition (log_softmax -> gather -> objective
+    -> autograd), op for op the reference's, timed on the first n_seq
+    sequences (for C2/C3/SFT: 2 whole groups of 8, self-contained), and the
+    same sub-batch through the HIP path as its parity batch."""
 
     import torch
 
     from oracle import roserlhf_oracle as o
+    from rosellm_amd import roserlhf as R
 
     T = inp["T"]
     if cfg.get("lm_head"):
         return cpu_baseline_lm_head(inp, cfg, n_seq, runs)
+    if cfg.get("sft"):
+        return cpu_baseline_sft(inp, n_seq, runs)
     x = inp["logits"].detach()[:n_seq].cpu()
     t = inp["actions"][:n_seq].cpu()
-    if cfg.get("sft"):
-        return cpu_baseline_sft(x, t, inp, n_seq, runs)
     old = inp["old"][:n_seq].cpu()
     mask = inp["mask"][:n_seq].cpu()
-    objective = cfg["objective"]
     if objective == "sapo":
         adv, _ = o.gae(inp["rewards"][:n_seq].cpu(), inp["values"][:n_seq].cpu(), gamma=1.0,
                        gae_lambda=0.95, valid_mask=mask)
@@ -309,68 +392,81 @@ def cpu_baseline(inp, cfg, n_seq, runs):
         seq_adv = o.group_standardize(inp["rewards"].cpu()).reshape(-1)[:n_seq]
         adv = seq_adv if objective == "gspo" else seq_adv[:, None].expand(n_seq, T)
     kind = {"clipped": "ppo"}.get(objective, objective)
-    threads = torch.get_num_threads()
-    times = []
-    for i in range(runs + 1):
-        t0 = time.perf_counter()
-        o.policy_step(kind, x, t, old, adv, mask, **cfg["kw"])
-        dt = time.perf_counter() - t0
-        if i > 0:
-            times.append(dt)
-        log(f"[bench] cpu oracle run {i}: {dt:.2f} s")
-    med = statistics.median(times)
+    med, (out_c, _lp, dl_c) = _median_runs(
+        lambda: o.policy_step(kind, x, t, old, adv, mask, **cfg["kw"]), runs, name)
+    # the same sub-batch on the GPU (a copy of its logits: C4 works in place)
+    dev = inp["logits"].device
+    xg = inp["logits"].detach()[:n_seq].clone().requires_grad_()
+    d = lambda z: z.to(dev)  # noqa: E731
+    if path == "fused":
+        out_g = R.fused_policy_loss(xg, d(t), d(old), d(adv), d(mask), objective=objective,
+                                    **cfg["kw"])
+    else:
+        fn = {"clipped": R.clipped_policy_loss, "gspo": R.gspo_policy_loss,
+              "gspo_token": R.gspo_token_policy_loss, "sapo": R.sapo_policy_loss}[objective]
+        out_g = fn(R.gather_token_logprobs(xg, d(t)), d(old), d(adv), d(mask), **cfg["kw"])
+    out_g.loss.backward()
+    torch.cuda.synchronize()
+    lc, lg = float(out_c["loss"]), float(out_g.loss)
+    parity = {"loss_cpu": lc, "loss_gpu": lg,
+              "loss_rel_err": abs(lg - lc) / max(abs(lc), 1e-30),
+              "dlogits": _err(xg.grad, dl_c)}
+    del xg, dl_c
+    rows = n_seq * T
     return {
-        "value": round(n_seq * T / med, 1),
-        "unit": "tokens/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"first {n_seq} of {inp['B']} sequences ({n_seq * T} token rows, same "
-                   f"tensors), oracle log_softmax->gather->{objective}->autograd on the fp32 "
-                   f"upcast, "
-                   f"median of {runs} runs after 1 warm-up, torch threads={threads}, "
-                   f"os.cpu_count()={os.cpu_count()}"),
+        "value": round(rows / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+        "kind": "port", "median_s": round(med, 4),
+        "sample": (f"first {n_seq} of {inp['B']} sequences ({rows} token rows, the same "
+                   f"tensors copied from the GPU), oracle log_softmax->gather->{objective}->"
+                   f"autograd on the fp32 upcast, median of {runs} runs after 1 warm-up"),
+        **cpu_info(), "gpu_parity": parity,
     }
 
 
-def cpu_baseline_sft(x, t, inp, n_seq, runs):
+def cpu_baseline_sft(inp, n_seq, runs):
     """SFT loss on the CPU: the oracle's shift -> log_softmax -> gather ->
-    mean -> autograd on the float32 upcast of the first n_seq sequences."""
+    mean -> autograd on the float32 upcast of the first n_seq sequences; the
+    same sub-batch through the HIP path as its parity batch."""
 
     import torch
 
     from oracle import roserlhf_oracle as o
+    from rosellm_amd import rosetrainer as RT
 
     T = inp["T"]
-    threads = torch.get_num_threads()
-    times = []
-    for i in range(runs + 1):
-        t0 = time.perf_counter()
-        o.sft_step(x, t, causal=True)
-        dt = time.perf_counter() - t0
-        if i > 0:
-            times.append(dt)
-        log(f"[bench] cpu oracle run {i}: {dt:.2f} s")
-    med = statistics.median(times)
+    x = inp["logits"].detach()[:n_seq].cpu()
+    t = inp["actions"][:n_seq].cpu()
+    med, (loss_c, dl_c) = _median_runs(lambda: o.sft_step(x, t, causal=True), runs, "sft")
+    xg = inp["logits"].detach()[:n_seq].clone().requires_grad_()
+    loss_g = RT.causal_lm_loss(xg, t.to(xg.device))
+    loss_g.backward()
+    torch.cuda.synchronize()
+    lc, lg = float(loss_c), float(loss_g)
+    parity = {"loss_cpu": lc, "loss_gpu": lg,
+              "loss_rel_err": abs(lg - lc) / max(abs(lc), 1e-30),
+              "dlogits": _err(xg.grad, dl_c)}
+    del xg, dl_c
+    rows = n_seq * T
     return {
-        "value": round(n_seq * T / med, 1),
-        "unit": "tokens/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"first {n_seq} of {inp['B']} sequences ({n_seq * T} token rows, same "
+        "value": round(rows / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+        "kind": "port", "median_s": round(med, 4),
+        "sample": (f"first {n_seq} of {inp['B']} sequences ({rows} token rows, the same "
                    f"tensors), oracle shift->log_softmax->gather->mean->autograd on the fp32 "
-                   f"upcast, median of {runs} runs after 1 warm-up, torch threads={threads}, "
-                   f"os.cpu_count()={os.cpu_count()}"),
+                   f"upcast, median of {runs} runs after 1 warm-up"),
+        **cpu_info(), "gpu_parity": parity,
     }
 
 
 def cpu_baseline_lm_head(inp, cfg, n_seq, runs):
     """Config 5 on the CPU: the reference chain (hidden @ W.T, log_softmax,
     gather, clipped objective, autograd back through the linear map) in
-    float32 on the first n_seq sequences."""
+    float32 on the first n_seq sequences; the same sub-batch through the HIP
+    path as its parity batch."""
 
     import torch
 
     from oracle import roserlhf_oracle as o
+    from rosellm_amd import roserlhf as R
 
     T = inp["T"]
     h = inp["hidden"].detach()[:n_seq].cpu().float()
@@ -380,27 +476,32 @@ def cpu_baseline_lm_head(inp, cfg, n_seq, runs):
     mask = inp["mask"][:n_seq].cpu()
     seq_adv = o.group_standardize(inp["rewards"].cpu()).reshape(-1)[:n_seq]
     adv = seq_adv[:, None].expand(n_seq, T)
-    threads = torch.get_num_threads()
-    times = []
-    for i in range(runs + 1):
-        t0 = time.perf_counter()
+
+    def run():
         x = h @ w.t()
-        o.lm_head_step("ppo", h, w, x, t, old, adv, mask, **cfg["kw"])
-        dt = time.perf_counter() - t0
-        del x
-        if i > 0:
-            times.append(dt)
-        log(f"[bench] cpu oracle run {i}: {dt:.2f} s")
-    med = statistics.median(times)
+        return o.lm_head_step("ppo", h, w, x, t, old, adv, mask, **cfg["kw"])
+
+    med, (out_c, _lp, dh_c, dw_c) = _median_runs(run, runs, "c5")
+    dev = inp["hidden"].device
+    hg = inp["hidden"].detach()[:n_seq].clone().requires_grad_()
+    wg = inp["weight"].detach().clone().requires_grad_()
+    d = lambda z: z.to(dev)  # noqa: E731
+    out_g = R.fused_linear_policy_loss(hg, wg, d(t), d(old), d(adv), d(mask), **cfg["kw"])
+    out_g.loss.backward()
+    torch.cuda.synchronize()
+    lc, lg = float(out_c["loss"]), float(out_g.loss)
+    parity = {"loss_cpu": lc, "loss_gpu": lg,
+              "loss_rel_err": abs(lg - lc) / max(abs(lc), 1e-30),
+              "dhidden": _err(hg.grad, dh_c), "dweight": _err(wg.grad, dw_c)}
+    del hg, wg
+    rows = n_seq * T
     return {
-        "value": round(n_seq * T / med, 1),
-        "unit": "tokens/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"first {n_seq} of {inp['B']} sequences ({n_seq * T} token rows, same "
+        "value": round(rows / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+        "kind": "port", "median_s": round(med, 4),
+        "sample": (f"first {n_seq} of {inp['B']} sequences ({rows} token rows, same "
                    f"tensors), oracle hidden@W.T->log_softmax->gather->clip->autograd through "
-                   f"the LM head in float32, median of {runs} runs after 1 warm-up, torch "
-                   f"threads={threads}, os.cpu_count()={os.cpu_count()}"),
+                   f"the LM head in float32, median of {runs} runs after 1 warm-up"),
+        **cpu_info(), "gpu_parity": parity,
     }
 
 
@@ -418,29 +519,281 @@ def traffic_from_profiles(kernel_key, workload_key):
         return None
 
 
-def timed_steps(step, steps, kernels):
-    """Time `steps` calls of `step` by the wall clock, bracketed by device
-    synchronisations, then run as many again with HIP events recorded around
-    every launch of `kernels` (on the stream each is launched on).  Returns
-    (seconds of the first loop, its last output, {kernel: [(start, end)]}):
-    the events never sit inside the wall-clock loop."""
+def timed_steps(step, steps, kernels, prepare=None):
+    """Time `steps` calls of `step`: a wall-clock loop bracketed by device
+    synchronisations, with one event recorded between consecutive steps (the
+    per-step times), then as many steps again with HIP events recorded around
+    every launch of `kernels` (on the stream each is launched on).  With
+    `prepare` (run before each step, outside its events) the wall clock would
+    include it: only the per-step events time the steps.  Returns a dict:
+    wall_s (None with prepare), step_ms (list), out (the last output), launches
+    ({kernel: [(start, end)]})."""
 
     import torch
 
     from rosellm_amd import _native as nat
 
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
+    out = None
+    for i in range(steps):
+        if prepare is not None:
+            prepare()
+        ev[2 * i].record()
         out = step()
+        ev[2 * i + 1].record()
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    wall = None if prepare is not None else time.perf_counter() - t0
+    if prepare is None:
+        # consecutive steps: the time from one step's start to the next one's
+        step_ms = [ev[2 * i].elapsed_time(ev[2 * i + 2]) for i in range(steps - 1)]
+        step_ms.append(ev[2 * steps - 2].elapsed_time(ev[2 * steps - 1]))
+    else:
+        step_ms = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(steps)]
     timed = nat.time_calls(*kernels, capacity=steps * 32)
     for _ in range(steps):
+        if prepare is not None:
+            prepare()
         step()
     torch.cuda.synchronize()
     nat.time_calls()
-    return elapsed, out, timed
+    return {"wall_s": wall, "step_ms": step_ms, "out": out, "launches": timed}
+
+
+def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
+                   skip_masked_variant=False):
+    """One configuration (a key of CONFIGS, or "c3_gspo_token"): inputs,
+    warm-up, timed steps, the roofline of its dominant kernel and, with
+    with_cpu, the CPU baseline with its GPU parity batch.  Returns the
+    headline-format result dict."""
+
+    import torch
+
+    objective_override = None
+    if name == "c3_gspo_token":
+        name, objective_override = "c3", "gspo_token"
+    cfg = CONFIGS[name]
+    log(f"[bench] config {name}{'/' + objective_override if objective_override else ''}: "
+        f"generating inputs")
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        inp = make_inputs(cfg, device, args.seed)
+    torch.cuda.synchronize()
+    log(f"[bench] inputs ready in {time.perf_counter() - t0:.1f} s")
+    N, V = inp["B"] * inp["T"], inp["V"]
+    objective = objective_override or cfg["objective"]
+    cfg = dict(cfg, objective=objective)
+    # GSPO needs every token's log-prob before any gradient: its fused entry is
+    # the two-kernel composition (forward sweep, backward sweep).
+    path = args.path if objective in ("clipped", "sapo") else "composed"
+    if cfg.get("sft"):
+        path = "fused"
+    step = make_step(inp, cfg, path, objective)
+    prepare = None
+    if objective == "sapo":
+        # C4 works in place: the logits are regenerated before each step.
+        prepare = lambda: fill_logits(inp["logits"].data, cfg, device, args.seed)  # noqa: E731
+
+    for i in range(warmup):
+        if prepare is not None:
+            prepare()
+        step()
+        torch.cuda.synchronize()
+    log(f"[bench] {warmup} warm-up steps done")
+
+    if cfg.get("lm_head"):
+        kernels = ["rrl_lm_head_fwd", "rrl_lm_head_dweight", "rrl_lm_head_dhidden"]
+    elif path == "fused":
+        kernels = ["rrl_fused_logprob_policy"]
+    else:
+        kernels = ["rrl_logprob_fwd", "rrl_logprob_bwd"]
+    res = timed_steps(step, steps, kernels, prepare)
+    step_ms = res["step_ms"]
+    ms_step = (res["wall_s"] * 1e3 / steps if res["wall_s"] is not None
+               else sum(step_ms) / len(step_ms))
+    ms_median = statistics.median(step_ms)
+    out = res["out"]
+    tok_s = N / (ms_step * 1e-3)
+    in_b = (inp["hidden"] if cfg.get("lm_head") else inp["logits"]).element_size()
+    k_rows, side = ((inp["B"] * (inp["T"] - 1), SFT_SIDE_BYTES) if cfg.get("sft")
+                    else (N, SIDE_BYTES))
+    alg = {
+        # read logits + write dlogits, 8 target + 4 old + 4 advantage + 1 mask + 4 logp
+        "rrl_fused_logprob_policy": k_rows * (V * (in_b + in_b) + side),
+        # read logits, 8 target, write 4 logp + 4 lse
+        "rrl_logprob_fwd": N * (V * in_b + 8 + 4 + 4),
+        # read logits + write dlogits, 8 target + 4 lse + 4 logp + 4 g (the
+        # logits read is narrowed to the rows with a non-zero g below)
+        "rrl_logprob_bwd": N * (V * (in_b + in_b) + 8 + 4 + 4 + 4),
+    }
+    if path == "composed" and not cfg.get("lm_head"):
+        # Rows whose d loss / d logp is exactly zero (masked, clipped or
+        # zero-advantage tokens) are written as zeros without reading their
+        # logits: count them on one extra, untimed step.
+        probe = {}
+        make_step(inp, cfg, path, objective, probe=probe)()
+        torch.cuda.synchronize()
+        active = probe["active"]
+        alg["rrl_logprob_bwd"] = N * V * in_b + active * V * in_b + N * (8 + 4 + 4 + 4)
+        log(f"[bench] backward reads the logits of {active} of {N} rows")
+    kstats = {}
+    for k in kernels:
+        kms = [s.elapsed_time(e) for s, e in res["launches"][k]]
+        if kms:
+            kstats[k] = (sum(kms) / len(kms), len(kms) / steps)
+    kernels = [k for k in kernels if k in kstats]
+    kernel = max(kernels, key=lambda k: kstats[k][0] * kstats[k][1])  # the dominant kernel
+    k_avg = kstats[kernel][0]
+    log(f"[bench] {steps} steps: {ms_step:.3f} ms/step (median {ms_median:.3f}), "
+        f"{tok_s / 1e6:.3f} M tok/s; "
+        + ", ".join(f"{k} avg {v[0]:.3f} ms" for k, v in kstats.items())
+        + f"; loss {out.loss.item():.6g}")
+    workload_key = f"{name}-{path}" + (f"-{objective}" if name == "c3" else "")
+    if cfg.get("lm_head"):
+        roofline = lm_head_roofline(inp, cfg, kstats, ms_step)
+    else:
+        achieved = alg[kernel] / (k_avg * 1e-3) / 1e9
+        roofline = {
+            "bound": "hbm",
+            "kernel": kernel,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles(kernel, workload_key),
+            "kernel_ms": round(k_avg, 4),
+            "alg_bytes_per_launch": alg[kernel],
+            "kernels_ms": {k: round(v[0], 4) for k, v in kstats.items()},
+            # whole step against the algorithmic minimum of one logits read and
+            # one dlogits write
+            "step_frac": round(k_rows * (V * 2 * in_b + side) / (ms_step * 1e-3) / 1e9
+                               / HBM_PEAK_GBS, 4),
+        }
+
+    variants = {}
+    if skip_masked_variant and path == "fused" and objective == "clipped" \
+            and not cfg.get("lm_head"):
+        # The same step with skip_masked_rows=True (zero-weight rows are never
+        # read); reported beside the exact-semantics headline, not as `value`.
+        vstep = make_step(inp, cfg, path, objective, skip_masked=True)
+        for _ in range(warmup):
+            vstep()
+        vres = timed_steps(vstep, steps, kernels[:1])
+        v_el = vres["wall_s"]
+        v_ms = [s.elapsed_time(e) for s, e in vres["launches"][kernels[0]]]
+        v_k = sum(v_ms) / len(v_ms)
+        assert vres["out"].loss.item() == out.loss.item(), "skip_masked_rows changed the loss"
+        n_active = int(inp["mask"].sum().item())
+        v_alg = n_active * V * in_b + N * V * in_b + N * SIDE_BYTES
+        variants["skip_masked_rows"] = {
+            "value": round(N / (v_el / steps), 1),
+            "ms_per_step": round(v_el * 1e3 / steps, 4),
+            "ms_per_step_median": round(statistics.median(vres["step_ms"]), 4),
+            "kernel_ms": round(v_k, 4),
+            "active_rows": n_active,
+            "alg_bytes_per_launch": v_alg,
+            "achieved": round(v_alg / (v_k * 1e-3) / 1e9, 1),
+            "frac": round(v_alg / (v_k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        log(f"[bench] skip_masked_rows: {v_el * 1e3 / steps:.3f} ms/step, "
+            f"{N / (v_el / steps) / 1e6:.3f} M tok/s, kernel {v_k:.3f} ms")
+
+    if args.calibrate_copy:
+        # Calibration kernel of known traffic for the HBM counters: a bf16 ->
+        # float32 conversion of 2^30 random elements reads 2 GiB and writes
+        # 4 GiB (a same-dtype copy would run as a DMA blit, invisible to the
+        # counters; constant data can compress in the memory fabric).
+        src = torch.randn(1 << 30, dtype=torch.bfloat16, device=device)
+        dst = torch.empty(1 << 30, dtype=torch.float32, device=device)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration conversion: {src.numel() * 2} B read, "
+            f"{dst.numel() * 4} B written")
+        del src, dst
+
+    cpu = None
+    if with_cpu:
+        if prepare is not None:
+            prepare()  # C4: the config's logits, not the last step's dlogits
+        n_seq = min(cpu_seqs or CPU_SEQS.get(name, 16), inp["B"])
+        cpu = cpu_baseline(inp, cfg, name, objective, path, n_seq, args.cpu_runs)
+
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_step, 4),
+        "ms_per_step_median": round(ms_median, 4),
+        "step_time": ("wall clock over the timed steps" if res["wall_s"] is not None else
+                      "mean of per-step events (the logits are regenerated between steps)"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg["dtype"].replace("bfloat16", "bf16").replace("float32", "fp32"),
+        "data": "synthetic (config distributions, generated on the GPU, seed 1234+i)",
+        "config": {
+            "workload": cfg["workload"],
+            "objective": objective,
+            "path": path,
+            "sequences": inp["B"],
+            "seq_len": inp["T"],
+            "vocab": V,
+            **({"hidden": inp["hidden"].shape[-1]} if cfg.get("lm_head") else {}),
+            "tokens_per_step": N,
+            "parallelism": "none (1 GPU)",
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    if variants:
+        result["variants"] = variants
+    return result
+
+
+def lm_head_roofline(inp, cfg, kstats, ms_step):
+    """Config 5: the step against the dense bf16 MFMA peak on the reference's
+    three products (3 x 2*N*H*V, the model's flops), and each kernel's
+    executed flops (the work skipping is exact: blocks of 64 tokens none of
+    which needs obar run the log-sum-exp pass only, and the dW pass visits
+    the 32-token tiles holding a token with a non-zero gradient)."""
+
+    N = inp["B"] * inp["T"]
+    V, H = inp["V"], inp["hidden"].shape[-1]
+    mask = inp["mask"].reshape(-1)
+    need_blocks = int(mask[: (N // 64) * 64].reshape(-1, 64).any(dim=1).sum().item())
+    flops_model = 3 * 2 * N * H * V
+    fwd_exec = 2 * N * H * V + 2 * need_blocks * 64 * H * V
+    # tiles with a non-zero gradient: at most the tiles holding a masked-in token
+    act_tiles = int(mask[: (N // 32) * 32].reshape(-1, 32).any(dim=1).sum().item())
+    dw_exec = 2 * 2 * act_tiles * 32 * H * V
+    fwd_ms = kstats["rrl_lm_head_fwd"][0]
+    dw_ms = kstats["rrl_lm_head_dweight"][0]
+    step_tf = flops_model / (ms_step * 1e-3) / 1e12
+    fwd_tf = fwd_exec / (fwd_ms * 1e-3) / 1e12
+    return {
+        "bound": "mfma",
+        "kernel": "rrl_lm_head_fwd",
+        "achieved": round(fwd_tf, 1),
+        "peak": MFMA_BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(fwd_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+        "traffic": None,
+        "kernel_ms": round(fwd_ms, 4),
+        "alg_flops_per_launch": fwd_exec,
+        "step": {"model_flops": flops_model, "achieved_TFLOPs": round(step_tf, 1),
+                 "frac": round(step_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                 "note": "the reference's three products 3*2*N*H*V over the step time"},
+        "dweight": {"kernel_ms": round(dw_ms, 4), "executed_flops": dw_exec,
+                    "achieved_TFLOPs": round(dw_exec / (dw_ms * 1e-3) / 1e12, 1),
+                    "active_tiles_bound": act_tiles},
+        "fwd_obar_blocks": need_blocks,
+        "kernels_ms": {k: round(v[0], 4) for k, v in kstats.items()},
+    }
 
 
 SAMPLE_ROWS = 256
@@ -450,15 +803,13 @@ SAMPLE_VARIANTS = {"default": dict(temperature=1.0, top_k=0, top_p=1.0, do_sampl
                    "greedy": dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=False)}
 
 
-def bench_sample(args):
+def bench_sample(args, steps, warmup, with_cpu):
     """Rollout sampling: tokens/s of sample_next_token_batch over 256 rows of
     151936 bf16 logits (config 2's distribution), one call per step."""
 
-    import numpy as np
     import torch
 
     from oracle import sampler_oracle as so
-    from rosellm_amd import _native as nat
     from rosellm_amd.roseinfer import sample_next_token_batch
 
     device = torch.device("cuda", 0)
@@ -470,43 +821,41 @@ def bench_sample(args):
     x[rows, hot[rows]] = (x[rows, hot[rows]].float() + 15.0).to(torch.bfloat16)
     results = {}
     for name, kw in SAMPLE_VARIANTS.items():
-        for i in range(args.warmup):
+        for i in range(warmup):
             sample_next_token_batch(x, seed=args.seed, offset=i, **kw)
-        offs = iter(range(100, 100 + 2 * args.steps))
-        el, out, timed = timed_steps(
-            lambda: sample_next_token_batch(x, seed=args.seed, offset=next(offs), **kw),
-            args.steps, ["rrl_sample_logprobs"])
-        kms = [s.elapsed_time(e) for s, e in timed["rrl_sample_logprobs"]]
-        results[name] = dict(ms=el * 1e3 / args.steps, kernel_ms=sum(kms) / len(kms),
-                             tokens=out.token_ids)
-        log(f"[bench] sample {name}: {el * 1e3 / args.steps:.4f} ms/step, kernel "
-            f"{results[name]['kernel_ms']:.4f} ms")
+        offs = iter(range(100, 100 + 2 * steps))
+        res = timed_steps(lambda: sample_next_token_batch(x, seed=args.seed, offset=next(offs),
+                                                          **kw),
+                          steps, ["rrl_sample_logprobs"])
+        kms = [s.elapsed_time(e) for s, e in res["launches"]["rrl_sample_logprobs"]]
+        ms = res["wall_s"] * 1e3 / steps
+        results[name] = dict(ms=ms, median=statistics.median(res["step_ms"]),
+                             kernel_ms=sum(kms) / len(kms))
+        log(f"[bench] sample {name}: {ms:.4f} ms/step, kernel {results[name]['kernel_ms']:.4f} ms")
     head = results["default"]
     alg = B * (V * 2 + 8 + 4 + 4)  # one read of the logits; token + two log-probs out
     achieved = alg / (head["kernel_ms"] * 1e-3) / 1e9
     cpu = None
-    if not args.skip_cpu:
+    if with_cpu:
         n = 16
         xc = x[:n].float().cpu().numpy()
-        times = []
-        for i in range(args.cpu_runs + 1):
-            t0 = time.perf_counter()
-            so.sample_rows(xc, temperature=1.0, top_k=0, top_p=1.0, do_sample=True,
-                           seed=args.seed, offset=0)
-            if i:
-                times.append(time.perf_counter() - t0)
-        med = statistics.median(times)
+        med, _ = _median_runs(lambda: so.sample_rows(xc, temperature=1.0, top_k=0, top_p=1.0,
+                                                     do_sample=True, seed=args.seed, offset=0),
+                              args.cpu_runs, "sampler")
         cpu = {"value": round(n / med, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "median_s": round(med, 4),
                "sample": f"first {n} of {B} rows, oracle inverse-CDF sampler in float64 NumPy "
-                         f"(one thread), median of {args.cpu_runs} runs after 1 warm-up"}
-    result = {
+                         f"(one thread), median of {args.cpu_runs} runs after 1 warm-up",
+               **cpu_info()}
+    return {
         "metric": "tokens/sec sampled with behaviour log-probs @151936 vocab (rollout side)",
         "value": round(B / (head["ms"] * 1e-3), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(head["ms"], 4),
+        "ms_per_step_median": round(head["median"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -525,7 +874,33 @@ def bench_sample(args):
                          "value": round(B / (v["ms"] * 1e-3), 1)}
                      for k, v in results.items() if k != "default"},
     }
-    print(json.dumps(result), flush=True)
+
+
+def compact(r):
+    """The fields of a configuration's result kept under the headline's variants."""
+
+    keep = {k: r.get(k) for k in ("value", "unit", "ms_per_step", "ms_per_step_median",
+                                   "steps", "dtype", "step_time")}
+    keep["workload"] = r["config"]["workload"]
+    rf = r["roofline"]
+    keep["roofline"] = {k: rf.get(k) for k in ("bound", "kernel", "achieved", "peak", "unit",
+                                                "frac", "kernel_ms", "alg_bytes_per_launch",
+                                                "alg_flops_per_launch", "step", "dweight",
+                                                "kernels_ms") if k in rf}
+    keep["cpu_baseline"] = r.get("cpu_baseline")
+    if r.get("variants"):
+        keep["variants"] = r["variants"]
+    return keep
+
+
+def default_steps(name, args):
+    """Timed steps and warm-up of a configuration: 200 / 20 for C1 and the
+    sampler (sub-millisecond, host-bound steps), else --steps / --warmup
+    (default 10 / 2)."""
+
+    if name in ("c1", "sample"):
+        return max(args.steps or 0, 200), max(args.warmup or 0, 20)
+    return args.steps or 10, args.warmup if args.warmup is not None else 2
 
 
 def main():
@@ -535,231 +910,43 @@ def main():
               "shards by whole GRPO groups with one scalar all-reduce per step, which "
               "is not run here.", file=sys.stderr)
         sys.exit(2)
-    if args.steps is None:
-        args.steps = 200 if args.config in ("c1", "sample") else 10
-    if args.warmup is None:
-        args.warmup = 20 if args.config in ("c1", "sample") else 2
-    if args.config == "sample":
-        bench_sample(args)
-        return
+
+    import gc
 
     import torch
 
-    from rosellm_amd import _native as nat
-
     device = torch.device("cuda", 0)
-    cfg = CONFIGS[args.config]
-    log(f"[bench] config {args.config} path {args.path}: generating inputs")
-    t0 = time.perf_counter()
-    with torch.no_grad():
-        inp = make_inputs(cfg, device, args.seed)
-    torch.cuda.synchronize()
-    log(f"[bench] inputs ready in {time.perf_counter() - t0:.1f} s")
-    N, V = inp["B"] * inp["T"], inp["V"]
-    objective = cfg["objective"]
-    if args.objective:
-        if args.config != "c3":
-            raise SystemExit("--objective applies to config c3")
-        objective = args.objective
-    cfg = dict(cfg, objective=objective)
-    # GSPO needs every token's log-prob before any gradient: its fused entry is
-    # the two-kernel composition (forward sweep, backward sweep).
-    path = args.path if objective in ("clipped", "sapo") else "composed"
-    if cfg.get("sft"):
-        path = "fused"
-    step = make_step(inp, cfg, path, objective)
-
-    for i in range(args.warmup):
-        step()
-        torch.cuda.synchronize()
-        log(f"[bench] warmup {i} done")
-
-    kernels = (["rrl_fused_logprob_policy"] if path == "fused"
-               else ["rrl_logprob_fwd", "rrl_logprob_bwd"])
-    elapsed, out, timed = timed_steps(step, args.steps, kernels)
-    ms_step = elapsed * 1e3 / args.steps
-    tok_s = N / (elapsed / args.steps)
-    in_b = (inp["hidden"] if cfg.get("lm_head") else inp["logits"]).element_size()
-    # Rows one launch of the single-pass kernel processes, and their side data
-    # (the SFT loss scores the B*(T-1) positions that have a next token).
-    k_rows, side = (inp["B"] * (inp["T"] - 1), SFT_SIDE_BYTES) if cfg.get("sft") else (N, SIDE_BYTES)
-    # Algorithmic bytes per launch of each timed entry point.
-    alg = {
-        # read logits + write dlogits, 8 target + 4 old + 4 advantage + 1 mask + 4 logp
-        "rrl_fused_logprob_policy": k_rows * (V * (in_b + in_b) + side),
-        # read logits, 8 target, write 4 logp + 4 lse
-        "rrl_logprob_fwd": N * (V * in_b + 8 + 4 + 4),
-        # read logits + write dlogits, 8 target + 4 lse + 4 logp + 4 g (the
-        # logits read is narrowed to the rows with a non-zero g below)
-        "rrl_logprob_bwd": N * (V * (in_b + in_b) + 8 + 4 + 4 + 4),
-    }
-    if path == "composed":
-        # Rows whose d loss / d logp is exactly zero (masked, clipped or
-        # zero-advantage tokens) are written as zeros without reading their
-        # logits: count them on one extra, untimed step.
-        probe = {}
-        make_step(inp, cfg, path, objective, probe=probe)()
-        torch.cuda.synchronize()
-        active = probe["active"]
-        alg["rrl_logprob_bwd"] = N * V * in_b + active * V * in_b + N * (8 + 4 + 4 + 4)
-        log(f"[bench] backward reads the logits of {active} of {N} rows")
-    kstats = {}
-    for k in kernels:
-        kms = [s.elapsed_time(e) for s, e in timed[k]]
-        kstats[k] = sum(kms) / len(kms)
-    kernel = max(kernels, key=lambda k: kstats[k])  # the dominant kernel
-    k_avg = kstats[kernel]
-    log(f"[bench] {args.steps} steps: {ms_step:.3f} ms/step, {tok_s / 1e6:.3f} M tok/s; "
-        + ", ".join(f"{k} avg {v:.3f} ms" for k, v in kstats.items())
-        + f"; loss {out.loss.item():.6g}")
-    achieved = alg[kernel] / (k_avg * 1e-3) / 1e9
-    workload_key = f"{args.config}-{path}" + (f"-{objective}" if args.config == "c3" else "")
-    if cfg.get("lm_head"):
-        # Config 5 is bound by the three GEMMs (hidden x W^T, dlogits x W,
-        # dlogits^T x hidden): 3 x 2*N*H*V flops per step against the dense
-        # bf16 MFMA peak; the row kernel's share is reported beside it.
-        H = inp["hidden"].shape[-1]
-        flops = 3 * 2 * N * H * V
-        tflops = flops / (ms_step * 1e-3) / 1e12
-        per_step = len(timed[kernel]) / args.steps  # row-kernel launches per step
-        rows_launch = N / per_step
-        alg_launch = (rows_launch * (V * (in_b + in_b) + SIDE_BYTES) if kernel != "rrl_logprob_fwd"
-                      else rows_launch * (V * in_b + 16))
-        k_gbs = alg_launch / (k_avg * 1e-3) / 1e9
-        roofline = {
-            "bound": "mfma",
-            "kernel": "whole step (hipBLASLt GEMMs + " + kernel + ")",
-            "achieved": round(tflops, 1),
-            "peak": MFMA_BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
-            "alg_flops_per_step": flops,
-            "row_kernel": {"name": kernel, "launches_per_step": per_step,
-                           "kernel_ms": round(k_avg, 4),
-                           "ms_per_step": round(k_avg * per_step, 4),
-                           "alg_bytes_per_launch": alg_launch,
-                           "achieved_GBs": round(k_gbs, 1),
-                           "frac_hbm": round(k_gbs / HBM_PEAK_GBS, 4)},
-            "kernels_ms": {k: round(v, 4) for k, v in kstats.items()},
-            "blas": str(torch.backends.cuda.preferred_blas_library()),
-        }
+    if args.objective and args.config != "c3":
+        raise SystemExit("--objective applies to config c3")
+    head_name = "c3_gspo_token" if args.objective == "gspo_token" else args.config
+    steps, warmup = default_steps(args.config, args)
+    if args.config == "sample":
+        result = bench_sample(args, steps, warmup, not args.skip_cpu)
     else:
-        roofline = {
-            "bound": "hbm",
-            "kernel": kernel,
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_from_profiles(kernel, workload_key),
-            "kernel_ms": round(k_avg, 4),
-            "alg_bytes_per_launch": alg[kernel],
-            "kernels_ms": {k: round(v, 4) for k, v in kstats.items()},
-            # whole step against the algorithmic minimum of one logits read and
-            # one dlogits write
-            "step_frac": round(N * (V * 2 * in_b + side) / (ms_step * 1e-3) / 1e9
-                               / HBM_PEAK_GBS, 4),
-        }
-
-    # The same step with skip_masked_rows=True (zero-weight rows are never
-    # read); reported beside the exact-semantics headline, not as `value`.
-    variants = {}
-
-    def time_variant(vstep):
-        """Warm-up, then the timed steps of a variant: (seconds, average
-        duration of the dominant entry point in ms, last output)."""
-
-        for _ in range(args.warmup):
-            vstep()
-        v_el, vout, vt = timed_steps(vstep, args.steps, kernels[:1])
-        v_ms = [s.elapsed_time(e) for s, e in vt[kernels[0]]]
-        return v_el, sum(v_ms) / len(v_ms), vout
-
-    if (path == "fused" and objective == "clipped" and not args.no_variants
-            and not cfg.get("lm_head")):
-        v_el, v_k, vout = time_variant(make_step(inp, cfg, path, objective, skip_masked=True))
-        assert vout.loss.item() == out.loss.item(), "skip_masked_rows changed the loss"
-        n_active = int(inp["mask"].sum().item())
-        v_alg = n_active * V * in_b + N * V * in_b + N * SIDE_BYTES
-        variants["skip_masked_rows"] = {
-            "value": round(N / (v_el / args.steps), 1),
-            "ms_per_step": round(v_el * 1e3 / args.steps, 4),
-            "kernel_ms": round(v_k, 4),
-            "active_rows": n_active,
-            "alg_bytes_per_launch": v_alg,
-            "achieved": round(v_alg / (v_k * 1e-3) / 1e9, 1),
-            "frac": round(v_alg / (v_k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        }
-        log(f"[bench] skip_masked_rows: {v_el * 1e3 / args.steps:.3f} ms/step, "
-            f"{N / (v_el / args.steps) / 1e6:.3f} M tok/s, kernel {v_k:.3f} ms")
-
-    if objective == "sapo" and not args.no_variants:
-        # Config 4 is specified with tau_negative = 1.0; the reference's
-        # default (tau_positive 1.0, tau_negative 1.05) is reported beside it.
-        # Same bytes per step: the taus change only the per-token arithmetic.
-        ref_kw = dict(tau_positive=1.0, tau_negative=1.05)
-        v_el, v_k, _ = time_variant(make_step(inp, dict(cfg, kw=ref_kw), path, objective))
-        v_alg = alg[kernels[0]]
-        variants["reference_default_taus"] = {
-            "kw": ref_kw,
-            "value": round(N / (v_el / args.steps), 1),
-            "ms_per_step": round(v_el * 1e3 / args.steps, 4),
-            "kernel_ms": round(v_k, 4),
-            "achieved": round(v_alg / (v_k * 1e-3) / 1e9, 1),
-            "frac": round(v_alg / (v_k * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        }
-        log(f"[bench] SAPO with the reference's default taus: {v_el * 1e3 / args.steps:.3f} "
-            f"ms/step, {N / (v_el / args.steps) / 1e6:.3f} M tok/s, kernel {v_k:.3f} ms")
-
-    if args.calibrate_copy:
-        # Calibration kernel of known traffic for the HBM counters: a bf16 ->
-        # float32 conversion of 2^30 random elements reads 2 GiB and writes
-        # 4 GiB (a same-dtype copy would run as a DMA blit, invisible to the
-        # counters; constant data can compress in the memory fabric).
-        src = torch.randn(1 << 30, dtype=torch.bfloat16, device=device)
-        dst = torch.empty(1 << 30, dtype=torch.float32, device=device)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"[bench] calibration conversion: {src.numel() * 2} B read, {dst.numel() * 4} B written")
-        del src, dst
-
-    cpu = None
-    if not args.skip_cpu:
-        n_seq = min(args.cpu_sample_seqs, inp["B"])
-        cpu = cpu_baseline(inp, cfg, n_seq, args.cpu_runs)
-
-    result = {
-        "metric": METRIC,
-        "value": round(tok_s, 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": cfg["dtype"].replace("bfloat16", "bf16").replace("float32", "fp32"),
-        "data": "synthetic (config distributions, generated on the GPU, seed 1234+i)",
-        "config": {
-            "workload": cfg["workload"],
-            "objective": objective,
-            "path": path,
-            "sequences": inp["B"],
-            "seq_len": inp["T"],
-            "vocab": V,
-            **({"hidden": inp["hidden"].shape[-1], "row_block": LM_HEAD_ROW_BLOCK}
-               if cfg.get("lm_head") else {}),
-            "tokens_per_step": N,
-            "parallelism": "none (1 GPU)",
-        },
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-    }
-    if variants:
-        result["variants"] = variants
+        result = measure_config(head_name, args, device, steps, warmup, not args.skip_cpu,
+                                cpu_seqs=args.cpu_sample_seqs,
+                                skip_masked_variant=not args.no_variants)
+    gc.collect()
+    torch.cuda.empty_cache()
+    if not args.no_variants:
+        variants = result.setdefault("variants", {})
+        for name in VARIANTS:
+            if name == head_name:
+                continue
+            t0 = time.perf_counter()
+            try:
+                v_steps, v_warm = default_steps(name, args)
+                if name == "sample":
+                    r = bench_sample(args, v_steps, v_warm, not args.skip_cpu)
+                else:
+                    r = measure_config(name, args, device, v_steps, v_warm, not args.skip_cpu)
+                variants[name] = compact(r)
+            except Exception as e:  # recorded, never fatal to the headline
+                variants[name] = {"error": f"{type(e).__name__}: {e}"[:400]}
+                log(f"[bench] variant {name} failed: {variants[name]['error']}")
+            variants.get(name, {})["bench_s"] = round(time.perf_counter() - t0, 1)
+            gc.collect()
+            torch.cuda.empty_cache()
     print(json.dumps(result), flush=True)
 
 
