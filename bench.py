@@ -131,7 +131,11 @@ def parse_args():
     p.add_argument("--cpu-runs", type=int, default=3)
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--no-variants", action="store_true",
-                   help="time the headline configuration only")
+                   help="time the headline configuration only, without its skip_masked_rows "
+                        "variant")
+    p.add_argument("--headline-only", action="store_true",
+                   help="time the headline configuration and its own variants, not the other "
+                        "configurations")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also launch one device copy of known size (HBM counter calibration)")
     p.add_argument("--seed", type=int, default=1234)
@@ -585,8 +589,9 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
     objective = objective_override or cfg["objective"]
     cfg = dict(cfg, objective=objective)
     # GSPO needs every token's log-prob before any gradient: its fused entry is
-    # the two-kernel composition (forward sweep, backward sweep).
-    path = args.path if objective in ("clipped", "sapo") else "composed"
+    # a forward sweep and a backward sweep (rrl_logprob_fwd, rrl_logprob_bwd).
+    gspo_like = objective in ("gspo", "gspo_token")
+    path = args.path
     if cfg.get("sft"):
         path = "fused"
     step = make_step(inp, cfg, path, objective)
@@ -604,7 +609,7 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
 
     if cfg.get("lm_head"):
         kernels = ["rrl_lm_head_fwd", "rrl_lm_head_dweight", "rrl_lm_head_dhidden"]
-    elif path == "fused":
+    elif path == "fused" and not gspo_like:
         kernels = ["rrl_fused_logprob_policy"]
     else:
         kernels = ["rrl_logprob_fwd", "rrl_logprob_bwd"]
@@ -627,12 +632,13 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
         # logits read is narrowed to the rows with a non-zero g below)
         "rrl_logprob_bwd": N * (V * (in_b + in_b) + 8 + 4 + 4 + 4),
     }
-    if path == "composed" and not cfg.get("lm_head"):
+    active = None
+    if (path == "composed" or gspo_like) and not cfg.get("lm_head"):
         # Rows whose d loss / d logp is exactly zero (masked, clipped or
         # zero-advantage tokens) are written as zeros without reading their
-        # logits: count them on one extra, untimed step.
+        # logits: count them on one extra, untimed step of the composition.
         probe = {}
-        make_step(inp, cfg, path, objective, probe=probe)()
+        make_step(inp, cfg, "composed", objective, probe=probe)()
         torch.cuda.synchronize()
         active = probe["active"]
         alg["rrl_logprob_bwd"] = N * V * in_b + active * V * in_b + N * (8 + 4 + 4 + 4)
@@ -672,6 +678,40 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
         }
 
     variants = {}
+    if skip_masked_variant and path == "fused" and gspo_like:
+        # GSPO with skip_masked_rows=True: the forward sweep reads the masked-in
+        # rows only; the backward reads the rows with a non-zero gradient and
+        # writes every dlogits row.  Bytes it moves: those reads, one dlogits
+        # write, and the side data of both sweeps.
+        vstep = make_step(inp, cfg, path, objective, skip_masked=True)
+        for _ in range(warmup):
+            vstep()
+        vk = ["rrl_logprob_fwd_masked", "rrl_logprob_bwd"]
+        vres = timed_steps(vstep, steps, vk)
+        v_el = vres["wall_s"]
+        vms = {k: [s.elapsed_time(e) for s, e in vres["launches"][k]] for k in vk}
+        vavg = {k: sum(v) / len(v) for k, v in vms.items()}
+        assert torch.equal(vres["out"].loss, out.loss), "skip_masked_rows changed the loss"
+        n_active = int((inp["mask"] != 0).sum().item())
+        v_alg = {"rrl_logprob_fwd_masked": n_active * V * in_b + N * (8 + 1 + 4 + 4),
+                 "rrl_logprob_bwd": active * V * in_b + N * V * in_b + N * (8 + 4 + 4 + 4)}
+        k_sum = sum(vavg.values())
+        step_alg = sum(v_alg.values())
+        variants["skip_masked_rows"] = {
+            "value": round(N / (v_el / steps), 1),
+            "ms_per_step": round(v_el * 1e3 / steps, 4),
+            "ms_per_step_median": round(statistics.median(vres["step_ms"]), 4),
+            "kernels_ms": {k: round(v, 4) for k, v in vavg.items()},
+            "mask_active_rows": n_active,
+            "grad_active_rows": active,
+            "alg_bytes_per_step": step_alg,
+            "alg_bytes_per_launch": v_alg,
+            "achieved": round(step_alg / (k_sum * 1e-3) / 1e9, 1),
+            "frac": round(step_alg / (k_sum * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "note": "achieved = both sweeps' bytes over both kernels' time",
+        }
+        log(f"[bench] skip_masked_rows: {v_el * 1e3 / steps:.3f} ms/step, kernels "
+            + ", ".join(f"{k} {v:.3f} ms" for k, v in vavg.items()))
     if skip_masked_variant and path == "fused" and objective == "clipped" \
             and not cfg.get("lm_head"):
         # The same step with skip_masked_rows=True (zero-weight rows are never
@@ -928,7 +968,7 @@ def main():
                                 skip_masked_variant=not args.no_variants)
     gc.collect()
     torch.cuda.empty_cache()
-    if not args.no_variants:
+    if not (args.no_variants or args.headline_only):
         variants = result.setdefault("variants", {})
         for name in VARIANTS:
             if name == head_name:

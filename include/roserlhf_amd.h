@@ -163,6 +163,17 @@ RRL_API int rrl_logprob_fwd(const void* logits, int32_t logits_dtype, int64_t B,
                     void* logp_out, int32_t logp_dtype, void* lse_out,
                     int32_t* status, void* stream);
 
+/* rrl_logprob_fwd over the rows whose mask is nonzero: a row whose mask
+ * element (B x T view, any dtype; -0.0 counts as 0) is exactly 0 is not read
+ * and its logp and lse are written as 0.  For objectives in which such a
+ * token's log-prob enters only multiplied by its zero mask weight (GSPO's
+ * sequence log-ratio, losses.py:249-256, and its token form), the results are
+ * those of rrl_logprob_fwd for finite logits.  No reference counterpart. */
+RRL_API int rrl_logprob_fwd_masked(const void* logits, int32_t logits_dtype, int64_t B,
+                    int64_t T, int64_t V, int64_t ls_b, int64_t ls_t, rrl_view targets,
+                    rrl_view mask, void* logp_out, int32_t logp_dtype, void* lse_out,
+                    int32_t* status, void* stream);
+
 /* dlogits[b,t,v] (+)= g[b*T+t] * ([v == target] - exp(x[b,t,v] - lse[b*T+t])),
  * the composed gather_backward + log_softmax_backward (autograd of
  * losses.py:34-38).  g, lse and logp are contiguous acc-typed [B*T] (logp as

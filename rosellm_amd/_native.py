@@ -89,6 +89,7 @@ SIGNATURES = {
     "rrl_last_error": (ctypes.c_char_p, []),
     "rrl_abi_version": (ctypes.c_int, []),
     "rrl_logprob_fwd": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I64, _V, _P, _I32, _P, _P, _P]),
+    "rrl_logprob_fwd_masked": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I64, _V, _V, _P, _I32, _P, _P, _P]),
     "rrl_logprob_bwd": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I64, _V, _P, _P, _P, _P, _I32, _I64, _I64, _I32, _P]),
     "rrl_scale_rows": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _D, _P]),
     "rrl_policy_workspace_bytes": (ctypes.c_size_t, [_I64, _I32]),

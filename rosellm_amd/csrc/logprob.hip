@@ -45,11 +45,13 @@ __global__ __launch_bounds__(NT) void row_kernel(RowArgs a) {
     const int64_t tgt = load_index(a.tgt.ptr, a.tgt.dt, b * a.tgt.sr + t * a.tgt.sc);
     const bool tgt_ok = tgt >= 0 && tgt < a.V;
     const int64_t tgt_safe = tgt_ok ? tgt : 0;  // never address outside the row
+    // rrl_logprob_fwd_masked: a row whose mask is exactly 0 is never read.
+    const bool fwd_skip = MODE == MODE_FWD && a.mask.ptr != nullptr && !a.mask.truth(b, t);
     // A row without a valid target (NLL's ignored label; an out-of-range id,
     // which is flagged) takes xt = -inf: e_t = 0, so the log-sum-exp stays the
     // row's own and its gradient row is exact (zeros when g = 0); its log-prob
     // is set to NaN below.
-    const Acc xt = tgt_ok ? Tag::cvt(row[tgt_safe]) : -M<Acc>::inf();
+    const Acc xt = tgt_ok && !fwd_skip ? Tag::cvt(row[tgt_safe]) : -M<Acc>::inf();
 
     Acc lse, g, logp;
     bool have_logp = true;
@@ -59,6 +61,16 @@ __global__ __launch_bounds__(NT) void row_kernel(RowArgs a) {
       have_logp = a.logp_in != nullptr;
       logp = have_logp ? static_cast<const Acc*>(a.logp_in)[r] : Acc(0);
       if (threadIdx.x == 0 && !tgt_ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+    } else if (fwd_skip) {
+      // logp and lse written as 0; a target id outside [0, V) is still flagged.
+      lse = Acc(0);
+      logp = Acc(0);
+      g = Acc(0);
+      if (threadIdx.x == 0) {
+        if (!tgt_ok) raise_flag(a.status, RRL_FLAG_TARGET_RANGE);
+        store_as<Acc>(a.logp, a.logp_dt, r, logp);
+        static_cast<Acc*>(a.lse_out)[r] = lse;
+      }
     } else if (MODE == MODE_FUSED && (a.pp.flags & RRL_POLICY_SKIP_MASKED) &&
                weight_coef(mask_weight<Acc>(PolicyConsts<Acc>::make(a.pp), a.mask, b, t),
                            static_cast<const Acc*>(a.row_coef)[b]) == Acc(0)) {
@@ -205,6 +217,27 @@ extern "C" int rrl_logprob_fwd(const void* logits, int32_t logits_dtype, int64_t
   RowArgs a{};
   a.logits = logits; a.B = B; a.T = T; a.V = V; a.ls_b = ls_b; a.ls_t = ls_t;
   a.tgt = to_view(targets);
+  a.logp = logp_out; a.logp_dt = logp_dtype; a.lse_out = lse_out;
+  a.status = status;
+  return dispatch_row<MODE_FWD>(a, logits_dtype, as_stream(stream));
+}
+
+extern "C" int rrl_logprob_fwd_masked(const void* logits, int32_t logits_dtype, int64_t B,
+                                      int64_t T, int64_t V, int64_t ls_b, int64_t ls_t,
+                                      rrl_view targets, rrl_view mask, void* logp_out,
+                                      int32_t logp_dtype, void* lse_out, int32_t* status,
+                                      void* stream) {
+  clear_error();
+  int rc = validate_logits(logits, logits_dtype, B, T, V, targets);
+  if (rc) return rc;
+  RRL_REQUIRE(logp_dtype == RRL_F32 || logp_dtype == RRL_F64, RRL_EDTYPE,
+              "logp dtype must be float32 or float64");
+  RRL_REQUIRE(B * T == 0 || (logp_out && lse_out && mask.ptr), RRL_EINVAL,
+              "null pointer argument");
+  RowArgs a{};
+  a.logits = logits; a.B = B; a.T = T; a.V = V; a.ls_b = ls_b; a.ls_t = ls_t;
+  a.tgt = to_view(targets);
+  a.mask = to_view(mask);
   a.logp = logp_out; a.logp_dt = logp_dtype; a.lse_out = lse_out;
   a.status = status;
   return dispatch_row<MODE_FWD>(a, logits_dtype, as_stream(stream));

@@ -108,10 +108,16 @@ def _raise_target_range() -> None:
 
 
 class _TokenLogprobs(torch.autograd.Function):
-    """log_softmax(logits)[target] per row; backward writes dlogits in one sweep."""
+    """log_softmax(logits)[target] per row; backward writes dlogits in one sweep.
+
+    With ``skip_mask`` (same shape as the targets) a row whose mask is exactly
+    0 is not read: its log-prob and log-sum-exp are 0 (for objectives that
+    weight such a token's log-prob by its zero mask; its d loss / d logp is
+    then 0 and the backward writes its dlogits row as zeros unread)."""
 
     @staticmethod
-    def forward(ctx, logits: Tensor, target_ids: Tensor) -> Tensor:
+    def forward(ctx, logits: Tensor, target_ids: Tensor,
+                skip_mask: Optional[Tensor] = None) -> Tensor:
         dev = nat.require_device(logits, target_ids)
         x, B, T, V, s_b, s_t = nat.logits_rows(logits)
         tview, tkeep = nat.rows_view(target_ids, B, T)
@@ -119,11 +125,19 @@ class _TokenLogprobs(torch.autograd.Function):
         logp = torch.empty(B * T, dtype=acc, device=dev)
         lse = torch.empty(B * T, dtype=acc, device=dev)
         status = nat.new_status(dev)
-        nat.call(
-            "rrl_logprob_fwd", x.data_ptr(), nat.dtype_code(x.dtype), B, T, V, s_b, s_t, tview,
-            logp.data_ptr(), nat.dtype_code(acc), lse.data_ptr(), status.data_ptr(),
-            nat.stream_ptr(dev),
-        )
+        if skip_mask is None:
+            nat.call(
+                "rrl_logprob_fwd", x.data_ptr(), nat.dtype_code(x.dtype), B, T, V, s_b, s_t,
+                tview, logp.data_ptr(), nat.dtype_code(acc), lse.data_ptr(), status.data_ptr(),
+                nat.stream_ptr(dev),
+            )
+        else:
+            mview, _mkeep = nat.rows_view(skip_mask, B, T)
+            nat.call(
+                "rrl_logprob_fwd_masked", x.data_ptr(), nat.dtype_code(x.dtype), B, T, V, s_b,
+                s_t, tview, mview, logp.data_ptr(), nat.dtype_code(acc), lse.data_ptr(),
+                status.data_ptr(), nat.stream_ptr(dev),
+            )
         if B * T and nat.read_status(status) & nat.FLAG_TARGET_RANGE:
             _raise_target_range()
         # The backward forms the target column from logp (-g * expm1(logp)); a
@@ -136,7 +150,7 @@ class _TokenLogprobs(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad: Optional[Tensor]):
         if grad is None or not ctx.needs_input_grad[0]:
-            return None, None
+            return None, None, None
         x, tkeep, lse, logp = ctx.saved_tensors
         B, T, V, s_b, s_t, shape, dtype = ctx.meta
         g = grad.reshape(-1).to(lse.dtype).contiguous()
@@ -147,7 +161,7 @@ class _TokenLogprobs(torch.autograd.Function):
             lse.data_ptr(), logp.data_ptr(), g.data_ptr(), dl.data_ptr(), nat.dtype_code(dtype),
             T * V, V, 0, nat.stream_ptr(x.device),
         )
-        return dl, None
+        return dl, None, None
 
 
 def gather_token_logprobs(logits: Tensor, target_ids: Tensor) -> Tensor:
@@ -949,12 +963,13 @@ def fused_policy_loss(
     step; the logits are destroyed).  ``return_logprobs=True`` returns
     ``(output, logprobs)``.
 
-    ``skip_masked_rows=True`` (token-local objectives, without
-    ``return_logprobs``) never reads the logits of tokens whose mask weight is
-    exactly 0: their dlogits rows are written as zeros.  For finite logits the
-    loss and dlogits are bit-identical to the default; the one difference is
-    that a NaN/inf logit at a masked position no longer turns the loss into
-    NaN, as ``0 * NaN`` does in the reference's masked mean.
+    ``skip_masked_rows=True`` (without ``return_logprobs``) never reads the
+    logits of tokens whose mask weight is exactly 0: their dlogits rows are
+    written as zeros (GSPO: its forward sweep skips them and its backward
+    writes their zero-gradient rows unread).  For finite logits the loss and
+    dlogits are bit-identical to the default; the one difference is that a
+    NaN/inf logit at a masked position no longer turns the loss into NaN, as
+    ``0 * NaN`` does in the reference's masked mean.
     """
 
     if objective not in _OBJECTIVES:
@@ -973,10 +988,20 @@ def fused_policy_loss(
         raise ValueError("skip_masked_rows=True leaves masked log-probs uncomputed; "
                          "it cannot be combined with return_logprobs=True")
     if kind in (nat.OBJ_GSPO, nat.OBJ_GSPO_TOKEN):
-        if inplace or skip_masked_rows:
-            raise ValueError("inplace=True and skip_masked_rows=True apply to the single-sweep "
-                             "objectives only")
-        logp = gather_token_logprobs(logits, target_ids)
+        if inplace:
+            raise ValueError("inplace=True applies to the single-sweep objectives only")
+        # GSPO needs every token's log-prob before any gradient: a forward
+        # sweep, then the objective, then a backward sweep that reuses the
+        # forward's log-sum-exp and writes rows with a zero gradient unread.
+        # With skip_masked_rows the forward does not read tokens whose mask
+        # is 0: they enter the sequence log-ratio only times their zero mask.
+        if skip_masked_rows:
+            mask_dev = _on_device(action_mask, logits)
+            if mask_dev.shape != target_ids.shape:
+                mask_dev = mask_dev.expand(target_ids.shape)
+            logp = _TokenLogprobs.apply(logits, target_ids, mask_dev)
+        else:
+            logp = gather_token_logprobs(logits, target_ids)
         fn = gspo_policy_loss if kind == nat.OBJ_GSPO else gspo_token_policy_loss
         out = fn(logp, old_logprobs, advantages, action_mask, clip_low=clip_low,
                  clip_high=clip_low if clip_high is None else clip_high,

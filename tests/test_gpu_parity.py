@@ -802,6 +802,49 @@ def test_fused_skip_masked_rows_bit_identical(device, dtype, V, objective):
                             skip_masked_rows=True, return_logprobs=True, **kw)
 
 
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 151936), (torch.float32, 3001),
+                                     (torch.float16, 4099)])
+@pytest.mark.parametrize("objective", ["gspo", "gspo_token"])
+def test_gspo_skip_masked_rows_bit_identical(device, dtype, V, objective):
+    """GSPO's forward sweep with skip_masked_rows=True does not read masked
+    tokens (their log-probs enter the sequence log-ratio only times their zero
+    mask): loss, diagnostics and dlogits equal the default bit for bit, masked
+    dlogits rows are zero, and a NaN logit at a masked position no longer
+    reaches the loss (the default, like the reference's 0 * NaN, gives NaN)."""
+
+    print(f"[gspo-skip] objective={objective} dtype={dtype} V={V}", flush=True)
+    B, T = 16, 24
+    x, t, old, adv, mask = _fused_inputs(38, B, T, V, dtype)
+    a = adv[:, 0].contiguous() if objective == "gspo" else adv
+    kw = dict(clip_low=3e-4, clip_high=4e-4)
+    d = lambda z: z.to(device)  # noqa: E731
+    outs, grads = [], []
+    for skip in (False, True):
+        xd = d(x).requires_grad_()
+        out = R.fused_policy_loss(xd, d(t), d(old), d(a), d(mask), objective=objective,
+                                  skip_masked_rows=skip, **kw)
+        out.loss.backward()
+        outs.append(out)
+        grads.append(xd.grad)
+    fields = [f for f in ("loss", "objective", "sequence_ratio_divergence",
+                          "sequence_clip_fraction", "mean_sequence_ratio", "sequence_ratios",
+                          "approximate_kl", "mean_ratio") if hasattr(outs[0], f)]
+    assert fields
+    for f in fields:
+        assert torch.equal(getattr(outs[0], f), getattr(outs[1], f)), f
+    assert torch.equal(grads[0], grads[1])
+    assert torch.count_nonzero(grads[1][~d(mask)]).item() == 0
+    # a NaN logit at a masked token: read (and propagated) only by the default
+    xn = x.clone()
+    b, tt = torch.nonzero(~mask)[0].tolist()
+    xn[b, tt, 0] = float("nan")
+    ln = R.fused_policy_loss(d(xn), d(t), d(old), d(a), d(mask), objective=objective,
+                             skip_masked_rows=True, **kw).loss
+    assert torch.equal(ln, outs[1].loss)
+    l0 = R.fused_policy_loss(d(xn), d(t), d(old), d(a), d(mask), objective=objective, **kw).loss
+    assert torch.isnan(l0)
+
+
 @pytest.mark.parametrize(
     "dtype,V,B,T",
     [
