@@ -2,3 +2,5 @@
 path.  ``rosellm_amd.roserlhf`` is the drop-in for ``rosellm.roserlhf``."""
 
 __version__ = "0.1.0"
+
+from ._config import reference_dtypes, set_reference_dtypes  # noqa: E402,F401

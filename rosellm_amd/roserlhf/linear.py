@@ -35,6 +35,7 @@ import torch
 from torch import Tensor
 
 from .. import _native as nat
+from .. import _config as _cfg
 from . import losses as L
 
 __all__ = ["fused_linear_policy_loss", "linear_token_logprobs"]
@@ -222,7 +223,8 @@ def linear_token_logprobs(hidden: Tensor, weight: Tensor, target_ids: Tensor, *,
 
     if row_block < 1:
         raise ValueError("row_block must be positive")
-    return _LinearLogprobs.apply(L._params(nat.OBJ_PPO), hidden, weight, target_ids)
+    return _cfg.as_reference_dtype(
+        _LinearLogprobs.apply(L._params(nat.OBJ_PPO), hidden, weight, target_ids), hidden)
 
 
 def linear_label_logprobs(hidden: Tensor, weight: Tensor, labels: Tensor,
@@ -291,7 +293,7 @@ def fused_linear_policy_loss(
         out = fn(logp, old_logprobs, advantages, action_mask, clip_low=clip_low,
                  clip_high=clip_low if clip_high is None else clip_high,
                  max_log_ratio=max_log_ratio)
-        return (out, logp.detach()) if return_logprobs else out
+        return (out, _cfg.as_reference_dtype(logp.detach(), hidden)) if return_logprobs else out
 
     p = L._token_local_params(kind, hidden.shape[:-1], old_logprobs, advantages, action_mask,
                               clip_low=clip_low, clip_high=clip_high,
@@ -300,4 +302,4 @@ def fused_linear_policy_loss(
     logp = _LinearLogprobs.apply(ppo, hidden, weight, target_ids, mask)
     obj, d1, d2, d3, _seq, trusted = L._objective(p, logp, old_logprobs, advantages, mask)
     out = L._token_local_output(kind, obj, d1, d2, d3, trusted)
-    return (out, logp.detach()) if return_logprobs else out
+    return (out, _cfg.as_reference_dtype(logp.detach(), hidden)) if return_logprobs else out

@@ -25,6 +25,7 @@ import torch
 from torch import Tensor
 
 from .. import _native as nat
+from .. import _config as _cfg
 
 __all__ = [
     "GspoPolicyLossOutput",
@@ -184,7 +185,7 @@ def gather_token_logprobs(logits: Tensor, target_ids: Tensor) -> Tensor:
         )
     if target_ids.dtype not in (torch.int32, torch.int64):
         raise TypeError("target_ids must be an integer tensor")
-    return _TokenLogprobs.apply(logits, target_ids)
+    return _cfg.as_reference_dtype(_TokenLogprobs.apply(logits, target_ids), logits)
 
 
 # ---------------------------------------------------------------------------
@@ -1006,7 +1007,7 @@ def fused_policy_loss(
         out = fn(logp, old_logprobs, advantages, action_mask, clip_low=clip_low,
                  clip_high=clip_low if clip_high is None else clip_high,
                  max_log_ratio=max_log_ratio)
-        return (out, logp.detach()) if return_logprobs else out
+        return (out, _cfg.as_reference_dtype(logp.detach(), logits)) if return_logprobs else out
 
     p = _token_local_params(kind, logits.shape[:-1], old_logprobs, advantages, action_mask,
                             clip_low=clip_low, clip_high=clip_high,
@@ -1018,5 +1019,5 @@ def fused_policy_loss(
     obj, d1, d2, d3, logp, trusted = _FusedPolicy.apply(p, bool(inplace), logits, target_ids,
                                                         old_logprobs, advantages, mask)
     out = _token_local_output(kind, obj, d1, d2, d3, trusted)
-    return (out, logp) if return_logprobs else out
+    return (out, _cfg.as_reference_dtype(logp, logits)) if return_logprobs else out
 

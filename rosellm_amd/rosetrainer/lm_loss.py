@@ -32,6 +32,7 @@ import torch
 from torch import Tensor
 
 from .. import _native as nat
+from .. import _config as _cfg
 from ..roserlhf import linear as _linear
 from ..roserlhf import losses as _losses
 
@@ -196,7 +197,8 @@ def cross_entropy(input: Tensor, target: Tensor, *, ignore_index: int = -100,
         raise ValueError(
             f"Expected input batch_size ({n_in}) to match target batch_size ({target.numel()}).")
     p = _nll_params(ignore_index, reduction)
-    return _CrossEntropyRows.apply(p, bool(inplace), False, input, target)
+    return _cfg.as_reference_dtype(
+        _CrossEntropyRows.apply(p, bool(inplace), False, input, target), input)
 
 
 def causal_lm_loss(logits: Tensor, labels: Tensor, *, ignore_index: int = -100,
@@ -215,7 +217,8 @@ def causal_lm_loss(logits: Tensor, labels: Tensor, *, ignore_index: int = -100,
         raise ValueError(
             f"labels shape {tuple(labels.shape)} must match logits prefix {tuple(logits.shape[:2])}")
     p = _nll_params(ignore_index, reduction)
-    return _CrossEntropyRows.apply(p, bool(inplace), True, logits, labels)
+    return _cfg.as_reference_dtype(
+        _CrossEntropyRows.apply(p, bool(inplace), True, logits, labels), logits)
 
 
 def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, target: Tensor, *,
@@ -241,7 +244,7 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, target: Tensor, *
     logp = _linear.linear_label_logprobs(hidden, weight, target, ignore_index)
     unused = torch.zeros((), dtype=torch.float32, device=dev).expand(target.shape)
     obj = _losses._objective(p, logp, unused, unused, target)[0]
-    return -obj
+    return _cfg.as_reference_dtype(-obj, hidden)
 
 
 def linear_causal_lm_loss(hidden: Tensor, weight: Tensor, labels: Tensor, *,

@@ -80,8 +80,25 @@ def _field(out: Any, name: str):
     return getattr(out, name)
 
 
-def run_case(case: Dict[str, Any], backend: str, device) -> None:
-    fns = _oracle_fns() if backend == "oracle" else _hip_fns()
+def shim_fns(R, L):
+    """The same functions taken from a ``rosellm.roserlhf`` package (the
+    opt-in shim) and its ``losses`` module."""
+
+    names = [
+        "gather_token_logprobs", "clipped_policy_loss", "direct_double_sided_mask",
+        "sao_policy_loss", "gspo_policy_loss", "gspo_token_policy_loss", "sapo_policy_loss",
+        "discounted_returns", "generalized_advantage_estimation", "leave_one_out_advantages",
+        "group_standardized_advantages", "broadcast_turn_advantages",
+        "skip_observation_generalized_advantage_estimation",
+    ]
+    fns = {n: getattr(R, n) for n in names}
+    fns["sequence_log_ratio"] = L.sequence_log_ratio
+    return fns
+
+
+def run_case(case: Dict[str, Any], backend: str, device, fns=None) -> None:
+    if fns is None:
+        fns = _oracle_fns() if backend == "oracle" else _hip_fns()
     fn = fns[case["fn"]]
     dtype = getattr(torch, case["dtype"])
     args = {k: _tensor(v, dtype, device) for k, v in case["args"].items()}
