@@ -6,8 +6,9 @@
 // One workgroup owns one sequence; each lane owns a contiguous chunk of time
 // steps:
 //   1. every lane composes the affine map of its chunk (reverse time);
-//   2. lane 0 pushes the initial state through the chunk maps from the last
-//      chunk to the first, leaving each chunk's incoming state in LDS;
+//   2. a log-depth suffix scan of the chunk maps over the lanes (8 steps
+//      through LDS for 256 lanes) gives each lane the composition of every
+//      later chunk, hence its chunk's incoming state;
 //   3. every lane replays its chunk with the reference's step arithmetic from
 //      its incoming state and writes the outputs.
 #include "rrl_common.hpp"
@@ -139,7 +140,6 @@ template <typename Acc, int KIND>
 __global__ __launch_bounds__(SCAN_NT) void reverse_scan_kernel(ScanArgs a) {
   constexpr int D = StateDim<KIND>::D;
   __shared__ Aff<Acc, D> sh_map[SCAN_NT];
-  __shared__ Acc sh_in[SCAN_NT][D];
   // gamma and gamma*lambda as the reference forms them: python float products
   // rounded to the tensor dtype.
   const Acc g = (Acc)a.gamma;
@@ -150,23 +150,31 @@ __global__ __launch_bounds__(SCAN_NT) void reverse_scan_kernel(ScanArgs a) {
     const int64_t t1 = (t0 + C < a.T) ? t0 + C : a.T;
     Aff<Acc, D> f = Aff<Acc, D>::identity();
     for (int64_t t = t1 - 1; t >= t0; --t) f.prepend(step_map<Acc, KIND>(a, b, t, g, gl));
+    // Log-depth inclusive suffix scan of the chunk maps (Kogge-Stone over
+    // the lanes, through LDS): after the step of distance d, lane j holds
+    // P_j = f_j o f_(j+1) o ... o f_(j+2d-1) (the later chunks applied first),
+    // and after the last step P_j runs through every chunk from the
+    // sequence's end down to chunk j.
     sh_map[threadIdx.x] = f;
     __syncthreads();
-    if (threadIdx.x == 0) {
-      Acc S[D];
-      if (KIND == 0) S[0] = a.boot.present() ? a.boot.get<Acc>(b, 0) : Acc(0);
-      if (KIND == 1) { S[0] = a.boot.present() ? a.boot.get<Acc>(b, 0) : Acc(0); S[1] = Acc(0); }
-      if (KIND == 2) S[0] = Acc(0);
-      for (int j = SCAN_NT - 1; j >= 0; --j) {
-#pragma unroll
-        for (int i = 0; i < D; ++i) sh_in[j][i] = S[i];
-        sh_map[j].apply(S);
+    for (int d = 1; d < SCAN_NT; d <<= 1) {
+      const bool has = threadIdx.x + d < SCAN_NT;
+      Aff<Acc, D> later;
+      if (has) later = sh_map[threadIdx.x + d];
+      __syncthreads();
+      if (has) {
+        later.prepend(f);  // `later` first, then this lane's map
+        f = later;
       }
+      sh_map[threadIdx.x] = f;
+      __syncthreads();
     }
-    __syncthreads();
+    // Chunk j's incoming state: the initial state through P_(j+1).
     Acc S[D];
-#pragma unroll
-    for (int i = 0; i < D; ++i) S[i] = sh_in[threadIdx.x][i];
+    if (KIND == 0) S[0] = a.boot.present() ? a.boot.get<Acc>(b, 0) : Acc(0);
+    if (KIND == 1) { S[0] = a.boot.present() ? a.boot.get<Acc>(b, 0) : Acc(0); S[1] = Acc(0); }
+    if (KIND == 2) S[0] = Acc(0);
+    if (threadIdx.x + 1 < SCAN_NT) sh_map[threadIdx.x + 1].apply(S);
     for (int64_t t = t1 - 1; t >= t0; --t) {
       Acc o0, o1;
       ref_step<Acc, KIND>(a, b, t, g, gl, S, o0, o1);
