@@ -137,7 +137,8 @@ def parse_args():
                    help="time the headline configuration and its own variants, not the other "
                         "configurations")
     p.add_argument("--calibrate-copy", action="store_true",
-                   help="also launch one device copy of known size (HBM counter calibration)")
+                   help="after the headline, launch two conversions of known traffic (HBM counter "
+                        "calibration)")
     p.add_argument("--seed", type=int, default=1234)
     return p.parse_args()
 
@@ -739,20 +740,6 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
         log(f"[bench] skip_masked_rows: {v_el * 1e3 / steps:.3f} ms/step, "
             f"{N / (v_el / steps) / 1e6:.3f} M tok/s, kernel {v_k:.3f} ms")
 
-    if args.calibrate_copy:
-        # Calibration kernel of known traffic for the HBM counters: a bf16 ->
-        # float32 conversion of 2^30 random elements reads 2 GiB and writes
-        # 4 GiB (a same-dtype copy would run as a DMA blit, invisible to the
-        # counters; constant data can compress in the memory fabric).
-        src = torch.randn(1 << 30, dtype=torch.bfloat16, device=device)
-        dst = torch.empty(1 << 30, dtype=torch.float32, device=device)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"[bench] calibration conversion: {src.numel() * 2} B read, "
-            f"{dst.numel() * 4} B written")
-        del src, dst
-
     cpu = None
     if with_cpu:
         if prepare is not None:
@@ -943,6 +930,29 @@ def default_steps(name, args):
     return args.steps or 10, args.warmup if args.warmup is not None else 2
 
 
+def calibration_conversions(device, reps=2):
+    """Kernels of known traffic for the HBM counters: ``reps`` bf16 -> float32
+    conversions of 2^29 random elements, each one dispatch that reads exactly
+    1 GiB and writes exactly 2 GiB.  2^29 is the largest count that torch
+    converts in one launch (the float32 output's largest byte offset,
+    2^31 - 4, still fits its 32-bit indexing; 2^30 elements would run as two
+    launches of 2^29).  A same-dtype copy would run as a DMA blit, invisible
+    to the counters, and constant data could compress in the memory fabric."""
+
+    import torch
+
+    n = 1 << 29
+    src = torch.randn(n, dtype=torch.bfloat16, device=device)
+    dst = torch.empty(n, dtype=torch.float32, device=device)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] calibration: {reps} conversions, each {n * 2} B read and {n * 4} B "
+        "written in one launch")
+    del src, dst
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -968,6 +978,8 @@ def main():
                                 skip_masked_variant=not args.no_variants)
     gc.collect()
     torch.cuda.empty_cache()
+    if args.calibrate_copy:
+        calibration_conversions(device)
     if not (args.no_variants or args.headline_only):
         variants = result.setdefault("variants", {})
         for name in VARIANTS:
