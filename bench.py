@@ -991,7 +991,9 @@ def main():
                 if name == "sample":
                     r = bench_sample(args, v_steps, v_warm, not args.skip_cpu)
                 else:
-                    r = measure_config(name, args, device, v_steps, v_warm, not args.skip_cpu)
+                    # C3's two objectives also time their skip_masked_rows entry
+                    r = measure_config(name, args, device, v_steps, v_warm, not args.skip_cpu,
+                                       skip_masked_variant=name in ("c3", "c3_gspo_token"))
                 variants[name] = compact(r)
             except Exception as e:  # recorded, never fatal to the headline
                 variants[name] = {"error": f"{type(e).__name__}: {e}"[:400]}

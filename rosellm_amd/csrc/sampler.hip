@@ -309,6 +309,19 @@ __device__ __forceinline__ void argmax_merge(float& bx, int& bi, float ox, int o
   }
 }
 
+// Minimum of v over the workgroup (every thread takes part; the result is
+// the same in every thread).
+__device__ __forceinline__ int block_min_i32(int v) {
+  __shared__ int sh_min[SWAVES];
+  v = wave_min_dpp(v);
+  if ((threadIdx.x & 63) == 0) sh_min[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int m = sh_min[0];
+  for (int w = 1; w < SWAVES; ++w) m = min(m, sh_min[w]);
+  __syncthreads();
+  return m;
+}
+
 // First element, in vocabulary order, whose inclusive prefix of the weights
 // exceeds target(total of the weights).  wfn(e, bits) >= 0 must be a pure
 // function of its arguments (it is evaluated twice per element).  Each lane
@@ -643,9 +656,24 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   const bool row_bad = bx == -__builtin_huge_valf() || bi >= V || os != os ||
                        __builtin_fabsf(bx * iT) == __builtin_huge_valf();
   if (row_bad) {
+    int tok_bad = bi < V ? bi : 0;
+    if (a.greedy && os != os) {
+      // Greedy decoding is torch.argmax, which ranks NaN above every number:
+      // the row's first NaN is its token.
+      int fn = 0x7fffffff;
+      for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
+#pragma unroll
+        for (int i = VEC - 1; i >= 0; --i) {
+          const float v = Bits<Tag>::val(u[i]);
+          if ((full || e0 + i < V) && v != v) fn = min(fn, e0 + i);
+        }
+      });
+      fn = block_min_i32(fn);
+      if (fn < V) tok_bad = fn;
+    }
     if (tid == 0) {
       raise_flag(a.status, RRL_FLAG_BAD_PROBS);
-      a.token[r] = bi < V ? bi : 0;
+      a.token[r] = tok_bad;
       a.logp[r] = __builtin_nanf("");
       if (a.logq) a.logq[r] = __builtin_nanf("");
     }
@@ -1120,9 +1148,27 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
     bi = sh_m[w] == M ? min(bi, sh_i[w]) : bi;
   }
   if (M == NEG || Z != Z || __builtin_fabsf(M * iT) == __builtin_huge_valf() || bi >= V) {
+    int tok_bad = bi < V ? bi : 0;
+    if (a.greedy && Z != Z) {
+      // Greedy decoding is torch.argmax, which ranks NaN above every number:
+      // the row's first NaN is its token (entries past the row hold -inf).
+      int fn = 0x7fffffff;
+#pragma unroll
+      for (int k = SL - 1; k >= 0; --k) {
+        if (k < nslab) {
+          float v[8];
+          unpack8<Tag>(x[k], v);
+#pragma unroll
+          for (int i = 7; i >= 0; --i)
+            if (v[i] != v[i]) fn = (k * SNT + tid) * 8 + i;
+        }
+      }
+      fn = block_min_i32(fn);
+      if (fn < V) tok_bad = fn;
+    }
     if (tid == 0) {
       raise_flag(a.status, RRL_FLAG_BAD_PROBS);
-      a.token[r] = bi < V ? bi : 0;
+      a.token[r] = tok_bad;
       a.logp[r] = __builtin_nanf("");
       if (a.logq) a.logq[r] = __builtin_nanf("");
     }

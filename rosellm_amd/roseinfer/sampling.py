@@ -23,8 +23,9 @@ device) and returns, with it,
 The distribution is the reference's on the float32 upcast of the logits (the
 reference divides by T and normalises in the logits dtype); ties at a top-k or
 top-p threshold are kept lowest index first (torch.topk leaves their order
-unspecified).  Rows with NaN or +inf logits raise, as ``torch.multinomial``
-does.
+unspecified).  When sampling, rows with NaN or +inf logits raise, as
+``torch.multinomial`` does; greedy decoding returns ``torch.argmax``'s token
+for them (the first NaN, else the first maximum) with a NaN log-prob.
 """
 
 from __future__ import annotations
@@ -95,8 +96,13 @@ def sample_next_token_batch(
              x.stride(0) if B > 1 else V, float(temperature), int(top_k), float(top_p),
              int(bool(do_sample)), int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 64 - 1),
              tokens.data_ptr(), logp.data_ptr(), logq.data_ptr(), None, nat.stream_ptr(dev))
-    # NaN anywhere makes the sum NaN (the log-probs are never +inf).
-    if B and bool(np.isnan(logp.cpu().numpy().sum())):
+    # Sampling raises on such rows, as torch.multinomial does; NaN anywhere
+    # makes the sum NaN (the log-probs are never +inf).  Greedy decoding is
+    # torch.argmax in the reference (engine.py:1117-1118), which never raises:
+    # its bad rows keep their argmax token (NaN ranking above every number)
+    # and a NaN log-prob, and the call makes no host synchronisation.
+    greedy = (not do_sample) or temperature <= 0.0
+    if B and not greedy and bool(np.isnan(logp.cpu().numpy().sum())):
         raise RuntimeError("probability tensor contains either `inf`, `nan` or element < 0")
     return SampleOutput(tokens, logp, logq)
 

@@ -233,18 +233,35 @@ def test_resident_draws_follow_the_distribution(device):
     assert chi2 < dof + 6 * np.sqrt(2 * dof), (chi2, dof)
 
 
-@pytest.mark.parametrize("bad", ["nan", "inf", "all_neg_inf"])
-def test_resident_bad_rows(device, bad):
-    x = torch.randn(4, 4096, device=device).to(torch.bfloat16)
+@pytest.mark.parametrize("bad", ["nan", "nan_after_inf", "inf", "all_neg_inf"])
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 4096), (torch.float32, 4099)])
+def test_bad_rows_sampling_raises_greedy_is_argmax(device, bad, dtype, V):
+    """Sampling raises on a row with NaN / +inf / no finite logit, as
+    torch.multinomial does; greedy decoding is torch.argmax in the reference
+    (engine.py:1117-1118), which never raises: the bad row keeps argmax's token
+    (the first NaN, else the first maximum) and gets a NaN log-prob.  bf16 rows
+    of whole vectors take the register-resident kernel, V = 4099 float32 rows
+    the streaming one."""
+
+    x = torch.randn(4, V, device=device).to(dtype)
     if bad == "nan":
         x[2, 4000] = float("nan")
+        x[2, 4001] = float("nan")
+    elif bad == "nan_after_inf":
+        x[2, 9] = float("inf")
+        x[2, 3000] = float("nan")
     elif bad == "inf":
         x[2, 7] = float("inf")
+        x[2, 70] = float("inf")
     else:
         x[2] = -float("inf")
-    for do_sample in (True, False):
-        with pytest.raises(RuntimeError, match="inf"):
-            RI.sample_next_token_batch(x, 1.0, 0, 1.0, do_sample, seed=1)
+    with pytest.raises(RuntimeError, match="inf"):
+        RI.sample_next_token_batch(x, 1.0, 0, 1.0, True, seed=1)
+    for temperature, do_sample in ((1.0, False), (0.0, True)):
+        out = RI.sample_next_token_batch(x, temperature, 0, 1.0, do_sample, seed=1)
+        assert torch.equal(out.token_ids.cpu(), torch.argmax(x.cpu(), dim=-1))
+        lp = out.logprobs.cpu()
+        assert torch.isnan(lp[2]) and torch.isfinite(lp[[0, 1, 3]]).all()
     # the other rows of a call are unaffected when run alone
     ok = RI.sample_next_token_batch(x[:2], 1.0, 0, 1.0, False)
     assert torch.equal(ok.token_ids.cpu(), torch.argmax(x[:2].float(), dim=-1).cpu())
@@ -276,6 +293,8 @@ def test_bad_rows_through_the_c_abi(device, dtype):
         assert torch.equal(bad, want_bad), (temperature, bad)
         assert bool(flagged)
         assert torch.isnan(lq.cpu()[want_bad]).all() and torch.isfinite(lp.cpu()[~want_bad]).all()
+        if not do_sample:
+            assert torch.equal(tok.cpu(), torch.argmax(x.cpu(), dim=-1))
 
 
 @pytest.mark.parametrize("dtype,misaligned", [(torch.bfloat16, False), (torch.bfloat16, True),
