@@ -825,6 +825,8 @@ def lm_head_roofline(inp, cfg, kstats, ms_step):
 
 SAMPLE_ROWS = 256
 SAMPLE_VARIANTS = {"default": dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=True),
+                   "default_without_log_q": dict(temperature=1.0, top_k=0, top_p=1.0,
+                                                 do_sample=True, sampling_logprobs=False),
                    "topk50_topp0.9_T0.7": dict(temperature=0.7, top_k=50, top_p=0.9,
                                                do_sample=True),
                    "greedy": dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=False)}
@@ -846,6 +848,39 @@ def bench_sample(args, steps, warmup, with_cpu):
     hot = torch.randint(0, V, (B,), device=device, generator=g)
     rows = torch.arange(0, B, 20, device=device)
     x[rows, hot[rows]] = (x[rows, hot[rows]].float() + 15.0).to(torch.bfloat16)
+    from rosellm_amd import _native as nat
+
+    def kernel_ms(kw):
+        """Mean duration of `steps` launches of the entry point with the
+        arguments the API passes, back to back on the stream.  The API call
+        ends in a host synchronisation (its bad-row check), so an event pair
+        around it would also count the launch's own submission gap on an idle
+        GPU: several microseconds on a kernel of twenty."""
+
+        tok = torch.empty(B, dtype=torch.int64, device=device)
+        lp = torch.empty(B, dtype=torch.float32, device=device)
+        lq = torch.empty(B, dtype=torch.float32, device=device)
+        want_q = kw.get("sampling_logprobs", True)
+        greedy = not kw["do_sample"] or kw["temperature"] <= 0.0
+
+        def launch(off):
+            nat.call("rrl_sample_logprobs", x.data_ptr(), nat.dtype_code(x.dtype), B, V,
+                     x.stride(0), float(kw["temperature"]), int(kw["top_k"]),
+                     float(kw["top_p"]), int(not greedy), args.seed, off, tok.data_ptr(),
+                     lp.data_ptr(), lq.data_ptr() if want_q else None, None,
+                     nat.stream_ptr(device))
+
+        for i in range(warmup):
+            launch(i)
+        torch.cuda.synchronize()
+        timed = nat.time_calls("rrl_sample_logprobs", capacity=steps)
+        for i in range(steps):
+            launch(100 + i)
+        torch.cuda.synchronize()
+        nat.time_calls()
+        kms = [s.elapsed_time(e) for s, e in timed["rrl_sample_logprobs"]]
+        return sum(kms) / len(kms)
+
     results = {}
     for name, kw in SAMPLE_VARIANTS.items():
         for i in range(warmup):
@@ -853,8 +888,8 @@ def bench_sample(args, steps, warmup, with_cpu):
         offs = iter(range(100, 100 + 2 * steps))
         res = timed_steps(lambda: sample_next_token_batch(x, seed=args.seed, offset=next(offs),
                                                           **kw),
-                          steps, ["rrl_sample_logprobs"])
-        kms = [s.elapsed_time(e) for s, e in res["launches"]["rrl_sample_logprobs"]]
+                          steps, [])
+        kms = [kernel_ms(kw)]
         ms = res["wall_s"] * 1e3 / steps
         results[name] = dict(ms=ms, median=statistics.median(res["step_ms"]),
                              kernel_ms=sum(kms) / len(kms))

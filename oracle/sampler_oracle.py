@@ -11,14 +11,23 @@ its PyTorch path) on the float64 upcast of the logits:
   kept iff its inclusive cumulative p is <= top_p, the first always (the
   reference's ``mask = cum_probs > top_p; mask[..., 0] = False``);
 * q = max(p * kept, 1e-9) on the candidates (``masked_fill`` then
-  ``clamp_min(1e-9)``), 0 elsewhere; the token is the first index, in
-  vocabulary order, whose inclusive cumulative q exceeds u * sum(q).
+  ``clamp_min(1e-9)``), 0 elsewhere; with top-k or top-p active the token is
+  the first index, in vocabulary order, whose inclusive cumulative q exceeds
+  u * sum(q);
+* without top-k and top-p (the reference's ``softmax(...).clamp_min(1e-9)``
+  branch) q = p + g with g = max(1e-9 - p, 0) is drawn as a mixture: the
+  floor's excess g when u1 < G / (S + G) (S = sum p = 1, G = sum g), else p;
+  the token is the first index whose inclusive cumulative weight of that
+  component exceeds u times the component's total.  Both rules sample q / sum q
+  exactly: (S / (S + G)) p / S + (G / (S + G)) g / G = q / (S + G).
 
-The uniform of row r is Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC 2011)
-of counter (r, r >> 32, offset, offset >> 32) and key (seed, seed >> 32):
-u = (first word >> 8) * 2^-24.  ``philox4x32_10`` is pinned by the known-answer
-vectors published with the Random123 library; the distribution by a direct
-restatement of the reference's torch op chain (tests/test_oracle_sampler.py).
+The uniforms of row r come from Philox4x32-10 (Salmon, Moraes, Dror, Shaw,
+SC 2011) of counter (r, r >> 32, offset, offset >> 32) and key
+(seed, seed >> 32), words w0..w3: u = (w0 >> 8) * 2^-24 and
+u1 = ((w1 << 21) | (w2 >> 11)) * 2^-53.  ``philox4x32_10`` is pinned by the
+known-answer vectors published with the Random123 library; the distribution
+by a direct restatement of the reference's torch op chain and the mixture
+identity (tests/test_oracle_sampler.py).
 """
 
 from __future__ import annotations
@@ -49,10 +58,51 @@ def philox4x32_10(ctr, key) -> Tuple[int, int, int, int]:
     return c0, c1, c2, c3
 
 
-def row_uniform(seed: int, offset: int, row: int) -> float:
+def row_uniforms(seed: int, offset: int, row: int) -> Tuple[float, float]:
+    """(u, u1) of row r: the position uniform (24 bits) and the component
+    uniform (53 bits)."""
+
     w = philox4x32_10((row & M32, (row >> 32) & M32, offset & M32, (offset >> 32) & M32),
                       (seed & M32, (seed >> 32) & M32))
-    return (w[0] >> 8) * 2.0 ** -24
+    return (w[0] >> 8) * 2.0 ** -24, (((w[1] << 21) | (w[2] >> 11)) & ((1 << 53) - 1)) * 2.0 ** -53
+
+
+def row_uniform(seed: int, offset: int, row: int) -> float:
+    return row_uniforms(seed, offset, row)[0]
+
+
+def mixture_parts(p: np.ndarray) -> Tuple[np.ndarray, np.ndarray, float]:
+    """(p, g = max(1e-9 - p, 0), pi = G / (S + G)) of a full softmax p: the
+    two components of max(p, 1e-9) and the probability of the floor's."""
+
+    g = np.maximum(1e-9 - p, 0.0)
+    S, G = float(p.sum()), float(g.sum())
+    return p, g, (G / (S + G) if G > 0.0 else 0.0)
+
+
+def inverse_cdf(w: np.ndarray, u: float) -> Tuple[int, float]:
+    """(first index whose inclusive cumulative w exceeds u * sum(w), the
+    distance of u * sum(w) to the nearest boundary relative to sum(w));
+    rounding past the end takes the last positive entry."""
+
+    cdf = np.cumsum(w)
+    total = cdf[-1]
+    tgt = u * total
+    tok = int(np.searchsorted(cdf, tgt, side="right"))
+    if tok >= w.size:
+        tok = int(np.nonzero(w > 0)[0][-1])
+    lo = cdf[tok - 1] if tok > 0 else 0.0
+    return tok, min(tgt - lo, cdf[tok] - tgt) / total
+
+
+def mixture_draw(p: np.ndarray, u: float, u1: float) -> Tuple[int, float]:
+    """(token, margin) of the mixture rule; the margin is the smaller of the
+    position margin inside the chosen component and |u1 - pi| / pi."""
+
+    rho, g, pi = mixture_parts(p)
+    tok, pos = inverse_cdf(g if u1 < pi else rho, u)
+    comp = abs(u1 - pi) / pi if pi > 0.0 else math.inf
+    return tok, min(pos, comp)
 
 
 def _descending(x: np.ndarray) -> np.ndarray:
@@ -92,7 +142,8 @@ def sample_rows(logits: np.ndarray, *, temperature: float, top_k: int, top_p: fl
                 do_sample: bool, seed: int, offset: int) -> Dict[str, np.ndarray]:
     """Per row: token, logp = log_softmax(x/T)[token] (T = 1 when greedy),
     logq = log(q[token]/sum q) (0 when greedy), and margin = the distance of
-    u*sum(q) to the nearest cumulative boundary relative to sum(q) (decisions
+    the draw's target to the nearest cumulative boundary relative to the
+    total drawn over, or of u1 to the mixture's pi relative to pi (decisions
     closer than float32 rounding can go either way)."""
 
     x = np.asarray(logits, dtype=np.float64)
@@ -108,14 +159,15 @@ def sample_rows(logits: np.ndarray, *, temperature: float, top_k: int, top_p: fl
             out["margin"][r] = math.inf
         else:
             q, _ = sampling_distribution(row, T, top_k, top_p)
-            cdf = np.cumsum(q)
-            total = cdf[-1]
-            tgt = row_uniform(seed, offset, r) * total
-            tok = int(np.searchsorted(cdf, tgt, side="right"))
-            tok = min(tok, V - 1)
-            lo = cdf[tok - 1] if tok > 0 else 0.0
-            out["margin"][r] = min(tgt - lo, cdf[tok] - tgt) / total
-            out["logq"][r] = math.log(q[tok] / total)
+            u, u1 = row_uniforms(seed, offset, r)
+            if 0 < top_k < V or 0.0 < top_p < 1.0:
+                tok, margin = inverse_cdf(q, u)
+            else:
+                s = row / T
+                e = np.exp(s - s.max())
+                tok, margin = mixture_draw(e / e.sum(), u, u1)
+            out["margin"][r] = margin
+            out["logq"][r] = math.log(q[tok] / q.sum())
         s = row / T
         mx = s.max()
         out["logp"][r] = s[tok] - (mx + math.log(np.exp(s - mx).sum()))

@@ -911,13 +911,41 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
         if (tid == 0) logq = (float)(log((double)wfn(tok, load_one<Tag>(row, tok))) - log(qtot));
       };
       if (!use_k && !p_found) {
-        // The floored softmax itself: q = max(exp((x - max) / T) / Z, 1e-9) on
-        // every entry, one hardware exponential per entry.
-        draw(
+        // The floored softmax max(p, 1e-9) as sample_resident_kernel's
+        // mixture: p with probability 1 / (1 + G), else the floor's excess
+        // g = max(1e-9 - p, 0), chosen by the component uniform u1; G takes
+        // a pass of its own only when u1 < V * 1e-9 (>= G / (1 + G)) or
+        // log q is asked for.
+        const float lz = log2f(zs);
+        auto rho_of = [&](uint32_t b) {
+          return exp2_hw(__builtin_fmaf(Bits<Tag>::val(b) - bx, c2, -lz));
+        };
+        const double u1 = (double)(((uint64_t)c[1] << 21) | (c[2] >> 11)) * 0x1p-53;
+        const bool near = u1 < (double)V * 1.001e-9;
+        double G = 0.0;
+        if (a.logq || near) {
+          float gs = 0.0f;
+          for_slabs<Tag>(row, V, al16, nslab, [&](int, int e0, const uint32_t (&u)[VEC], auto full) {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i)
+              if (full || e0 + i < V) gs += fmaxf(1e-9f - rho_of(u[i]), 0.0f);
+          });
+          double t[1] = {(double)gs};
+          block_sum<SNT, 1, double>(t, sh.wave_tot);
+          G = t[0];
+        }
+        const bool use_g = near && u1 < G / (1.0 + G);
+        tok = vocab_search<Tag, false>(
+            row, V, al16, nslab,
             [&](int, uint32_t b) {
-              return fmaxf(exp2_hw((Bits<Tag>::val(b) - bx) * c2) * inv_z, 1e-9f);
+              const float p = rho_of(b);
+              return use_g ? fmaxf(1e-9f - p, 0.0f) : p;
             },
-            std::true_type{});
+            target, sh);
+        __syncthreads();
+        if (tok < 0 || tok >= V) tok = bi;  // no positive weight: cannot happen with p
+        if (tid == 0 && a.logq)
+          logq = (float)(log((double)fmaxf(rho_of(load_one<Tag>(row, tok)), 1e-9f)) - log1p(G));
       } else {
         draw(qw, std::false_type{});
       }
@@ -949,24 +977,20 @@ int launch_sample(const SampleArgs& a, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
-// Register-resident rows: sampling without top-k / top-p, greedy decoding,
-// and top-k (top_k <= the lanes holding row data) with or without top-p, of
-// 16-bit rows made of whole 16-byte vectors (V % 8 == 0, rows 16-byte
-// aligned, V <= 8 * 1024 * RES_MAX_SLABS).  Lane j holds vector
-// k*1024 + j of its row in four VGPRs per slab k (the sample_kernel layout),
-// so the row is read from memory once:
+// Register-resident rows of 16-bit logits made of whole 16-byte vectors
+// (V % 8 == 0, rows 16-byte aligned, V <= 8 * 1024 * RES_MAX_SLABS).  Lane j
+// holds vector k*1024 + j of its row in four VGPRs per slab k (the
+// sample_kernel layout), so the row is read from memory once.  Greedy
+// decoding and plain sampling run sample_blocks_kernel (below); top-k
+// (top_k <= the lanes holding row data) with or without top-p runs
+// sample_resident_kernel:
 //   A. as the slab loads land: the lane's first maximum (value and slab) and
 //      its online sum of exp((x - max) / T); one LDS exchange gives the row
 //      maximum, Z and the lowest-index argmax;
-//   K. (top-k) the k-th largest lane maximum t0 (a radix select over the
-//      1024 lane maxima), every entry >= t0 gathered into the LDS list, the
-//      exact k-th key on the list, then list_draw (ties, top-p, the draw);
-//      a row whose list overflows gets token -1 for sample_kernel's
-//      fill-in launch;
-//   B. (plain sampling) each lane's float sum of the floored softmax weights per
-//      slab into LDS, float64 slab totals, the slab holding u * total, a
-//      prefix scan of that slab's lane sums and the claiming lane's own
-//      entries: the search and tiling rule of vocab_search;
+//   K. the k-th largest lane maximum t0 (a radix select over the 1024 lane
+//      maxima), every entry >= t0 gathered into the LDS list, the exact k-th
+//      key on the list, then list_draw (ties, top-p, the draw); a row whose
+//      list overflows gets token -1 for sample_kernel's fill-in launch;
 //   C. the sampled token's S_other: for the argmax, the sum over every other
 //      entry relative to the row maximum, formed by the argmax lane's wave
 //      (the other lanes' sweep-A sums, the argmax lane's entries shared out
@@ -1037,34 +1061,16 @@ __device__ __forceinline__ uint32_t block_kth_key16(uint32_t key, bool valid, in
   return prefix;
 }
 
-// The defaults' floored softmax weight max(2^((x - max) * c2) / Z, 1e-9),
-// rounded the same way wherever it is evaluated.
-__device__ __forceinline__ float floored_weight(float x, float M, float c2, float inv_z) {
-  float w = fmaxf(exp2_hw((x - M) * c2) * inv_z, 1e-9f);
-  asm volatile("" : "+v"(w));
-  return w;
-}
-
 template <class Tag, int SL>
 __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   static_assert(Tag::VEC == 8, "16-bit rows");
-  // Sweep B's lane sums of the weights per slab, or top-k's candidate list.
-  __shared__ union {
-    float part[SL][SNT];
-    CandShared cs;
-  } u;
-  auto& part = u.part;
-  auto& cs = u.cs;
+  __shared__ CandShared cs;  // top-k's candidate list
   __shared__ uint32_t hist[256];
   __shared__ uint32_t sh_digit, sh_above, sh_kth;
   __shared__ int sh_need;
   __shared__ float sh_z[SWAVES];
-  __shared__ double slab_tot[SL];
-  __shared__ double scan_ws[SWAVES];
   __shared__ float sh_m[SWAVES], sh_s[SWAVES];
   __shared__ int sh_i[SWAVES];
-  __shared__ int sh_sel;
-  __shared__ float sh_w, sh_x;
   __shared__ u32x4 arg_row[SL];  // the argmax lane's registers (sweep C)
 
   const int r = blockIdx.x;
@@ -1148,27 +1154,9 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
     bi = sh_m[w] == M ? min(bi, sh_i[w]) : bi;
   }
   if (M == NEG || Z != Z || __builtin_fabsf(M * iT) == __builtin_huge_valf() || bi >= V) {
-    int tok_bad = bi < V ? bi : 0;
-    if (a.greedy && Z != Z) {
-      // Greedy decoding is torch.argmax, which ranks NaN above every number:
-      // the row's first NaN is its token (entries past the row hold -inf).
-      int fn = 0x7fffffff;
-#pragma unroll
-      for (int k = SL - 1; k >= 0; --k) {
-        if (k < nslab) {
-          float v[8];
-          unpack8<Tag>(x[k], v);
-#pragma unroll
-          for (int i = 7; i >= 0; --i)
-            if (v[i] != v[i]) fn = (k * SNT + tid) * 8 + i;
-        }
-      }
-      fn = block_min_i32(fn);
-      if (fn < V) tok_bad = fn;
-    }
     if (tid == 0) {
       raise_flag(a.status, RRL_FLAG_BAD_PROBS);
-      a.token[r] = tok_bad;
+      a.token[r] = bi < V ? bi : 0;
       a.logp[r] = __builtin_nanf("");
       if (a.logq) a.logq[r] = __builtin_nanf("");
     }
@@ -1180,7 +1168,7 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
 #pragma unroll
     for (int k = 0; k < SL; ++k) arg_row[k] = x[k];  // -inf past the row's end
   }
-  // Greedy decoding reads it next in the same wave, with no barrier between.
+  // Sweep C reads it in the same wave, after the top-k draw's barriers.
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
   uint32_t c[4] = {(uint32_t)r, 0u, (uint32_t)a.offset, (uint32_t)(a.offset >> 32)};
@@ -1189,158 +1177,69 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
 
   int tok = bi;
   float logq = 0.0f;
-  float xt_raw = M;  // the token's logit
-  const bool use_k = a.top_k > 0 && a.top_k < V;
-  if (!a.greedy && use_k) {
-    // Top-k (top_k <= the lanes holding row data, so every lane maximum
-    // counts): the k-th largest lane maximum t0 has at least k entries at or
-    // above it.  Those entries (a float compare: a superset of the keys
-    // >= t0 when -0 and +0 meet) go to the LDS list; the exact k-th key,
-    // its ties, top-p and the draw are found on the list.  A row whose list
-    // overflows gets token -1 and is redone by sample_kernel.
-    const int kq = (int)a.top_k;
-    constexpr int KB = Bits<Tag>::KB;
-    const uint32_t t0 = block_kth_key16(float_key<KB>(Bits<Tag>::bits_of(lm)), tid < nvec, kq,
-                                        hist, &sh_digit, &sh_above);
-    const float t0f = Bits<Tag>::val(key_bits<KB>(t0));
-    if (tid == 0) cs.n = 0;
-    __syncthreads();
+  // K. Top-k (top_k <= the lanes holding row data, so every lane maximum
+  // counts): the k-th largest lane maximum t0 has at least k entries at or
+  // above it.  Those entries (a float compare: a superset of the keys >= t0
+  // when -0 and +0 meet) go to the LDS list; the exact k-th key, its ties,
+  // top-p and the draw are found on the list.  A row whose list overflows
+  // gets token -1 and is redone by sample_kernel.
+  const int kq = (int)a.top_k;
+  constexpr int KB = Bits<Tag>::KB;
+  const uint32_t t0 = block_kth_key16(float_key<KB>(Bits<Tag>::bits_of(lm)), tid < nvec, kq,
+                                      hist, &sh_digit, &sh_above);
+  const float t0f = Bits<Tag>::val(key_bits<KB>(t0));
+  if (tid == 0) cs.n = 0;
+  __syncthreads();
 #pragma unroll
-    for (int k = 0; k < SL; ++k) {
-      if (k < nslab) {
-        float v[8];
-        unpack8<Tag>(x[k], v);
-        const bool inside = k * SNT + tid < nvec;
-        bool any = false;
+  for (int k = 0; k < SL; ++k) {
+    if (k < nslab) {
+      float v[8];
+      unpack8<Tag>(x[k], v);
+      const bool inside = k * SNT + tid < nvec;
+      bool any = false;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) any = any || v[i] >= t0f;
-        if (inside && any) {
-          const uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+      for (int i = 0; i < 8; ++i) any = any || v[i] >= t0f;
+      if (inside && any) {
+        const uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            if (v[i] >= t0f) {
-              const int p = atomicAdd(&cs.n, 1);
-              if (p < KCAP) {
-                cs.idx[p] = (k * SNT + tid) * 8 + i;
-                cs.bits[p] = (w[i >> 1] >> (16 * (i & 1))) & 0xffffu;
-              }
+        for (int i = 0; i < 8; ++i) {
+          if (v[i] >= t0f) {
+            const int p = atomicAdd(&cs.n, 1);
+            if (p < KCAP) {
+              cs.idx[p] = (k * SNT + tid) * 8 + i;
+              cs.bits[p] = (w[i >> 1] >> (16 * (i & 1))) & 0xffffu;
             }
           }
         }
       }
     }
-    __syncthreads();
-    const int n = cs.n;
-    if (n > KCAP) {
-      if (tid == 0) a.token[r] = -1;
-      return;
+  }
+  __syncthreads();
+  const int n = cs.n;
+  if (n > KCAP) {
+    if (tid == 0) a.token[r] = -1;
+    return;
+  }
+  // The exact k-th key: the entry with fewer than k keys above it and at
+  // least k at or above it (every such entry writes the same values).
+  if (tid < n) {
+    const uint32_t ki = float_key<KB>(cs.bits[tid]);
+    int gt = 0, eq = 0;
+    for (int j = 0; j < n; ++j) {
+      const uint32_t kj = float_key<KB>(cs.bits[j]);
+      gt += kj > ki ? 1 : 0;
+      eq += kj == ki ? 1 : 0;
     }
-    // The exact k-th key: the entry with fewer than k keys above it and at
-    // least k at or above it (every such entry writes the same values).
-    if (tid < n) {
-      const uint32_t ki = float_key<KB>(cs.bits[tid]);
-      int gt = 0, eq = 0;
-      for (int j = 0; j < n; ++j) {
-        const uint32_t kj = float_key<KB>(cs.bits[j]);
-        gt += kj > ki ? 1 : 0;
-        eq += kj == ki ? 1 : 0;
-      }
-      if (gt < kq && kq <= gt + eq) {
-        sh_kth = ki;
-        sh_need = kq - gt;
-      }
-    }
-    __syncthreads();
-    uint32_t tok_bits;
-    list_draw<Tag>(cs, sh_z, n, sh_kth, sh_need, a.top_p > 0.0 && a.top_p < 1.0, a.top_p, iT,
-                   M * iT, float_key<KB>(Bits<Tag>::bits_of(M)), u01, tok, logq, tok_bits);
-    xt_raw = Bits<Tag>::val(tok_bits);
-  } else if (!a.greedy) {
-    // B. Inverse CDF of the floored softmax in vocabulary order.
-    const float inv_z = 1.0f / Z;
-#pragma unroll
-    for (int k = 0; k < SL; ++k) {
-      if (k < nslab) {
-        float v[8];
-        unpack8<Tag>(x[k], v);
-        float w[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = floored_weight(v[i], M, c2, inv_z);
-        float f = sum8(w);
-        if (k >= nfull) {
-          asm volatile("");
-          if (k * SNT + tid >= nvec) f = 0.0f;  // -inf entries past the end weigh nothing
-        }
-        part[k][tid] = f;
-      }
-    }
-    __syncthreads();
-    for (int k = wave; k < nslab; k += SWAVES) {
-      double s = 0.0;
-#pragma unroll
-      for (int j = 0; j < SNT / 64; ++j) s += (double)part[k][lane + 64 * j];
-      s = wave_sum_d(s);
-      if (lane == 0) slab_tot[k] = s;
-    }
-    __syncthreads();
-    double total = 0.0;
-    for (int k = 0; k < nslab; ++k) total += slab_tot[k];
-    const double target = u01 * total;
-    int ks = -1;
-    double run = 0.0;
-    for (int k = 0; k < nslab; ++k) {
-      const double t = slab_tot[k];
-      if (run + t > target) {
-        ks = k;
-        break;
-      }
-      run += t;
-    }
-    if (ks < 0) {  // rounding left the target past the end: the last slab
-      ks = nslab - 1;
-      run -= slab_tot[ks];
-    }
-    if (tid == 0) sh_sel = -1;
-    const double lw = (double)part[ks][tid];
-    double incl, excl, scan_total;
-    block_scan_d(lw, scan_ws, incl, excl, scan_total);
-    const double lexcl = run + excl, lincl = run + incl;
-    // [lexcl, lincl) of consecutive lanes tile the slab from `run`; the last
-    // lane inside the row takes what rounding leaves past the end.
-    const int last_lane = min(nvec - ks * SNT, SNT) - 1;
-    if (lw > 0.0 && lexcl <= target && (target < lincl || tid == last_lane)) {
-      u32x4 xv = x[0];
-#pragma unroll
-      for (int k = 1; k < SL; ++k) xv = k == ks ? x[k] : xv;
-      float v[8];
-      unpack8<Tag>(xv, v);
-      double cum = lexcl;
-      int pick = -1;
-      float wp = 0.0f, xp = v[7];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float w = floored_weight(v[i], M, c2, inv_z);
-        if (pick < 0 && (cum + (double)w > target || i == 7)) {
-          pick = i;
-          wp = w;
-          xp = v[i];
-        }
-        cum += (double)w;
-      }
-      sh_sel = (ks * SNT + tid) * 8 + pick;
-      sh_w = wp;
-      sh_x = xp;
-    }
-    __syncthreads();
-    const int sel = sh_sel;
-    if (sel >= 0) {
-      tok = sel;
-      xt_raw = sh_x;
-      logq = (float)(log((double)sh_w) - log(total));
-    } else {  // no lane claimed (not reached): the argmax with its own weight
-      logq = (float)(log((double)fmaxf(inv_z, 1e-9f)) - log(total));
+    if (gt < kq && kq <= gt + eq) {
+      sh_kth = ki;
+      sh_need = kq - gt;
     }
   }
+  __syncthreads();
+  uint32_t tok_bits;
+  list_draw<Tag>(cs, sh_z, n, sh_kth, sh_need, a.top_p > 0.0 && a.top_p < 1.0, a.top_p, iT,
+                 M * iT, float_key<KB>(Bits<Tag>::bits_of(M)), u01, tok, logq, tok_bits);
+  const float xt_raw = Bits<Tag>::val(tok_bits);
 
   // C. S_other of the token and its log-prob, by the wave holding it.
   const int W = ((tok >> 3) & (SNT - 1)) >> 6;
@@ -1377,6 +1276,443 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   }
 }
 
+
+// A value known to be the same in every active lane, moved to scalar
+// registers (the compiler cannot prove values read back from LDS uniform,
+// and the register-resident kernels have no vector registers to spare).
+__device__ __forceinline__ float uni(float v) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ double uni(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)b);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(b >> 32));
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// DPP row shift right by N lanes of a float64 (both halves moved alike); a
+// lane whose source lies before its row's start reads 0.
+template <int N>
+__device__ __forceinline__ double row_shr_d(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo =
+      (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)b, 0x110 + N, 0xF, 0xF, true);
+  const unsigned hi =
+      (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), 0x110 + N, 0xF, 0xF, true);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// Inclusive prefix sums of v within each row of 16 lanes.
+__device__ __forceinline__ double row_scan_d(double v) {
+  v += row_shr_d<1>(v);
+  v += row_shr_d<2>(v);
+  v += row_shr_d<4>(v);
+  v += row_shr_d<8>(v);
+  return v;
+}
+
+// Inclusive and exclusive float64 prefix sums over the wave in lane order,
+// and the total.  Each lane's exclusive value is the previous lane's
+// inclusive one (the same operands, the same operation), so the ranges
+// [excl, incl) of consecutive lanes tile [0, total).
+__device__ __forceinline__ void wave_scan_d(double v, double& incl, double& excl, double& total) {
+  const int lane = threadIdx.x & 63, row = lane >> 4;
+  const double in = row_scan_d(v);
+  const double pin = row_shr_d<1>(in);  // the previous lane's, 0 at a row start
+  const double o1 = readlane_d(in, 15);
+  const double o2 = o1 + readlane_d(in, 31);
+  const double o3 = o2 + readlane_d(in, 47);
+  const double off = row == 0 ? 0.0 : (row == 1 ? o1 : (row == 2 ? o2 : o3));
+  incl = row == 0 ? in : off + in;
+  excl = (lane & 15) == 0 ? off : (row == 0 ? pin : off + pin);
+  total = o3 + readlane_d(in, 63);
+}
+
+// The lane whose range [base + excl, base + incl) of weight w > 0 holds
+// target, else (rounding left target at or past the end) the last lane with
+// w > 0, else -1; start = that lane's base + excl.
+__device__ __forceinline__ int wave_claim(double w, double lo, double hi, double target,
+                                          double& start) {
+  const unsigned long long hit = __ballot(w > 0.0 && lo <= target && target < hi);
+  const unsigned long long pos = __ballot(w > 0.0);
+  const int l = hit ? __builtin_ctzll(hit) : (pos ? 63 - __builtin_clzll(pos) : -1);
+  start = l >= 0 ? readlane_d(lo, l) : 0.0;
+  return l;
+}
+
+// ---------------------------------------------------------------------------
+// Register-resident rows, greedy decoding and sampling without top-k / top-p
+// (the reference's defaults), on block sums.  The row layout is
+// sample_resident_kernel's (lane j holds vector k*1024 + j of slab k).  Block
+// (k, w) is wave w's 512 entries of slab k; taken in (k, w) order the blocks
+// are the row in vocabulary order.
+//   A. as slab k lands, wave w adds 2^((x - R_w) c2) over its block into
+//      S[k][w] (one hardware exponential per entry), against a reference R_w
+//      fixed per wave: the maximum of its block of slab 0.  Each lane keeps
+//      its first maximum, for the argmax.  Nothing per lane is kept for
+//      later: a block is one number.
+//   After the loads: M and the lowest-index argmax from the wave maxima;
+//      block weights t[k][w] = S[k][w] 2^((R_w - M) c2), one per lane of 16
+//      lanes per slab (a wave whose R_w lies more than 64 binary orders below
+//      M first redoes its sums against M, so no block sum can have
+//      overflowed) and the slab totals T_k as DPP row sums in float64; wave 0
+//      alone then scans the T_k (Z is their total).
+//   B. (sampling) the floored softmax max(p, 1e-9) as the mixture of p
+//      (probability 1 / (1 + G)) and the floor's excess max(1e-9 - p, 0)
+//      (probability G / (1 + G), G = sum of the excess), chosen by a second
+//      uniform.  Wave 0 finds the slab holding target = u * total by a scan
+//      of the slab totals and then the block by a scan of that slab's block
+//      weights; the block's wave scans its lanes' sums (recomputed from
+//      registers), and the claiming lane walks its own 8 entries.  Every
+//      level tiles as wave_scan_d does, and the last positive slab, block,
+//      lane or entry takes a target that rounding leaves past the end.  G
+//      costs one exponential per entry, only when log q is asked for or the
+//      component uniform is below V * 1e-9 >= G / (1 + G); the excess's block
+//      sums are formed in the second case alone.
+//   C. S_other of the token: for the argmax, Z less its own block's weight
+//      (in float64) plus that block recomputed without it, so a dominant
+//      token keeps its relative precision; any other token: Z - e_tok.
+template <class Tag, int SL>
+__global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
+  static_assert(Tag::VEC == 8, "16-bit rows");
+  static_assert(SL <= 64, "one lane per slab in wave 0's scan");
+  __shared__ float blk_s[SL][SWAVES];   // S[k][w], later the excess's wave sums
+  __shared__ float blk_r[SWAVES];       // R_w
+  __shared__ double blk_t[SL][SWAVES];  // t[k][w]
+  __shared__ double slab_tot[SL];       // T_k
+  __shared__ double blk_g[SL][SWAVES];  // the excess's block sums (rare)
+  __shared__ double slab_g[SL];
+  __shared__ double red_ws[SWAVES];
+  __shared__ float sh_m[SWAVES];
+  __shared__ int sh_i[SWAVES];
+  __shared__ double sh_z, sh_run, sh_tgt;
+  __shared__ int sh_ks, sh_ws, sh_sel;
+  __shared__ float sh_x;
+
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int V = (int)a.V;
+  const int nvec = V >> 3;
+  const int nslab = (nvec + SNT - 1) / SNT;
+  const int nfull = nvec / SNT;  // slabs whose every lane lies inside the row
+  const float NEG = -__builtin_huge_valf();
+  const typename Tag::S* row = static_cast<const typename Tag::S*>(a.logits) + (int64_t)r * a.stride;
+  const __amdgpu_buffer_rsrc_t src = row_rsrc(row, (uint32_t)V * 2u);
+  u32x4 x[SL];
+#pragma unroll
+  for (int k = 0; k < SL; ++k)
+    x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, tid * 16, k * SNT * 16, kAuxLoad);
+
+  const float iT = 1.0f / a.temp;
+  const float c2 = iT * kLog2e;  // exp(y / T) = 2^(y * c2)
+
+  // A.  fmaxf skips NaN in the lane maxima and in R_w; NaN and +inf reach
+  // the block sums and flag the row.
+  float lm = NEG, R = 0.0f;
+  int lk = 0;
+#pragma unroll
+  for (int k = 0; k < SL; ++k) {
+    if (k < nslab) {
+      if (k >= nfull) {
+        // The row's last, partial slab: lanes past the end read zeros and
+        // hold -inf from here on (exponential 0).
+        asm volatile("");
+        if (k * SNT + tid >= nvec) x[k] = u32x4{Bits<Tag>::NEG_INF, Bits<Tag>::NEG_INF,
+                                                Bits<Tag>::NEG_INF, Bits<Tag>::NEG_INF};
+      }
+      float v[8];
+      unpack8<Tag>(x[k], v);
+      const float mc = max8(v);
+      lk = mc > lm ? k : lk;
+      lm = fmaxf(lm, mc);
+      if (k == 0) R = uni(fmaxf(wave_max_dpp(mc), -__FLT_MAX__));
+      float e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = exp2_hw((v[i] - R) * c2);
+      const float s = wave_sum_dpp(sum8(e));
+      if (lane == 0) blk_s[k][wave] = s;
+    }
+  }
+  // Per wave: the maximum and the lowest index holding it (found in the one
+  // slab where each such lane first met its maximum).
+  const float wm = wave_max_dpp(lm);
+  int ci = 0x7fffffff;
+  if (lm == wm && wm > NEG) {
+#pragma unroll
+    for (int k = 0; k < SL; ++k) {
+      if (k == lk) {
+        float v[8];
+        unpack8<Tag>(x[k], v);
+        int ic = 7;
+#pragma unroll
+        for (int i = 6; i >= 0; --i) ic = v[i] == wm ? i : ic;
+        ci = (k * SNT + tid) * 8 + ic;
+      }
+    }
+  }
+  const int wi = wave_min_dpp(ci);
+  if (lane == 0) {
+    sh_m[wave] = wm;
+    sh_i[wave] = wi;
+    blk_r[wave] = R;
+  }
+  if (tid == 0) sh_sel = -1;
+  __syncthreads();
+  // Lane l of every wave reads wave (l & 15)'s values.
+  const float Rl = blk_r[lane & 15];
+  const float mw = sh_m[lane & 15];
+  const float M = uni(wave_max_dpp(mw));
+  const int bi = uni(wave_min_dpp(mw == M ? sh_i[lane & 15] : 0x7fffffff));
+
+  // A wave whose reference lies more than 64 binary orders below M (a later
+  // slab rose far above its first) redoes its block sums against M; every
+  // wave takes the same decision from the same LDS values.
+  auto far_below = [&](float Rw) { return (M - Rw) * c2 > 64.0f; };
+  if (__ballot(far_below(Rl)) != 0ull) {
+    if (far_below(R)) {
+#pragma unroll
+      for (int k = 0; k < SL; ++k) {
+        if (k < nslab) {
+          float v[8];
+          unpack8<Tag>(x[k], v);
+          float e[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) e[i] = exp2_hw((v[i] - M) * c2);
+          const float s = wave_sum_dpp(sum8(e));
+          if (lane == 0) blk_s[k][wave] = s;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // Block weights, one per thread of the first nslab * 16, and the slab
+  // totals as row sums (row k of 16 lanes is slab k).
+  if (tid < nslab * SWAVES) {
+    const int k = tid >> 4;
+    const float t = blk_s[k][lane & 15] * exp2_hw(((far_below(Rl) ? M : Rl) - M) * c2);
+    blk_t[k][lane & 15] = (double)t;
+    const double T = row_scan_d((double)t);
+    if ((lane & 15) == 15) slab_tot[k] = T;
+  }
+  __syncthreads();
+
+  // The row's uniforms (sampling only): u01 places the draw, u1 picks the
+  // mixture's component.
+  double u01 = 0.0, u1 = 1.0;
+  if (!a.greedy) {
+    uint32_t c[4] = {(uint32_t)r, 0u, (uint32_t)a.offset, (uint32_t)(a.offset >> 32)};
+    philox4x32_10(c, (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
+    u01 = uni((double)(c[0] >> 8) * 5.9604644775390625e-8);  // 2^-24
+    u1 = uni((double)(((uint64_t)c[1] << 21) | (c[2] >> 11)) * 0x1p-53);
+  }
+
+  // Wave 0: Z, and for sampling the slab and block holding u01 * total of
+  // the weights st (slab totals) and bt (block weights of slab k, lane w),
+  // into sh_ks, sh_ws, sh_run (the total before the block) and sh_tgt.
+  auto locate = [&](const double* st, auto bt) {
+    const double ts = lane < nslab ? st[lane] : 0.0;
+    double incl, excl, total;
+    wave_scan_d(ts, incl, excl, total);
+    const double target = u01 * total;
+    double run;
+    const int ks = wave_claim(ts, excl, incl, target, run);
+    const double tb = ks >= 0 && lane < SWAVES ? bt(ks, lane) : 0.0;
+    double bincl, bexcl, btot;
+    wave_scan_d(tb, bincl, bexcl, btot);
+    double brun;
+    const int ws = wave_claim(tb, run + bexcl, run + bincl, target, brun);
+    if (lane == 0) {
+      sh_ks = ks;
+      sh_ws = ks >= 0 ? ws : -1;
+      sh_run = brun;
+      sh_tgt = target;
+    }
+    return total;
+  };
+  if (wave == 0) {
+    const double Z = a.greedy ? 0.0 : locate(slab_tot, [&](int k, int w) { return blk_t[k][w]; });
+    if (lane == 0) {
+      if (a.greedy) {
+        double s = 0.0;
+        for (int k = 0; k < nslab; ++k) s += slab_tot[k];
+        sh_z = s;
+      } else {
+        sh_z = Z;
+      }
+    }
+  }
+  __syncthreads();
+  const double Zd = uni(sh_z);
+
+  if (M == NEG || Zd != Zd || __builtin_fabsf(M * iT) == __builtin_huge_valf() || bi >= V) {
+    int tok_bad = bi < V ? bi : 0;
+    if (a.greedy && Zd != Zd) {
+      // Greedy decoding is torch.argmax, which ranks NaN above every number:
+      // the row's first NaN is its token (entries past the row hold -inf).
+      int fn = 0x7fffffff;
+#pragma unroll
+      for (int k = SL - 1; k >= 0; --k) {
+        if (k < nslab) {
+          float v[8];
+          unpack8<Tag>(x[k], v);
+#pragma unroll
+          for (int i = 7; i >= 0; --i)
+            if (v[i] != v[i]) fn = (k * SNT + tid) * 8 + i;
+        }
+      }
+      fn = block_min_i32(fn);
+      if (fn < V) tok_bad = fn;
+    }
+    if (tid == 0) {
+      raise_flag(a.status, RRL_FLAG_BAD_PROBS);
+      a.token[r] = tok_bad;
+      a.logp[r] = __builtin_nanf("");
+      if (a.logq) a.logq[r] = __builtin_nanf("");
+    }
+    return;
+  }
+
+  int tok = bi;
+  float logq = 0.0f;
+  float xt_raw = M;  // the token's logit
+  if (!a.greedy) {
+    const float lz = uni(log2f((float)Zd));
+    const float K = uni(__builtin_fmaf(M, c2, lz));
+    auto rho = [&](float v) { return exp2_hw((v - M) * c2); };                   // Z p
+    auto pn = [&](float v) { return exp2_hw(__builtin_fmaf(v - M, c2, -lz)); };  // p
+    // The floor's side: p = 2^(x c2 - K) in one fma (its rounding only moves
+    // the excess, a sum of at most V * 1e-9, by parts in 1e6).
+    auto pf = [&](float v) { return exp2_hw(__builtin_fmaf(v, c2, -K)); };
+    auto g_of = [&](float v) { return fmaxf(1e-9f - pf(v), 0.0f); };
+    const bool want_q = a.logq != nullptr;
+    const bool near = u1 < (double)V * 1.001e-9;
+    double G = 0.0;
+    if (want_q || near) {
+      float gs = 0.0f;
+#pragma unroll
+      for (int k = 0; k < SL; ++k) {
+        if (k < nslab) {
+          float v[8];
+          unpack8<Tag>(x[k], v);
+          // sum of max(1e-9 - p, 0) = 8e-9 - sum of min(p, 1e-9)
+          float m[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) m[i] = fminf(pf(v[i]), 1e-9f);
+          float f = 8.0f * 1e-9f - sum8(m);
+          if (k >= nfull) {
+            asm volatile("");
+            if (k * SNT + tid >= nvec) f = 0.0f;  // -inf past the row's end is not floored
+          }
+          gs += f;
+          if (near) {
+            const float s = wave_sum_dpp(f);
+            if (lane == 0) blk_s[k][wave] = s;
+          }
+        }
+      }
+      double t[1] = {(double)gs};
+      block_sum<SNT, 1, double>(t, red_ws);
+      G = uni(t[0]);
+    }
+    const bool use_g = near && u1 < G / (1.0 + G);
+    if (use_g) {
+      // The excess's block sums (written in the G pass) and slab totals,
+      // then the same search over them.
+      if (tid < nslab * SWAVES) {
+        const int k = tid >> 4;
+        const double t = (double)blk_s[k][lane & 15];
+        blk_g[k][lane & 15] = t;
+        const double T = row_scan_d(t);
+        if ((lane & 15) == 15) slab_g[k] = T;
+      }
+      __syncthreads();
+      if (wave == 0) locate(slab_g, [&](int k, int w) { return blk_g[k][w]; });
+      __syncthreads();
+    }
+    // The block's wave: its lanes' sums of the entry weights (0 past the
+    // row's end), a float64 scan from the block's start, and the claiming
+    // lane's own 8 entries.
+    const int ks = uni(sh_ks), wsel = uni(sh_ws);
+    if (wave == wsel) {
+      const double run = uni(sh_run), target = uni(sh_tgt);
+      u32x4 xv = x[0];
+#pragma unroll
+      for (int k = 1; k < SL; ++k) xv = k == ks ? x[k] : xv;
+      float v[8];
+      unpack8<Tag>(xv, v);
+      const bool inside = ks * SNT + tid < nvec;
+      float w8[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w8[i] = !inside ? 0.0f : (use_g ? g_of(v[i]) : rho(v[i]));
+      const double lw = (double)sum8(w8);
+      double incl, excl, total;
+      wave_scan_d(lw, incl, excl, total);
+      double lstart;
+      const int lc = wave_claim(lw, run + excl, run + incl, target, lstart);
+      if (lane == lc) {
+        double cum = lstart;
+        int pick = -1, lastp = 7;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (w8[i] > 0.0f) {
+            lastp = i;
+            if (pick < 0 && cum + (double)w8[i] > target) pick = i;
+          }
+          cum += (double)w8[i];
+        }
+        pick = pick >= 0 ? pick : lastp;
+        float xp = v[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) xp = i == pick ? v[i] : xp;
+        sh_sel = (ks * SNT + tid) * 8 + pick;
+        sh_x = xp;
+      }
+    }
+    __syncthreads();
+    const int sel = sh_sel;
+    if (sel >= 0) {  // else (not reached: every total is positive) the argmax
+      tok = sel;
+      xt_raw = sh_x;
+    }
+    // log q(token) = log(max(p_tok, 1e-9)) - log(1 + G).
+    if (want_q) logq = (float)(log((double)fmaxf(pn(xt_raw), 1e-9f)) - log1p(G));
+  }
+
+  // C. S_other of the token and its log-prob.
+  const int tb = (bi >> 3) & (SNT - 1);  // the argmax's lane
+  const int kb = (bi >> 3) / SNT;        // and slab
+  const int W = tok == bi ? tb >> 6 : 0;
+  if (wave != W) return;
+  float s_other;
+  if (tok == bi) {
+    u32x4 xv = x[0];
+#pragma unroll
+    for (int k = 1; k < SL; ++k) xv = k == kb ? x[k] : xv;
+    float v[8];
+    unpack8<Tag>(xv, v);
+    float e[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = (tid == tb && i == (bi & 7)) ? 0.0f : exp2_hw((v[i] - M) * c2);
+    const float sb = wave_sum_dpp(sum8(e));
+    s_other = (float)((Zd - blk_t[kb][W]) + (double)sb);
+  } else {
+    s_other = (float)(Zd - (double)exp2_hw((xt_raw - M) * c2));
+  }
+  if (lane == 0) {
+    const RowLogprob<float> fr = finish_row<float>(M * iT, s_other, xt_raw * iT);
+    a.token[r] = tok;
+    a.logp[r] = fr.logp;
+    if (a.logq) a.logq[r] = logq;
+  }
+}
+
 template <class Tag, int SL>
 int launch_resident_sl(const SampleArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((sample_resident_kernel<Tag, SL>), dim3((unsigned)a.B), dim3(SNT), 0, st, a);
@@ -1390,6 +1726,21 @@ int launch_sample_resident(const SampleArgs& a, int nslab, hipStream_t st) {
   if (nslab <= 12) return launch_resident_sl<Tag, 12>(a, st);
   if (nslab <= 16) return launch_resident_sl<Tag, 16>(a, st);
   return launch_resident_sl<Tag, RES_MAX_SLABS>(a, st);
+}
+
+template <class Tag, int SL>
+int launch_blocks_sl(const SampleArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((sample_blocks_kernel<Tag, SL>), dim3((unsigned)a.B), dim3(SNT), 0, st, a);
+  return check_launch("sample_blocks_kernel");
+}
+
+template <class Tag>
+int launch_sample_blocks(const SampleArgs& a, int nslab, hipStream_t st) {
+  if (nslab <= 4) return launch_blocks_sl<Tag, 4>(a, st);
+  if (nslab <= 8) return launch_blocks_sl<Tag, 8>(a, st);
+  if (nslab <= 12) return launch_blocks_sl<Tag, 12>(a, st);
+  if (nslab <= 16) return launch_blocks_sl<Tag, 16>(a, st);
+  return launch_blocks_sl<Tag, RES_MAX_SLABS>(a, st);
 }
 
 }  // namespace
@@ -1439,9 +1790,12 @@ extern "C" int rrl_sample_logprobs(const void* logits, int32_t logits_dtype, int
       nvec <= (int64_t)SNT * RES_MAX_SLABS && ((uintptr_t)logits & 15u) == 0 &&
       (B == 1 || row_stride % 8 == 0)) {
     const int nslab = (int)((nvec + SNT - 1) / SNT);
+    if (!res_topk)
+      return logits_dtype == RRL_BF16 ? launch_sample_blocks<TagBF16>(a, nslab, st)
+                                      : launch_sample_blocks<TagF16>(a, nslab, st);
     const int rc = logits_dtype == RRL_BF16 ? launch_sample_resident<TagBF16>(a, nslab, st)
                                             : launch_sample_resident<TagF16>(a, nslab, st);
-    if (rc != RRL_OK || !res_topk) return rc;
+    if (rc != RRL_OK) return rc;
     // Rows whose candidate list overflowed (token -1) go through the
     // streaming kernel, which returns at once for every other row.
     a.fill_in = 1;

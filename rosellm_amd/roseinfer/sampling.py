@@ -10,9 +10,11 @@ trainer later compares with its own recomputation (the train/inference
 mismatch of docs/agentic-rl/systems.md:252-274).
 
 ``sample_next_token_batch`` runs ``rrl_sample_logprobs``: one workgroup per
-row chooses the token by inverse CDF with a counter-based uniform (Philox4x32-10
+row chooses the token by inverse CDF with counter-based uniforms (Philox4x32-10
 of row, ``offset`` and ``seed``: reproducible, no generator state on the
-device) and returns, with it,
+device; without top-k / top-p, ``max(p, 1e-9)`` is drawn as the mixture of p
+and the floor's excess ``max(1e-9 - p, 0)``, a second uniform choosing the
+component) and returns, with it,
 
 * ``logprobs``: ``log_softmax(logits / T)[token]`` over the whole row (T = 1
   when greedy), formed as the training row kernels form log-probs — at T = 1
@@ -42,9 +44,10 @@ __all__ = ["SampleOutput", "sample_next_token", "sample_next_token_batch"]
 
 
 class SampleOutput(NamedTuple):
-    token_ids: Tensor          # [B] int64
-    logprobs: Tensor           # [B] float32, log_softmax(logits / T)[token]
-    sampling_logprobs: Tensor  # [B] float32, log q(token) of the sampled distribution
+    token_ids: Tensor                    # [B] int64
+    logprobs: Tensor                     # [B] float32, log_softmax(logits / T)[token]
+    sampling_logprobs: Optional[Tensor]  # [B] float32, log q(token) of the sampled
+                                         # distribution (None when not asked for)
 
 
 def _draw_seed(generator: Optional[torch.Generator]) -> int:
@@ -63,6 +66,7 @@ def sample_next_token_batch(
     seed: Optional[int] = None,
     offset: int = 0,
     generator: Optional[torch.Generator] = None,
+    sampling_logprobs: bool = True,
 ) -> SampleOutput:
     """Sample one token per row of ``logits`` [B, V] with the reference's
     argument meaning (roseinfer/engine.py:1103-1171) and return its
@@ -72,6 +76,10 @@ def sample_next_token_batch(
     (r, offset)); with ``seed=None`` a seed is drawn from ``generator`` (a CPU
     ``torch.Generator``, default: torch's global one).  A decode loop can keep
     one seed and advance ``offset`` per step.
+
+    ``sampling_logprobs=False`` skips ``log q(token)`` (the field is None).
+    The token and ``logprobs`` do not change; without top-k / top-p, log q
+    needs the 1e-9 floor's total mass, one more exponential per entry.
     """
 
     if logits.dim() != 2:
@@ -87,7 +95,7 @@ def sample_next_token_batch(
         seed = _draw_seed(generator)
     tokens = torch.empty(B, dtype=torch.int64, device=dev)
     logp = torch.empty(B, dtype=torch.float32, device=dev)
-    logq = torch.empty(B, dtype=torch.float32, device=dev)
+    logq = torch.empty(B, dtype=torch.float32, device=dev) if sampling_logprobs else None
     # No status word: a row with NaN or +inf logits (or no finite maximum)
     # gets a NaN log-prob, and every other row a finite one, so one copy of
     # the log-probs to the host (the synchronisation the reference's own
@@ -95,7 +103,8 @@ def sample_next_token_batch(
     nat.call("rrl_sample_logprobs", x.data_ptr(), nat.dtype_code(x.dtype), B, V,
              x.stride(0) if B > 1 else V, float(temperature), int(top_k), float(top_p),
              int(bool(do_sample)), int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 64 - 1),
-             tokens.data_ptr(), logp.data_ptr(), logq.data_ptr(), None, nat.stream_ptr(dev))
+             tokens.data_ptr(), logp.data_ptr(), logq.data_ptr() if logq is not None else None,
+             None, nat.stream_ptr(dev))
     # Sampling raises on such rows, as torch.multinomial does; NaN anywhere
     # makes the sum NaN (the log-probs are never +inf).  Greedy decoding is
     # torch.argmax in the reference (engine.py:1117-1118), which never raises:

@@ -216,6 +216,62 @@ def test_resident_topk_list_overflow(device, top_k, top_p):
         _check(x, out, seed=13, offset=off, what=f"overflow k={top_k} off={off}", **kw)
 
 
+@pytest.mark.parametrize("case", ["spike", "cold", "masked_head"])
+@pytest.mark.parametrize("do_sample", [True, False])
+def test_block_sums_against_far_references(device, case, do_sample):
+    """Plain sampling and greedy decoding sum each wave's 512-entry block of a
+    slab against the maximum of that wave's block of slab 0; a wave whose
+    reference lies more than 64 binary orders below the row maximum redoes its
+    sums against the maximum.  Rows that take that path: a spike of +80 (half
+    the rows in slab 0, half later) over N(0, 1) logits at T = 1; N(0, 3)
+    logits at T = 0.08; a vocabulary head of 10000 entries masked to -inf, so
+    that every wave's block of slab 0 is empty."""
+
+    B, V = 24, 151936
+    g = torch.Generator().manual_seed(77)
+    x = torch.randn(B, V, generator=g)
+    T = 1.0
+    if case == "spike":
+        rows = torch.arange(B)
+        at = torch.where(rows % 2 == 0, 97 * rows, 20000 + 5003 * rows)
+        x[rows, at] = 80.0
+    elif case == "cold":
+        x *= 3.0
+        T = 0.08
+    else:
+        x *= 3.0
+        x[:, :10000] = float("-inf")
+    x = x.to(torch.bfloat16)
+    kw = dict(temperature=T, top_k=0, top_p=1.0, do_sample=do_sample)
+    print(f"[sampler] far references case={case} {kw}", flush=True)
+    xd = x.to(device)
+    for off in (0, 3):
+        out = RI.sample_next_token_batch(xd, seed=5, offset=off, **kw)
+        _check(x, out, seed=5, offset=off, what=f"{case} off={off}", **kw)
+        if T == 1.0:
+            lp = R.gather_token_logprobs(xd, out.token_ids).cpu().double()
+            assert torch.allclose(out.logprobs.cpu().double(), lp, rtol=1e-6, atol=1e-6)
+        if not do_sample:
+            assert torch.equal(out.token_ids.cpu(), torch.argmax(x.float(), dim=-1))
+
+
+@pytest.mark.parametrize("kw", [
+    dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=True),
+    dict(temperature=0.7, top_k=50, top_p=0.9, do_sample=True),
+    dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=False),
+], ids=["defaults", "topk-topp", "greedy"])
+def test_without_sampling_logprobs(device, kw):
+    """sampling_logprobs=False leaves the token and log-prob of every row as
+    they are (the same uniforms, the same draw) and returns no log q."""
+
+    x = _rows(5, 32, 151936, torch.bfloat16).to(device)
+    full = RI.sample_next_token_batch(x, seed=21, offset=4, **kw)
+    bare = RI.sample_next_token_batch(x, seed=21, offset=4, sampling_logprobs=False, **kw)
+    assert bare.sampling_logprobs is None
+    assert torch.equal(bare.token_ids, full.token_ids)
+    assert torch.equal(bare.logprobs, full.logprobs)
+
+
 def test_resident_draws_follow_the_distribution(device):
     """8192 draws from one bf16 row held in registers (a stride-0 view)."""
 

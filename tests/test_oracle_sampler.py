@@ -99,7 +99,56 @@ def test_inverse_cdf_draws_follow_the_distribution():
     np.testing.assert_allclose(out["logq"], np.log(q[out["token"]] / q.sum()), rtol=1e-12)
 
 
+@pytest.mark.parametrize("p", [
+    [5e-10, 2e-10, 3e-9, 1e-10, 0.0, 4e-9],
+    [1e-9, 7e-10, 7e-10, 2e-9],
+    [3e-10, 3e-10, 3e-10],  # every entry floored: p itself has the smaller share
+])
+def test_mixture_rule_draws_the_floored_weights(p):
+    """The plain-sampling draw of max(p, 1e-9) as a mixture of p and the
+    floor's excess, integrated exactly over both uniforms.  Weights this small
+    give the floor a large share, so a wrong component probability, swapped
+    components or a wrong excess changes the frequencies by far more than the
+    grid's resolution.  The frequencies must be max(p, 1e-9) / sum."""
+
+    p = np.asarray(p, dtype=np.float64)
+    q = np.maximum(p, 1e-9)
+    want = q / q.sum()
+    n = 4000
+    grid = (np.arange(n) + 0.5) / n
+    freq = np.zeros(p.size)
+    rho, g, pi = so.mixture_parts(p)
+    assert math.isclose(pi, g.sum() / (p.sum() + g.sum()), rel_tol=1e-15)
+    # u1 picks the component; u the position inside it: the frequencies of a
+    # grid over (u1, u) are pi * (grid draws of g) + (1 - pi) * (grid of p)
+    for comp, share in ((g, pi), (rho, 1.0 - pi)):
+        if share == 0.0:
+            continue
+        toks = np.array([so.inverse_cdf(comp, u)[0] for u in grid])
+        freq += share * np.bincount(toks, minlength=p.size) / n
+    np.testing.assert_allclose(freq, want, atol=2.0 / n)
+    # and mixture_draw picks the component the same way
+    for u1 in (0.0, pi * 0.999, pi * 1.001, 0.999999):
+        tok, _ = so.mixture_draw(p, 0.5, u1)
+        assert tok == so.inverse_cdf(g if u1 < pi else rho, 0.5)[0]
+
+
+def test_inverse_cdf_edges():
+    # the target lands on a boundary: the next entry with positive weight
+    w = np.array([0.25, 0.0, 0.25, 0.5])
+    assert so.inverse_cdf(w, 0.25)[0] == 2
+    assert so.inverse_cdf(w, 0.0)[0] == 0
+    assert so.inverse_cdf(w, 0.9999)[0] == 3
+    # rounding past the end takes the last positive entry, not a zero one
+    assert so.inverse_cdf(np.array([0.5, 0.5, 0.0]), 1.0)[0] == 1
+
+
 def test_uniforms():
+    u1 = np.array([so.row_uniforms(1234, 7, r)[1] for r in range(50000)])
+    assert abs(u1.mean() - 0.5) < 0.005 and abs(u1.var() - 1 / 12) < 0.002
+    # the component uniform takes bits the position uniform does not use
+    w = so.philox4x32_10((3, 0, 7, 0), (1234, 0))
+    assert so.row_uniforms(1234, 7, 3)[1] * 2.0 ** 53 == (w[1] << 21) | (w[2] >> 11)
     u = np.array([so.row_uniform(1234, 7, r) for r in range(50000)])
     assert abs(u.mean() - 0.5) < 0.005 and abs(u.var() - 1 / 12) < 0.002
     ks = np.max(np.abs(np.sort(u) - (np.arange(u.size) + 0.5) / u.size))
