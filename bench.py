@@ -252,7 +252,8 @@ def make_step(inp, cfg, path, objective, skip_masked=False, probe=None):
             weight.grad = None
             a = R.group_standardized_advantages(rewards).reshape(-1)[:, None].expand(B, T)
             if path == "fused":
-                out = R.fused_linear_policy_loss(hidden, weight, actions, old, a, mask, **kw)
+                out = R.fused_linear_policy_loss(hidden, weight, actions, old, a, mask,
+                                                 skip_masked_rows=skip_masked, **kw)
             else:
                 lp = R.gather_token_logprobs(F.linear(hidden, weight), actions)
                 _watch(lp, probe)
@@ -713,6 +714,38 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
         }
         log(f"[bench] skip_masked_rows: {v_el * 1e3 / steps:.3f} ms/step, kernels "
             + ", ".join(f"{k} {v:.3f} ms" for k, v in vavg.items()))
+    if skip_masked_variant and path == "fused" and cfg.get("lm_head"):
+        # Config 5 with skip_masked_rows=True: the forward leaves out the
+        # 64-token blocks whose tokens are all masked (no log-sum-exp pass);
+        # loss and gradients are those of the headline step.
+        vstep = make_step(inp, cfg, path, objective, skip_masked=True)
+        for _ in range(warmup):
+            vstep()
+        vk = ["rrl_lm_head_fwd", "rrl_lm_head_dweight", "rrl_lm_head_dhidden"]
+        vres = timed_steps(vstep, steps, vk)
+        v_el = vres["wall_s"]
+        vavg = {k: sum(s.elapsed_time(e) for s, e in vres["launches"][k])
+                / len(vres["launches"][k]) for k in vk}
+        assert vres["out"].loss.item() == out.loss.item(), "skip_masked_rows changed the loss"
+        H = inp["hidden"].shape[-1]
+        obar_blocks = roofline["fwd_obar_blocks"]
+        fwd_exec = 2 * 2 * obar_blocks * 64 * H * V
+        model = 3 * 2 * N * H * V
+        v_ms = v_el * 1e3 / steps
+        variants["skip_masked_rows"] = {
+            "value": round(N / (v_el / steps), 1),
+            "ms_per_step": round(v_ms, 4),
+            "ms_per_step_median": round(statistics.median(vres["step_ms"]), 4),
+            "kernels_ms": {k: round(v, 4) for k, v in vavg.items()},
+            "fwd_executed_flops": fwd_exec,
+            "fwd_TFLOPs": round(fwd_exec / (vavg["rrl_lm_head_fwd"] * 1e-3) / 1e12, 1),
+            "step_TFLOPs_model": round(model / (v_ms * 1e-3) / 1e12, 1),
+            "step_frac": round(model / (v_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "note": "fully masked 64-token blocks skipped in the forward; step_frac on the "
+                    "model's 3*2*N*H*V flops",
+        }
+        log(f"[bench] skip_masked_rows: {v_ms:.3f} ms/step, kernels "
+            + ", ".join(f"{k} {v:.3f} ms" for k, v in vavg.items()))
     if skip_masked_variant and path == "fused" and objective == "clipped" \
             and not cfg.get("lm_head"):
         # The same step with skip_masked_rows=True (zero-weight rows are never
@@ -1026,9 +1059,9 @@ def main():
                 if name == "sample":
                     r = bench_sample(args, v_steps, v_warm, not args.skip_cpu)
                 else:
-                    # C3's two objectives also time their skip_masked_rows entry
+                    # C3's two objectives and C5 also time their skip_masked_rows entry
                     r = measure_config(name, args, device, v_steps, v_warm, not args.skip_cpu,
-                                       skip_masked_variant=name in ("c3", "c3_gspo_token"))
+                                       skip_masked_variant=name in ("c3", "c3_gspo_token", "c5"))
                 variants[name] = compact(r)
             except Exception as e:  # recorded, never fatal to the headline
                 variants[name] = {"error": f"{type(e).__name__}: {e}"[:400]}

@@ -352,10 +352,13 @@ RRL_API int rrl_masked_whiten(int64_t B, int64_t T, rrl_view x, rrl_view mask, d
  * raises TARGET_RANGE; a token whose logits exceed the fixed reference point's
  * range raises LM_RANGE (rerun with mref_in = the lse of an obar-less call).
  * mref_in: NULL, or float32 [N] reference points (the rerun).  need_obar:
- * NULL, or uint8 [N] (nonzero: the token's obar is needed); a block of 64
- * consecutive tokens none of which needs it takes the log-sum-exp-only pass
- * and its obar rows are left unwritten (for tokens whose d loss / d logp is
- * zero by construction, such as masked tokens).  workspace: with need_obar
+ * NULL, or uint8 [N]: 1 = the token's obar is needed, 0 = its lse and logp
+ * only, 2 = neither.  A block of 64 consecutive tokens none of which needs
+ * obar takes the log-sum-exp-only pass and its obar rows are left unwritten
+ * (for tokens whose d loss / d logp is zero by construction, such as masked
+ * tokens); a block whose 64 tokens are all 2 is not computed at all, and its
+ * tokens get lse = logp = 0 (a masked token's log-prob that the caller
+ * discards; no reference counterpart).  workspace: with need_obar
  * and obar, rrl_lm_head_fwd_workspace_bytes(N) bytes of caller device memory
  * (16-byte aligned; the order in which the blocks are taken), else ignored. */
 RRL_API size_t rrl_lm_head_fwd_workspace_bytes(int64_t N);

@@ -184,10 +184,13 @@ struct LmArgs {
   float* obar;           // forward: sum_{v != a} p_v W_v per token, [nx, H] (ld obar_ld)
   int64_t obar_ld;
   const float* mref_in;  // forward: per-token reference point (NULL: first-tile rule)
-  const uint8_t* need_obar;  // forward: per-token "obar needed" (NULL: every token)
+  const uint8_t* need_obar;  // forward: per token 1 = obar needed, 0 = log-prob only,
+                             // 2 = neither (NULL: obar for every token)
   const int32_t* block_order;  // forward with need_obar: the 64-token blocks, those that
-                               // need obar first
-  const int32_t* block_count;  // forward with need_obar: how many blocks need obar
+                               // need obar first, then those that need log-probs only,
+                               // then those needing neither
+  const int32_t* block_count;  // forward with need_obar: [0] blocks that need obar,
+                               // [1] blocks that need obar or log-probs
   const int32_t* tile_list;  // dW pass: indices of the streamed tiles to visit (NULL: all)
   const int32_t* tile_count; // dW pass: number of entries of tile_list
   const float4* trec;    // dW pass: per streamed token {target bits, g, lse*log2e, g*(-expm1(logp))}
@@ -607,10 +610,12 @@ template <class Tag, int MODE, int H>
 __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[LdsLayout<H>::kTotal];
   if constexpr (MODE == kModeFwd) {
-    // With need_obar the launch covers both kinds of 64-token block, in
-    // block_order: workgroup i < count takes block block_order[i], which
-    // needs obar; the following workgroups take the remaining blocks two at
-    // a time through the log-sum-exp pass; surplus workgroups return at once.
+    // With need_obar the launch covers every 64-token block, in block_order:
+    // workgroup i < count takes block block_order[i], which needs obar; the
+    // following workgroups take the remaining blocks two at a time, through
+    // the log-sum-exp pass when some token of the block needs its log-prob,
+    // else writing 0 as every token's lse and log-prob (need value 2 on all
+    // 64: no work); surplus workgroups return at once.
     // Listing the obar blocks first, rather than taking blocks in token
     // order, spreads them evenly over the eight XCDs (consecutive workgroups
     // go to the XCDs in turn): masks that end each sequence in a run of
@@ -624,12 +629,24 @@ __global__ __launch_bounds__(kNT, 1) void lm_tile_kernel(LmArgs a) {
         lm_tile_body<Tag, MODE, H>(a, lds, blk * kBM, 0, (a.ny + kBN - 1) / kBN, nullptr);
         return;
       }
-      const int32_t nblocks = (a.nx + kBM - 1) / kBM;
+      const int32_t nblocks = (a.nx + kBM - 1) / kBM, live = a.block_count[1];
       const int32_t e = count + 2 * (i - count);
       if (e >= nblocks) return;
+      // Blocks of this pair that need no output: zeros, one thread per token.
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        if (e + q >= live && e + q < nblocks && threadIdx.x < kBM) {
+          const int32_t row = a.block_order[e + q] * kBM + (int32_t)threadIdx.x;
+          if (row < a.nx) {
+            a.lse_out[row] = 0.f;
+            a.logp_out[row] = 0.f;
+          }
+        }
+      }
+      if (e >= live) return;
       const int32_t x_a = __builtin_amdgcn_readfirstlane(a.block_order[e]) * kBM;
       const int32_t x_b =
-          e + 1 < nblocks ? __builtin_amdgcn_readfirstlane(a.block_order[e + 1]) * kBM : -1;
+          e + 1 < live ? __builtin_amdgcn_readfirstlane(a.block_order[e + 1]) * kBM : -1;
       lm_lse_body<Tag, H>(a, lds, x_a, x_b);
       return;
     }
@@ -884,18 +901,21 @@ __global__ __launch_bounds__(1024) void lm_tile_list_kernel(int32_t n, const uin
   if (tid == 0) *count = base;
 }
 
-// Order of the forward's 64-token blocks: those with a token whose obar is
-// needed first, then the others, each in ascending order (one workgroup).
+// Order of the forward's 64-token blocks (one workgroup): those with a token
+// whose obar is needed (need value 1) first, then those with a token that
+// needs its log-prob (value 0), then the rest (every token 2), each group in
+// ascending order; order[nblocks] = the first group's size, order[nblocks +
+// 1] = the first two groups' size.
 __global__ __launch_bounds__(1024) void lm_block_order_kernel(int32_t n, const uint8_t* need,
                                                               int32_t* order) {
   __shared__ int32_t wcount[16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int32_t nblocks = (n + kBM - 1) / kBM;
   int32_t base = 0;
-  for (int pass = 0; pass < 2; ++pass) {
+  for (int pass = 0; pass < 3; ++pass) {
     for (int32_t c0 = 0; c0 < nblocks; c0 += 1024) {
       const int32_t blk = c0 + tid;
-      bool any = false;
+      bool obar = false, live = false;  // a value 1; a value other than 2
       if (blk < nblocks) {
         const int32_t b = blk * kBM, e = n - b < kBM ? n : b + kBM;
         if (e - b == kBM && ((uintptr_t)(need + b) & 15) == 0) {
@@ -903,13 +923,19 @@ __global__ __launch_bounds__(1024) void lm_block_order_kernel(int32_t n, const u
 #pragma unroll
           for (int i = 0; i < kBM / 16; ++i) {
             const uint4 v = q[i];
-            any |= (v.x | v.y | v.z | v.w) != 0u;
+            obar |= ((v.x | v.y | v.z | v.w) & 0x01010101u) != 0u;
+            live |= ((v.x ^ 0x02020202u) | (v.y ^ 0x02020202u) | (v.z ^ 0x02020202u) |
+                     (v.w ^ 0x02020202u)) != 0u;
           }
         } else {
-          for (int32_t i = b; i < e; ++i) any |= need[i] != 0;
+          for (int32_t i = b; i < e; ++i) {
+            obar |= (need[i] & 1) != 0;
+            live |= need[i] != 2;
+          }
         }
       }
-      const bool take = blk < nblocks && any == (pass == 0);
+      const int grp = obar ? 0 : (live ? 1 : 2);
+      const bool take = blk < nblocks && grp == pass;
       const uint64_t bal = __builtin_amdgcn_ballot_w64(take);
       if (lane == 0) wcount[wv] = __popcll(bal);
       __syncthreads();
@@ -922,7 +948,7 @@ __global__ __launch_bounds__(1024) void lm_block_order_kernel(int32_t n, const u
       base = total;
       __syncthreads();
     }
-    if (pass == 0 && tid == 0) order[nblocks] = base;  // blocks that need obar
+    if (pass < 2 && tid == 0) order[nblocks + pass] = base;
   }
 }
 
@@ -1123,8 +1149,9 @@ extern "C" int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t d
   RRL_REQUIRE(workspace != nullptr && ((uintptr_t)workspace & 15) == 0, RRL_EINVAL,
               "lm head: need_obar requires a 16-byte aligned workspace of "
               "rrl_lm_head_fwd_workspace_bytes(N) bytes");
-  // Blocks that need obar (listed first) take the obar pass, the others the
-  // log-sum-exp pass, in one launch.
+  // Blocks that need obar (listed first) take the obar pass, those that need
+  // log-probs the log-sum-exp pass, in one launch; blocks that need neither
+  // get zeros.
   int32_t* order = static_cast<int32_t*>(workspace);
   hipLaunchKernelGGL(lm_block_order_kernel, dim3(1), dim3(1024), 0, st, (int32_t)N, need_obar,
                      order);
@@ -1136,7 +1163,7 @@ extern "C" int rrl_lm_head_fwd(const void* hidden, const void* weight, int32_t d
 
 extern "C" size_t rrl_lm_head_fwd_workspace_bytes(int64_t N) {
   if (N <= 0) return 0;
-  return (size_t)(((N + kBM - 1) / kBM + 1) * 4 + 255) / 256 * 256;
+  return (size_t)(((N + kBM - 1) / kBM + 2) * 4 + 255) / 256 * 256;
 }
 
 // Workspace of rrl_lm_head_dweight: 16-byte token records, then the tile

@@ -168,7 +168,8 @@ class _LinearLogprobs(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, check: nat.RrlPolicyParams, hidden: Tensor, weight: Tensor,
-                target_ids: Tensor, weight_mask: Optional[Tensor] = None):
+                target_ids: Tensor, weight_mask: Optional[Tensor] = None,
+                skip_masked: bool = False):
         dev = nat.require_device(hidden, weight, target_ids)
         B, T = _prepare(hidden, weight, target_ids)
         _check_mfma(hidden)
@@ -186,10 +187,16 @@ class _LinearLogprobs(torch.autograd.Function):
                  nat.stream_ptr(dev))
         need = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
         # Tokens whose mask weight is zero get d loss / d logp = 0 from every
-        # objective here, so their obar (the d hidden term) is never read.
+        # objective here, so their obar (the d hidden term) is never read;
+        # with skip_masked their log-probs are not needed either (value 2: a
+        # block of 64 such tokens is not computed, its log-probs are 0).
         need_rows = None
         if need and weight_mask is not None:
-            need_rows = (weight_mask.reshape(N) != 0).to(torch.uint8).contiguous()
+            live = weight_mask.reshape(N) != 0
+            if skip_masked:
+                need_rows = torch.where(live, 1, 2).to(torch.uint8).contiguous()
+            else:
+                need_rows = live.to(torch.uint8).contiguous()
         lse, logp, obar, flags = lm_head_forward(h2, w, tgt32, need, status, need_rows)
         if flags & nat.FLAG_TARGET_RANGE:
             L._raise_flags(nat.FLAG_TARGET_RANGE, check.kind)
@@ -202,11 +209,12 @@ class _LinearLogprobs(torch.autograd.Function):
     def backward(ctx, g):
         need_h, need_w = ctx.needs_input_grad[1], ctx.needs_input_grad[2]
         if g is None or not (need_h or need_w):
-            return None, None, None, None, None
+            return None, None, None, None, None, None
         h2, w, tgt32, lse, logp, obar = ctx.saved_tensors
         gc = g.reshape(-1).to(torch.float32).contiguous()
         dh, dw = lm_head_backward(h2, w, tgt32, lse, logp, obar, gc, need_h, need_w)
-        return None, (dh.view(ctx.hidden_shape) if dh is not None else None), dw, None, None
+        return (None, (dh.view(ctx.hidden_shape) if dh is not None else None), dw, None, None,
+                None)
 
 
 def linear_token_logprobs(hidden: Tensor, weight: Tensor, target_ids: Tensor, *,
@@ -267,9 +275,12 @@ def fused_linear_policy_loss(
     is differentiable into ``hidden`` and ``weight``.  The log-probs come from
     the matrix-core LM head (:func:`linear_token_logprobs`) and feed the
     objective's kernels; its backward hands d loss / d logp back to the LM
-    head's backward.  ``skip_masked_rows`` is not provided here: every token's
-    log-prob is formed (the reference's semantics).  ``row_block`` is accepted
-    and unused.
+    head's backward.  ``skip_masked_rows=True`` (a training step, with
+    gradients asked for) leaves out every block of 64 consecutive tokens whose
+    mask weights are all 0: their log-probs are taken as 0, which a masked
+    token's term multiplies by 0, so the loss and the gradients are those of
+    the full computation, without the log-sum-exp pass over those blocks (no
+    reference counterpart).  ``row_block`` is accepted and unused.
     """
 
     if objective not in L._OBJECTIVES:
@@ -280,15 +291,13 @@ def fused_linear_policy_loss(
     if skip_masked_rows and return_logprobs:
         raise ValueError("skip_masked_rows=True leaves masked log-probs uncomputed; "
                          "it cannot be combined with return_logprobs=True")
-    if skip_masked_rows:
-        raise ValueError("skip_masked_rows=True is not provided by the LM-head path: it forms "
-                         "every token's log-prob")
     if row_block < 1:
         raise ValueError("row_block must be positive")
     mask = L._on_device(action_mask, hidden)
     ppo = L._params(nat.OBJ_PPO)
     if kind in (nat.OBJ_GSPO, nat.OBJ_GSPO_TOKEN):
-        logp = _LinearLogprobs.apply(ppo, hidden, weight, target_ids, mask)
+        logp = _LinearLogprobs.apply(ppo, hidden, weight, target_ids, mask,
+                                     bool(skip_masked_rows))
         fn = L.gspo_policy_loss if kind == nat.OBJ_GSPO else L.gspo_token_policy_loss
         out = fn(logp, old_logprobs, advantages, action_mask, clip_low=clip_low,
                  clip_high=clip_low if clip_high is None else clip_high,
@@ -299,7 +308,7 @@ def fused_linear_policy_loss(
                               clip_low=clip_low, clip_high=clip_high,
                               max_log_ratio=max_log_ratio, detach_ratio=detach_ratio,
                               tau_positive=tau_positive, tau_negative=tau_negative)
-    logp = _LinearLogprobs.apply(ppo, hidden, weight, target_ids, mask)
+    logp = _LinearLogprobs.apply(ppo, hidden, weight, target_ids, mask, bool(skip_masked_rows))
     obj, d1, d2, d3, _seq, trusted = L._objective(p, logp, old_logprobs, advantages, mask)
     out = L._token_local_output(kind, obj, d1, d2, d3, trusted)
     return (out, _cfg.as_reference_dtype(logp.detach(), hidden)) if return_logprobs else out

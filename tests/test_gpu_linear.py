@@ -22,6 +22,7 @@ backward products, as the reference's bf16 autograd rounds them.  Bars:
 
 from __future__ import annotations
 
+import dataclasses
 import math
 
 import pytest
@@ -282,6 +283,88 @@ def test_fused_linear_masked_blocks_interleaved(device):
     _product_check(hd.grad.reshape(-1, H), dl, w, "dhidden", transpose=False)
     _product_check(wd.grad, dl, h.reshape(-1, H), "dweight", transpose=True)
     assert bool((hd.grad.reshape(-1, H)[~mask.reshape(-1).to(device)] == 0).all())
+
+
+@pytest.mark.parametrize("objective", ["clipped", "gspo", "sapo"])
+def test_fused_linear_skip_masked_rows(device, objective):
+    """skip_masked_rows=True leaves out the 64-token blocks whose tokens are
+    all masked: the loss, its diagnostics and both gradients are bit-identical
+    to the full computation (a masked token's term is multiplied by 0)."""
+
+    B, T, H, V = 8, 192, 256, 4099
+    h, w, x, t, old, adv, _mask = _inputs(49, B, T, H, V)
+    lengths = torch.tensor([64, 192, 0, 130, 1, 65, 128, 0])
+    mask = torch.arange(T)[None, :] < lengths[:, None]
+    if objective == "gspo":
+        adv = adv[:, 0].contiguous()
+    if objective in ("gspo", "sapo"):
+        mask[2, 0] = mask[7, 0] = True  # per-sequence means need a token in every sequence
+    d = lambda z: z.to(device)  # noqa: E731
+    res = []
+    for skip in (False, True):
+        hd = h.to(device).requires_grad_()
+        wd = w.to(device).requires_grad_()
+        out = R.fused_linear_policy_loss(hd, wd, d(t), d(old), d(adv), d(mask),
+                                         objective=objective, skip_masked_rows=skip,
+                                         **KW[objective])
+        out.loss.backward()
+        res.append((out, hd.grad, wd.grad))
+    (o0, h0, w0), (o1, h1, w1) = res
+    for f in dataclasses.fields(o0):
+        a, b = getattr(o0, f.name), getattr(o1, f.name)
+        if isinstance(a, torch.Tensor):
+            assert torch.equal(a, b), f.name
+    assert torch.equal(h0, h1) and torch.equal(w0, w1)
+
+
+def test_lm_head_fwd_blocks_needing_nothing(device):
+    """The forward's per-token need values through the C ABI: a block whose
+    64 tokens are all 2 gets lse = logp = 0 without being computed; a block
+    with a 1 takes the obar pass and one with only 0s and 2s the
+    log-sum-exp pass, both giving every token of the block its lse and logp
+    (those of an obar-less call, within float32 rounding of the two passes)."""
+
+    from rosellm_amd import _native as nat
+
+    N, H, V = 640, 256, 4099
+    h, w, _x, t, *_ = _inputs(50, 2, N // 2, H, V)
+    hd, wd = h.reshape(N, H).to(device), w.to(device)
+    t32 = t.reshape(N).to(torch.int32).to(device)
+    # blocks: obar / lse / skip / obar / skip / lse / skip / skip / lse / obar
+    kinds = [1, 0, 2, 1, 2, 0, 2, 2, 0, 1]
+    need = torch.full((N,), 2, dtype=torch.uint8)
+    for b, k in enumerate(kinds):
+        if k == 1:
+            need[64 * b + 5] = 1  # one token needs obar, the rest nothing
+        elif k == 0:
+            need[64 * b:64 * b + 64:7] = 0  # some need log-probs, the rest nothing
+    need_d = need.to(device)
+    st = nat.new_status(device)
+    dt = nat.dtype_code(torch.bfloat16)
+    s = nat.stream_ptr(device)
+    ref_lse = torch.empty(N, device=device)
+    ref_lp = torch.empty(N, device=device)
+    nat.call("rrl_lm_head_fwd", hd.data_ptr(), wd.data_ptr(), dt, N, H, V, H, H, t32.data_ptr(),
+             None, None, ref_lse.data_ptr(), ref_lp.data_ptr(), None, H, None, st.data_ptr(), s)
+    lse = torch.full((N,), float("nan"), device=device)
+    lp = torch.full((N,), float("nan"), device=device)
+    obar = torch.empty(N, H, device=device)
+    ws = torch.empty(nat.lib().rrl_lm_head_fwd_workspace_bytes(N), dtype=torch.uint8,
+                     device=device)
+    nat.call("rrl_lm_head_fwd", hd.data_ptr(), wd.data_ptr(), dt, N, H, V, H, H, t32.data_ptr(),
+             need_d.data_ptr(), None, lse.data_ptr(), lp.data_ptr(), obar.data_ptr(), H,
+             ws.data_ptr(), st.data_ptr(), s)
+    assert nat.read_status(st) == 0
+    order = ws[:4 * (len(kinds) + 2)].view(torch.int32).cpu().tolist()
+    # obar blocks, then log-prob-only blocks, then the rest; then the counts
+    assert order == [0, 3, 9, 1, 5, 8, 2, 4, 6, 7, 3, 6]
+    for b, k in enumerate(kinds):
+        sl = slice(64 * b, 64 * b + 64)
+        if k == 2:
+            assert bool((lse[sl] == 0).all()) and bool((lp[sl] == 0).all()), b
+        else:
+            assert torch.allclose(lse[sl], ref_lse[sl], rtol=1e-6, atol=1e-5), b
+            assert torch.allclose(lp[sl], ref_lp[sl], rtol=1e-5, atol=1e-5), b
 
 
 def test_strided_hidden_and_target_errors(device):

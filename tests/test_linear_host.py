@@ -31,8 +31,6 @@ def test_validation_messages():
                                    return_logprobs=True)
     with pytest.raises(ValueError, match="row_block must be positive"):
         R.linear_token_logprobs(h, w, t, row_block=0)
-    with pytest.raises(ValueError, match="not provided by the LM-head path"):
-        R.fused_linear_policy_loss(h, w, t, z, z, z.bool(), skip_masked_rows=True)
 
 
 def test_no_cpu_fallback():
@@ -42,5 +40,7 @@ def test_no_cpu_fallback():
     z = torch.zeros(2, 3)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         R.fused_linear_policy_loss(h, w, t, z, z, z.bool())
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        R.fused_linear_policy_loss(h, w, t, z, z, z.bool(), skip_masked_rows=True)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         R.linear_token_logprobs(h, w, t)
