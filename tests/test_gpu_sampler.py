@@ -255,6 +255,53 @@ def test_block_sums_against_far_references(device, case, do_sample):
             assert torch.equal(out.token_ids.cpu(), torch.argmax(x.float(), dim=-1))
 
 
+# (seed, row) pairs at offset 0 whose component uniform u1 lies below
+# V * 1e-9 for V = 8192, found by a search over seeds with the oracle's Philox.
+FLOOR_HITS = [(9715, 7), (15203, 4), (38829, 0)]
+
+
+@pytest.mark.parametrize("seed,row", FLOOR_HITS)
+@pytest.mark.parametrize("layout", ["resident", "streamed"])
+def test_floor_excess_component(device, seed, row, layout):
+    """The rare side of the mixture: rows whose component uniform falls below
+    V * 1e-9, where the kernels total the floor's excess G and draw from
+    max(1e-9 - p, 0) when u1 < G / (1 + G).  Row `row` is made almost
+    entirely floored (a spike of +30 over N(0, 1): G = (V - 1) 1e-9, the
+    excess is drawn), then half floored (4095 entries at 12, 4096 near 0:
+    G = 4096e-9, so u1 of the first two seeds lies between G / (1 + G) and
+    V * 1e-9 and p is drawn after all).  Both kernels against the oracle;
+    the excess's weights are near-uniform over thousands of entries, so the
+    decisions are far from any boundary."""
+
+    V, B = 8192, 16
+    u, u1 = so.row_uniforms(seed, 0, row)
+    assert u1 < V * 1e-9
+    g = torch.Generator().manual_seed(seed)
+    for shape in ("floored", "half"):
+        x = torch.randn(B, V, generator=g) * 3.0
+        x[row] = torch.randn(V, generator=g)
+        if shape == "half":
+            x[row, : V // 2] += 12.0
+        x[row, 1234] = 30.0
+        x = x.to(torch.bfloat16)
+        p = torch.softmax(x[row].double(), dim=0).numpy()
+        _, gx, pi = so.mixture_parts(p)
+        print(f"[sampler] floor excess seed={seed} row={row} {layout} {shape}: u1={u1:.3e} "
+              f"G/(1+G)={pi:.3e}", flush=True)
+        xd = x.to(device)
+        if layout == "streamed":  # one element off a 16-byte boundary
+            wide = torch.zeros(B, V + 8, dtype=x.dtype, device=device)
+            wide[:, 1:V + 1] = xd
+            xd = wide[:, 1:V + 1]
+        kw = dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=True)
+        out = RI.sample_next_token_batch(xd, seed=seed, offset=0, **kw)
+        tok = _check(x, out, seed=seed, offset=0, what=f"floor {shape} {layout}", **kw)
+        want = so.sample_rows(x.float().numpy(), seed=seed, offset=0, **kw)
+        assert want["margin"][row] > MARGIN
+        # the excess was drawn exactly when u1 < G / (1 + G): a floored token
+        assert (gx[tok[row]] > 0) == (u1 < pi), (shape, tok[row], u1, pi)
+
+
 @pytest.mark.parametrize("kw", [
     dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=True),
     dict(temperature=0.7, top_k=50, top_p=0.9, do_sample=True),
