@@ -7,13 +7,18 @@
 //
 // Row layout: slab k, lane j holds elements (k*1024 + j)*VEC .. +VEC-1 (VEC =
 // 16 bytes of logits), so every pass moves the row with coalesced 16-byte
-// loads, and vocabulary order is (slab, lane, element).  Two kernels:
-//   * sample_resident_kernel (plain sampling, greedy decoding and top-k with
-//     or without top-p, of 16-bit rows made of whole, aligned 16-byte
-//     vectors): the row stays in VGPRs and is read from memory once; its
-//     sweeps are described at its definition.
+// loads, and vocabulary order is (slab, lane, element).  Three kernels:
+//   * sample_blocks_kernel (plain sampling and greedy decoding) and
+//     sample_resident_kernel (top-k with or without top-p), both for 16-bit
+//     rows made of whole, aligned 16-byte vectors: the row stays in VGPRs
+//     and is read from memory once; their sweeps are described at their
+//     definitions.
 //   * sample_kernel (everything else): a row is re-read per pass (from L2 /
 //     the memory-side cache: a 151936-entry bf16 row is 297 KB).
+// Without top-k / top-p, max(p, 1e-9) is drawn as the mixture of p
+// (probability 1 / (1 + G)) and the floor's excess max(1e-9 - p, 0)
+// (probability G / (1 + G), G its total), a second uniform choosing the
+// component: (1 / (1 + G)) p + (G / (1 + G)) (g / G) = max(p, 1e-9) / (1 + G).
 //
 // sample_kernel's passes (top-k, top-p and the tie searches only when active):
 //   1. row max and its lowest index (greedy choice), the sums of
@@ -23,8 +28,9 @@
 //   3. Z = sum over the candidates of exp(x/T - max);
 //   4. top-p: radix select over fixed-point probability mass (exact,
 //      order-independent integer sums), descending key order;
-//   5. inverse CDF in vocabulary order: per-slab totals, then a lane scan
-//      inside the chosen slab;
+//   5. inverse CDF in vocabulary order (of the chosen mixture component
+//      without top-k / top-p): per-slab totals, then a lane scan inside the
+//      chosen slab;
 //   6. the token's log-prob in the form the training row kernels use
 //      (finish_row), from pass 1's sums.
 // Greedy decoding is pass 1 alone; sampling without top-k / top-p is passes 1
