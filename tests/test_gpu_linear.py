@@ -238,6 +238,37 @@ def test_logits_beyond_the_reference_range_rerun(device):
     _product_check(wd.grad, dl, h.reshape(-1, H), "dweight", transpose=True)
 
 
+def test_range_rerun_with_skipped_blocks(device):
+    """The rerun around the exact log-sum-exp (a logit far beyond the single
+    pass's reference range) with skip_masked_rows: the rerun keeps the
+    skipped blocks out too, and the loss and both gradients equal the full
+    computation's bit for bit."""
+
+    B, T, H, V = 4, 128, 256, 2048
+    h, w, _x, t, old, adv, _mask = _inputs(45, B, T, H, V)
+    w[1000] = (h[0, 0].float() * 0.6).to(torch.bfloat16)  # token (0, 0): logit ~ 150
+    x = h.double() @ w.double().t()
+    assert float(x[0, 0].max() - x[0, 0, :32].max()) > 100.0
+    lengths = torch.tensor([128, 0, 64, 5])  # blocks of 64: 2 live, 2 masked, 1 + 1, 1 + 1
+    mask = torch.arange(T)[None, :] < lengths[:, None]
+    d = lambda z: z.to(device)  # noqa: E731
+    res = []
+    for skip in (False, True):
+        hd = h.to(device).requires_grad_()
+        wd = w.to(device).requires_grad_()
+        out = R.fused_linear_policy_loss(hd, wd, d(t), d(old), d(adv), d(mask),
+                                         objective="clipped", skip_masked_rows=skip,
+                                         **KW["clipped"])
+        out.loss.backward()
+        res.append((out.loss, hd.grad, wd.grad))
+    (l0, h0, w0), (l1, h1, w1) = res
+    assert torch.equal(l0, l1) and torch.equal(h0, h1) and torch.equal(w0, w1)
+    out_o, _lpo, _dho, _dwo = o.lm_head_step("ppo", h, w, x, t, old, adv, mask, exact=True,
+                                             **KW["clipped"])
+    scale = max(abs(out_o["loss"].item()), adv.abs().mean().item())
+    assert abs(l0.item() - out_o["loss"].item()) <= 2e-3 * scale
+
+
 @pytest.mark.parametrize("H,V,B,T,hot", [(1024, 8256, 3, 67, 0.0), (128, 33, 2, 32, 0.0),
                                          (384, 1000, 2, 129, 0.0), (768, 2050, 2, 1, 0.0),
                                          (256, 4096, 4, 64, 0.8)])
