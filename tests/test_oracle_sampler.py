@@ -133,6 +133,48 @@ def test_mixture_rule_draws_the_floored_weights(p):
         assert tok == so.inverse_cdf(g if u1 < pi else rho, 0.5)[0]
 
 
+def _grid_freq(p, rule, n=4000):
+    """Frequencies of a two-component rule (weights a, b, probability of a)
+    integrated over a grid of both uniforms."""
+
+    p = np.asarray(p, dtype=np.float64)
+    grid = (np.arange(n) + 0.5) / n
+    a, b, pa = rule(p)
+    freq = np.zeros(p.size)
+    for comp, share in ((a, pa), (b, 1.0 - pa)):
+        if share > 0.0:
+            toks = np.array([so.inverse_cdf(comp, u)[0] for u in grid])
+            freq += share * np.bincount(toks, minlength=p.size) / n
+    return freq
+
+
+@pytest.mark.parametrize("mistake", ["swapped components", "pi of p", "no floor excess"])
+def test_mixture_check_catches_planted_mistakes(mistake):
+    """The frequency check of the mixture rule fails for plausible mistakes
+    planted in the rule (on the CPU): the excess drawn with p's probability,
+    the components' probabilities taken as S / (S + G), or the excess
+    dropped."""
+
+    p = np.array([5e-10, 2e-10, 3e-9, 1e-10, 0.0, 4e-9])
+    want = np.maximum(p, 1e-9) / np.maximum(p, 1e-9).sum()
+
+    def right(p):
+        rho, g, pi = so.mixture_parts(p)
+        return g, rho, pi
+
+    def wrong(p):
+        rho, g, pi = so.mixture_parts(p)
+        if mistake == "swapped components":
+            return rho, g, pi
+        if mistake == "pi of p":
+            return g, rho, 1.0 - pi
+        return g, rho, 0.0
+
+    tol = 2.0 / 4000
+    assert np.allclose(_grid_freq(p, right), want, atol=tol)
+    assert not np.allclose(_grid_freq(p, wrong), want, atol=tol)
+
+
 def test_inverse_cdf_edges():
     # the target lands on a boundary: the next entry with positive weight
     w = np.array([0.25, 0.0, 0.25, 0.5])
