@@ -47,10 +47,10 @@ wall clock over the timed steps; the median of the per-step event times is
 beside it), ``roofline`` for the dominant kernel (HIP events around its
 entry point over a second pass of the timed steps; algorithmic bytes
 N*(V*(2+2) + 21) for the row kernels) and ``cpu_baseline``: the oracle's
-PyTorch-CPU composition timed on the sub-batch BASELINE's CPU plan names
-(C1 whole, C2/C3/SFT 16 sequences = 2 groups of 8, C4 2 x 8192, C5 16
-sequences), with the same sub-batch run through the HIP path in the same run
-as its parity batch.
+PyTorch-CPU composition timed on a self-contained sub-batch (C1 whole,
+C2/C3/SFT 16 sequences = 2 groups of 8, C4 2 x 8192, C5 16 sequences), with
+the same sub-batch run through the HIP path in the same run as its parity
+batch.
 """
 
 from __future__ import annotations
