@@ -995,8 +995,9 @@ int launch_sample(const SampleArgs& a, hipStream_t st) {
 //      maximum, Z and the lowest-index argmax;
 //   K. the k-th largest lane maximum t0 (a radix select over the 1024 lane
 //      maxima), every entry >= t0 gathered into the LDS list, the exact k-th
-//      key on the list, then list_draw (ties, top-p, the draw); a row whose
-//      list overflows gets token -1 for sample_kernel's fill-in launch;
+//      key on the list, then list_draw (ties, top-p, the draw), by wave 0
+//      alone (wave_list_draw) when the list holds at most 64 entries; a row
+//      whose list overflows gets token -1 for sample_kernel's fill-in launch;
 //   C. the sampled token's S_other: for the argmax, the sum over every other
 //      entry relative to the row maximum, formed by the argmax lane's wave
 //      (the other lanes' sweep-A sums, the argmax lane's entries shared out
@@ -1067,6 +1068,184 @@ __device__ __forceinline__ uint32_t block_kth_key16(uint32_t key, bool valid, in
   return prefix;
 }
 
+// A value known to be the same in every active lane, moved to scalar
+// registers (the compiler cannot prove values read back from LDS uniform,
+// and the register-resident kernels have no vector registers to spare).
+__device__ __forceinline__ float uni(float v) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ double uni(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)b);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(b >> 32));
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// DPP row shift right by N lanes of a float64 (both halves moved alike); a
+// lane whose source lies before its row's start reads 0.
+template <int N>
+__device__ __forceinline__ double row_shr_d(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo =
+      (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)b, 0x110 + N, 0xF, 0xF, true);
+  const unsigned hi =
+      (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), 0x110 + N, 0xF, 0xF, true);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// Inclusive prefix sums of v within each row of 16 lanes.
+__device__ __forceinline__ double row_scan_d(double v) {
+  v += row_shr_d<1>(v);
+  v += row_shr_d<2>(v);
+  v += row_shr_d<4>(v);
+  v += row_shr_d<8>(v);
+  return v;
+}
+
+// Inclusive and exclusive float64 prefix sums over the wave in lane order,
+// and the total.  Each lane's exclusive value is the previous lane's
+// inclusive one (the same operands, the same operation), so the ranges
+// [excl, incl) of consecutive lanes tile [0, total).
+__device__ __forceinline__ void wave_scan_d(double v, double& incl, double& excl, double& total) {
+  const int lane = threadIdx.x & 63, row = lane >> 4;
+  const double in = row_scan_d(v);
+  const double pin = row_shr_d<1>(in);  // the previous lane's, 0 at a row start
+  const double o1 = readlane_d(in, 15);
+  const double o2 = o1 + readlane_d(in, 31);
+  const double o3 = o2 + readlane_d(in, 47);
+  const double off = row == 0 ? 0.0 : (row == 1 ? o1 : (row == 2 ? o2 : o3));
+  incl = row == 0 ? in : off + in;
+  excl = (lane & 15) == 0 ? off : (row == 0 ? pin : off + pin);
+  total = o3 + readlane_d(in, 63);
+}
+
+// The lane whose range [base + excl, base + incl) of weight w > 0 holds
+// target, else (rounding left target at or past the end) the last lane with
+// w > 0, else -1; start = that lane's base + excl.
+__device__ __forceinline__ int wave_claim(double w, double lo, double hi, double target,
+                                          double& start) {
+  const unsigned long long hit = __ballot(w > 0.0 && lo <= target && target < hi);
+  const unsigned long long pos = __ballot(w > 0.0);
+  const int l = hit ? __builtin_ctzll(hit) : (pos ? 63 - __builtin_clzll(pos) : -1);
+  start = l >= 0 ? readlane_d(lo, l) : 0.0;
+  return l;
+}
+
+// list_draw for a list of n <= 64 entries, by the calling wave alone (one
+// entry per lane, no workgroup barrier), with the exact k-th key (k = kq)
+// found on the list first: every entry whose key is above the k-th key and
+// the first need_k at it, lowest index first, are the candidates.  The same
+// rules as the k-th key search and list_draw: ranks and counts come from a
+// loop over the list's lanes (readlane), the entries are put in index order
+// through LDS (this wave's own accesses, in order), Z and the inverse CDF
+// scan run over the wave (wave_sum_dpp, wave_scan_d), and top-p takes the
+// threshold group from exact integer sums.  Every lane returns the token,
+// log q(token) and the token's stored bits.
+template <class Tag>
+__device__ __forceinline__ void wave_list_draw(CandShared& cs, int n, int kq, bool use_p,
+                                               double top_p, float iT, float m,
+                                               uint32_t max_key, double u01, int& tok,
+                                               float& logq, uint32_t& tok_bits) {
+  constexpr int KB = Bits<Tag>::KB;
+  const int lane = threadIdx.x & 63;
+  const bool have = lane < n;
+  const int e0 = have ? cs.idx[lane] : 0x7fffffff;
+  const uint32_t b0 = have ? cs.bits[lane] : 0u;
+  const uint32_t k0 = float_key<KB>(b0);
+  // Rank by vocabulary index (indices are distinct), and the counts of keys
+  // above and equal to this entry's.
+  int rank = 0, gt = 0, eq = 0;
+  for (int j = 0; j < n; ++j) {
+    const int ej = __builtin_amdgcn_readlane(e0, j);
+    const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)k0, j);
+    rank += ej < e0 ? 1 : 0;
+    gt += kj > k0 ? 1 : 0;
+    eq += kj == k0 ? 1 : 0;
+  }
+  // The k-th key: an entry with fewer than k keys above it and at least k at
+  // or above it (every such entry has the same key and counts).
+  const unsigned long long kh = __ballot(have && gt < kq && kq <= gt + eq);
+  const int kl = kh ? __builtin_ctzll(kh) : 0;
+  const uint32_t kth = (uint32_t)__builtin_amdgcn_readlane((int)k0, kl);
+  const int need_k = kq - __builtin_amdgcn_readlane(gt, kl);
+  if (have) {
+    cs.sidx[rank] = e0;
+    cs.sbits[rank] = b0;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const int se = have ? cs.sidx[lane] : 0;
+  const uint32_t sb = have ? cs.sbits[lane] : 0u;
+  const uint32_t sk = float_key<KB>(sb);
+  const unsigned long long below = (1ull << lane) - 1ull;
+  const bool tie = have && sk == kth;
+  const int tie_rank = __popcll(__ballot(tie) & below);
+  const bool cand = have && (sk > kth || (tie && tie_rank < need_k));
+  const unsigned long long cmask = __ballot(cand);
+  // Z over the candidates, with the general path's exp(x/T - m).
+  const float ev = cand ? expf(Bits<Tag>::val(sb) * iT - m) : 0.0f;
+  const float pc = ev * (1.0f / wave_sum_dpp(ev));
+  bool keep = true;
+  if (use_p) {
+    // The threshold group: the first key, in descending order, whose
+    // inclusive fixed-point mass passes P (the row maximum is always kept);
+    // ties in it are kept lowest index first.
+    const unsigned long long P = (unsigned long long)(top_p * kMassScale);
+    const unsigned long long mass = cand ? (unsigned long long)((double)pc * kMassScale) : 0ull;
+    unsigned long long A = 0, Ms = 0;
+    int C = 0, tr = 0;
+    for (int j = 0; j < n; ++j) {
+      if ((cmask >> j) & 1ull) {
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)sk, j);
+        const unsigned long long mj =
+            ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(mass >> 32), j) << 32) |
+            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mass, j);
+        const bool same = kj == sk;
+        A += kj > sk ? mj : 0ull;
+        Ms += same ? mj : 0ull;
+        C += same ? 1 : 0;
+        tr += (same && j < lane) ? 1 : 0;
+      }
+    }
+    const unsigned long long fh = __ballot(cand && Ms > 0 && A <= P && P < A + Ms);
+    if (fh) {
+      const int fl = __builtin_ctzll(fh);
+      const uint32_t pth = (uint32_t)__builtin_amdgcn_readlane((int)sk, fl);
+      const unsigned long long A0 =
+          ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(A >> 32), fl) << 32) |
+          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)A, fl);
+      const unsigned long long M0 =
+          ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(Ms >> 32), fl) << 32) |
+          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)Ms, fl);
+      const unsigned long long C0 = (unsigned long long)__builtin_amdgcn_readlane(C, fl);
+      const unsigned long long each = M0 / C0;  // equal keys, equal mass
+      unsigned long long n_keep = each > 0 ? (P - A0) / each : C0;
+      if (pth == max_key && n_keep == 0) n_keep = 1;
+      keep = sk > pth ||
+             (sk == pth && (n_keep >= C0 || (n_keep > 0 && (unsigned long long)tr < n_keep)));
+    }
+  }
+  // Inverse CDF over the candidates in vocabulary order; the last candidate
+  // takes a target that rounding leaves past the end.
+  const float wf = cand ? fmaxf(keep ? pc : 0.0f, 1e-9f) : 0.0f;
+  double incl, excl, tot;
+  wave_scan_d((double)wf, incl, excl, tot);
+  const double tgt = u01 * tot;
+  double start;
+  const int pl = wave_claim((double)wf, excl, incl, tgt, start);
+  tok = __builtin_amdgcn_readlane(se, pl);
+  tok_bits = (uint32_t)__builtin_amdgcn_readlane((int)sb, pl);
+  const float wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wf), pl));
+  logq = (float)(log((double)wp) - log(tot));
+}
+
 template <class Tag, int SL>
 __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   static_assert(Tag::VEC == 8, "16-bit rows");
@@ -1078,6 +1257,9 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   __shared__ float sh_m[SWAVES], sh_s[SWAVES];
   __shared__ int sh_i[SWAVES];
   __shared__ u32x4 arg_row[SL];  // the argmax lane's registers (sweep C)
+  __shared__ int sh_tok;         // a short list's draw (wave_list_draw)
+  __shared__ float sh_logq;
+  __shared__ uint32_t sh_bits;
 
   const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1226,6 +1408,28 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
     if (tid == 0) a.token[r] = -1;
     return;
   }
+  const bool use_p = a.top_p > 0.0 && a.top_p < 1.0;
+  const uint32_t max_key = float_key<KB>(Bits<Tag>::bits_of(M));
+  uint32_t tok_bits;
+  if (n <= 64) {
+    // A list of one wave's size (top-k up to a few dozen, as usual): wave 0
+    // finishes it alone, without workgroup barriers.
+    if (wave == 0) {
+      int t;
+      float q;
+      uint32_t tb;
+      wave_list_draw<Tag>(cs, n, kq, use_p, a.top_p, iT, M * iT, max_key, u01, t, q, tb);
+      if (lane == 0) {
+        sh_tok = t;
+        sh_logq = q;
+        sh_bits = tb;
+      }
+    }
+    __syncthreads();
+    tok = sh_tok;
+    logq = sh_logq;
+    tok_bits = sh_bits;
+  } else {
   // The exact k-th key: the entry with fewer than k keys above it and at
   // least k at or above it (every such entry writes the same values).
   if (tid < n) {
@@ -1242,9 +1446,9 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
     }
   }
   __syncthreads();
-  uint32_t tok_bits;
-  list_draw<Tag>(cs, sh_z, n, sh_kth, sh_need, a.top_p > 0.0 && a.top_p < 1.0, a.top_p, iT,
-                 M * iT, float_key<KB>(Bits<Tag>::bits_of(M)), u01, tok, logq, tok_bits);
+  list_draw<Tag>(cs, sh_z, n, sh_kth, sh_need, use_p, a.top_p, iT, M * iT, max_key, u01, tok,
+                 logq, tok_bits);
+  }
   const float xt_raw = Bits<Tag>::val(tok_bits);
 
   // C. S_other of the token and its log-prob, by the wave holding it.
@@ -1282,76 +1486,6 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   }
 }
 
-
-// A value known to be the same in every active lane, moved to scalar
-// registers (the compiler cannot prove values read back from LDS uniform,
-// and the register-resident kernels have no vector registers to spare).
-__device__ __forceinline__ float uni(float v) {
-  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
-}
-__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ double uni(double v) {
-  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
-  const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)b);
-  const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(b >> 32));
-  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
-}
-__device__ __forceinline__ double readlane_d(double v, int l) {
-  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
-  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
-  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
-  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
-}
-
-// DPP row shift right by N lanes of a float64 (both halves moved alike); a
-// lane whose source lies before its row's start reads 0.
-template <int N>
-__device__ __forceinline__ double row_shr_d(double v) {
-  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
-  const unsigned lo =
-      (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)b, 0x110 + N, 0xF, 0xF, true);
-  const unsigned hi =
-      (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), 0x110 + N, 0xF, 0xF, true);
-  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
-}
-
-// Inclusive prefix sums of v within each row of 16 lanes.
-__device__ __forceinline__ double row_scan_d(double v) {
-  v += row_shr_d<1>(v);
-  v += row_shr_d<2>(v);
-  v += row_shr_d<4>(v);
-  v += row_shr_d<8>(v);
-  return v;
-}
-
-// Inclusive and exclusive float64 prefix sums over the wave in lane order,
-// and the total.  Each lane's exclusive value is the previous lane's
-// inclusive one (the same operands, the same operation), so the ranges
-// [excl, incl) of consecutive lanes tile [0, total).
-__device__ __forceinline__ void wave_scan_d(double v, double& incl, double& excl, double& total) {
-  const int lane = threadIdx.x & 63, row = lane >> 4;
-  const double in = row_scan_d(v);
-  const double pin = row_shr_d<1>(in);  // the previous lane's, 0 at a row start
-  const double o1 = readlane_d(in, 15);
-  const double o2 = o1 + readlane_d(in, 31);
-  const double o3 = o2 + readlane_d(in, 47);
-  const double off = row == 0 ? 0.0 : (row == 1 ? o1 : (row == 2 ? o2 : o3));
-  incl = row == 0 ? in : off + in;
-  excl = (lane & 15) == 0 ? off : (row == 0 ? pin : off + pin);
-  total = o3 + readlane_d(in, 63);
-}
-
-// The lane whose range [base + excl, base + incl) of weight w > 0 holds
-// target, else (rounding left target at or past the end) the last lane with
-// w > 0, else -1; start = that lane's base + excl.
-__device__ __forceinline__ int wave_claim(double w, double lo, double hi, double target,
-                                          double& start) {
-  const unsigned long long hit = __ballot(w > 0.0 && lo <= target && target < hi);
-  const unsigned long long pos = __ballot(w > 0.0);
-  const int l = hit ? __builtin_ctzll(hit) : (pos ? 63 - __builtin_clzll(pos) : -1);
-  start = l >= 0 ? readlane_d(lo, l) : 0.0;
-  return l;
-}
 
 // ---------------------------------------------------------------------------
 // Register-resident rows, greedy decoding and sampling without top-k / top-p
