@@ -996,7 +996,8 @@ int launch_sample(const SampleArgs& a, hipStream_t st) {
 //   K. the k-th largest lane maximum t0 (a radix select over the 1024 lane
 //      maxima), every entry >= t0 gathered into the LDS list, the exact k-th
 //      key on the list, then list_draw (ties, top-p, the draw), by wave 0
-//      alone (wave_list_draw) when the list holds at most 64 entries; a row
+//      with the work split for a short list (small_list_draw) when the list holds
+//      at most 64 entries; a row
 //      whose list overflows gets token -1 for sample_kernel's fill-in launch;
 //   C. the sampled token's S_other: for the argmax, the sum over every other
 //      entry relative to the row maximum, formed by the argmax lane's wave
@@ -1138,112 +1139,174 @@ __device__ __forceinline__ int wave_claim(double w, double lo, double hi, double
   return l;
 }
 
-// list_draw for a list of n <= 64 entries, by the calling wave alone (one
-// entry per lane, no workgroup barrier), with the exact k-th key (k = kq)
-// found on the list first: every entry whose key is above the k-th key and
-// the first need_k at it, lowest index first, are the candidates.  The same
-// rules as the k-th key search and list_draw: ranks and counts come from a
-// loop over the list's lanes (readlane), the entries are put in index order
-// through LDS (this wave's own accesses, in order), Z and the inverse CDF
-// scan run over the wave (wave_sum_dpp, wave_scan_d), and top-p takes the
-// threshold group from exact integer sums.  Every lane returns the token,
-// log q(token) and the token's stored bits.
+// Pairwise sums of small_list_draw, entry i (lane i) against partners j of
+// wave w's four (4w .. 4w + 3).
+struct SmallShared {
+  int cnt[SWAVES][64];      // rank by index | keys above << 8 | keys equal << 16
+  uint32_t key[64];         // the candidates in index order: key,
+  double mass[64];          // fixed-point probability (an integer < 2^53; -1: not a candidate)
+  double above[SWAVES][64];  // top-p: mass of the candidates with a larger key,
+  double at[SWAVES][64];     // with the same key,
+  int eqc[SWAVES][64];       // how many with the same key | how many of them before i << 8
+  int tok;
+  float logq;
+  uint32_t bits;
+};
+
+// list_draw for a list of n <= 64 entries (top-k up to a few dozen, as
+// usual), with the exact k-th key (k = kq) found on the list first: every
+// entry whose key is above the k-th key and the first need_k at it, lowest
+// index first, are the candidates.  The rules are list_draw's; the work is
+// laid out for a short list.  Entry i is lane i of every wave, and the
+// pairwise counts (the rank by index, the keys above and equal, then top-p's
+// masses above and at a key, as exact integers in float64) are split over
+// the 16 waves, four partners each.  Wave 0 sums them, puts the entries in
+// index order through LDS, forms Z and the candidates' probabilities over
+// the wave and draws by a float64 scan over the wave: three workgroup
+// barriers and no serial loop over the list.  Every thread returns the
+// token, log q(token) and the token's stored bits.
 template <class Tag>
-__device__ __forceinline__ void wave_list_draw(CandShared& cs, int n, int kq, bool use_p,
-                                               double top_p, float iT, float m,
-                                               uint32_t max_key, double u01, int& tok,
-                                               float& logq, uint32_t& tok_bits) {
+__device__ __forceinline__ void small_list_draw(CandShared& cs, SmallShared& ss, int n, int kq,
+                                                bool use_p, double top_p, float iT, float m,
+                                                uint32_t max_key, double u01, int& tok,
+                                                float& logq, uint32_t& tok_bits) {
   constexpr int KB = Bits<Tag>::KB;
-  const int lane = threadIdx.x & 63;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool have = lane < n;
-  const int e0 = have ? cs.idx[lane] : 0x7fffffff;
-  const uint32_t b0 = have ? cs.bits[lane] : 0u;
-  const uint32_t k0 = float_key<KB>(b0);
-  // Rank by vocabulary index (indices are distinct), and the counts of keys
-  // above and equal to this entry's.
-  int rank = 0, gt = 0, eq = 0;
-  for (int j = 0; j < n; ++j) {
-    const int ej = __builtin_amdgcn_readlane(e0, j);
-    const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)k0, j);
-    rank += ej < e0 ? 1 : 0;
-    gt += kj > k0 ? 1 : 0;
-    eq += kj == k0 ? 1 : 0;
+  {
+    const int e0 = have ? cs.idx[lane] : 0x7fffffff;
+    const uint32_t k0 = float_key<KB>(have ? cs.bits[lane] : 0u);
+    int rank = 0, gt = 0, eq = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = 4 * wave + q;  // wave-uniform
+      if (j < n) {
+        const int ej = __builtin_amdgcn_readlane(e0, j);
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)k0, j);
+        rank += ej < e0 ? 1 : 0;
+        gt += kj > k0 ? 1 : 0;
+        eq += kj == k0 ? 1 : 0;
+      }
+    }
+    ss.cnt[wave][lane] = rank | (gt << 8) | (eq << 16);
   }
-  // The k-th key: an entry with fewer than k keys above it and at least k at
-  // or above it (every such entry has the same key and counts).
-  const unsigned long long kh = __ballot(have && gt < kq && kq <= gt + eq);
-  const int kl = kh ? __builtin_ctzll(kh) : 0;
-  const uint32_t kth = (uint32_t)__builtin_amdgcn_readlane((int)k0, kl);
-  const int need_k = kq - __builtin_amdgcn_readlane(gt, kl);
-  if (have) {
-    cs.sidx[rank] = e0;
-    cs.sbits[rank] = b0;
+  __syncthreads();
+  // Wave 0: the k-th key, the entries in index order, the candidates and
+  // their probabilities.
+  float pc = 0.0f;
+  bool cand = false;
+  int se = 0;
+  uint32_t sb = 0u, sk = 0u;
+  if (wave == 0) {
+    int rank = 0, gt = 0, eq = 0;
+#pragma unroll
+    for (int w = 0; w < SWAVES; ++w) {
+      const int c = ss.cnt[w][lane];
+      rank += c & 255;
+      gt += (c >> 8) & 255;
+      eq += c >> 16;
+    }
+    // The k-th key: an entry with fewer than k keys above it and at least
+    // k at or above it (every such entry has the same key and counts).
+    const uint32_t k0 = float_key<KB>(have ? cs.bits[lane] : 0u);
+    const unsigned long long kh = __ballot(have && gt < kq && kq <= gt + eq);
+    const int kl = kh ? __builtin_ctzll(kh) : 0;
+    const uint32_t kth = (uint32_t)__builtin_amdgcn_readlane((int)k0, kl);
+    const int need_k = kq - __builtin_amdgcn_readlane(gt, kl);
+    if (have) {
+      cs.sidx[rank] = cs.idx[lane];
+      cs.sbits[rank] = cs.bits[lane];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    se = have ? cs.sidx[lane] : 0;
+    sb = have ? cs.sbits[lane] : 0u;
+    sk = float_key<KB>(sb);
+    const bool tie = have && sk == kth;
+    const int tie_rank = __popcll(__ballot(tie) & ((1ull << lane) - 1ull));
+    cand = have && (sk > kth || (tie && tie_rank < need_k));
+    // Z over the candidates, with the general path's exp(x/T - m).
+    const float ev = cand ? expf(Bits<Tag>::val(sb) * iT - m) : 0.0f;
+    pc = ev * (1.0f / wave_sum_dpp(ev));
+    ss.key[lane] = sk;
+    ss.mass[lane] = cand ? (double)(unsigned long long)((double)pc * kMassScale) : -1.0;
   }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  const int se = have ? cs.sidx[lane] : 0;
-  const uint32_t sb = have ? cs.sbits[lane] : 0u;
-  const uint32_t sk = float_key<KB>(sb);
-  const unsigned long long below = (1ull << lane) - 1ull;
-  const bool tie = have && sk == kth;
-  const int tie_rank = __popcll(__ballot(tie) & below);
-  const bool cand = have && (sk > kth || (tie && tie_rank < need_k));
-  const unsigned long long cmask = __ballot(cand);
-  // Z over the candidates, with the general path's exp(x/T - m).
-  const float ev = cand ? expf(Bits<Tag>::val(sb) * iT - m) : 0.0f;
-  const float pc = ev * (1.0f / wave_sum_dpp(ev));
   bool keep = true;
   if (use_p) {
     // The threshold group: the first key, in descending order, whose
     // inclusive fixed-point mass passes P (the row maximum is always kept);
-    // ties in it are kept lowest index first.
-    const unsigned long long P = (unsigned long long)(top_p * kMassScale);
-    const unsigned long long mass = cand ? (unsigned long long)((double)pc * kMassScale) : 0ull;
-    unsigned long long A = 0, Ms = 0;
-    int C = 0, tr = 0;
-    for (int j = 0; j < n; ++j) {
-      if ((cmask >> j) & 1ull) {
-        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)sk, j);
-        const unsigned long long mj =
-            ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(mass >> 32), j) << 32) |
-            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mass, j);
-        const bool same = kj == sk;
-        A += kj > sk ? mj : 0ull;
-        Ms += same ? mj : 0ull;
-        C += same ? 1 : 0;
-        tr += (same && j < lane) ? 1 : 0;
+    // ties in it are kept lowest index first.  Masses are integers below
+    // 2^52 summing to at most about 2^52, exact in float64.
+    __syncthreads();
+    {
+      const uint32_t ki = ss.key[lane];
+      double ab = 0.0, at = 0.0;
+      int c = 0, before = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int j = 4 * wave + q;  // wave-uniform
+        const double mj = j < n ? ss.mass[j] : -1.0;
+        if (mj >= 0.0) {  // a candidate (its mass may round to 0)
+          const uint32_t kj = ss.key[j];
+          ab += kj > ki ? mj : 0.0;
+          const bool same = kj == ki;
+          at += same ? mj : 0.0;
+          c += same ? 1 : 0;
+          before += (same && j < lane) ? 1 : 0;
+        }
+      }
+      ss.above[wave][lane] = ab;
+      ss.at[wave][lane] = at;
+      ss.eqc[wave][lane] = c | (before << 8);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      double A = 0.0, Ms = 0.0;
+      int C = 0, tr = 0;
+#pragma unroll
+      for (int w = 0; w < SWAVES; ++w) {
+        A += ss.above[w][lane];
+        Ms += ss.at[w][lane];
+        const int c = ss.eqc[w][lane];
+        C += c & 255;
+        tr += c >> 8;
+      }
+      const unsigned long long P = (unsigned long long)(top_p * kMassScale);
+      const unsigned long long Ai = (unsigned long long)A, Mi = (unsigned long long)Ms;
+      const unsigned long long fh = __ballot(cand && Mi > 0 && Ai <= P && P < Ai + Mi);
+      if (fh) {
+        const int fl = __builtin_ctzll(fh);
+        const uint32_t pth = (uint32_t)__builtin_amdgcn_readlane((int)sk, fl);
+        const unsigned long long A0 = (unsigned long long)readlane_d(A, fl);
+        const unsigned long long M0 = (unsigned long long)readlane_d(Ms, fl);
+        const unsigned long long C0 = (unsigned long long)__builtin_amdgcn_readlane(C, fl);
+        const unsigned long long each = M0 / C0;  // equal keys, equal mass
+        unsigned long long n_keep = each > 0 ? (P - A0) / each : C0;
+        if (pth == max_key && n_keep == 0) n_keep = 1;
+        keep = sk > pth ||
+               (sk == pth && (n_keep >= C0 || (n_keep > 0 && (unsigned long long)tr < n_keep)));
       }
     }
-    const unsigned long long fh = __ballot(cand && Ms > 0 && A <= P && P < A + Ms);
-    if (fh) {
-      const int fl = __builtin_ctzll(fh);
-      const uint32_t pth = (uint32_t)__builtin_amdgcn_readlane((int)sk, fl);
-      const unsigned long long A0 =
-          ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(A >> 32), fl) << 32) |
-          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)A, fl);
-      const unsigned long long M0 =
-          ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(Ms >> 32), fl) << 32) |
-          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)Ms, fl);
-      const unsigned long long C0 = (unsigned long long)__builtin_amdgcn_readlane(C, fl);
-      const unsigned long long each = M0 / C0;  // equal keys, equal mass
-      unsigned long long n_keep = each > 0 ? (P - A0) / each : C0;
-      if (pth == max_key && n_keep == 0) n_keep = 1;
-      keep = sk > pth ||
-             (sk == pth && (n_keep >= C0 || (n_keep > 0 && (unsigned long long)tr < n_keep)));
+  }
+  if (wave == 0) {
+    // Inverse CDF over the candidates in vocabulary order; the last
+    // candidate takes a target that rounding leaves past the end.
+    const float wf = cand ? fmaxf(keep ? pc : 0.0f, 1e-9f) : 0.0f;
+    double incl, excl, tot;
+    wave_scan_d((double)wf, incl, excl, tot);
+    const double tgt = u01 * tot;
+    double start;
+    const int pl = wave_claim((double)wf, excl, incl, tgt, start);
+    if (lane == pl) {
+      ss.tok = se;
+      ss.bits = sb;
+      ss.logq = (float)(log((double)wf) - log(tot));
     }
   }
-  // Inverse CDF over the candidates in vocabulary order; the last candidate
-  // takes a target that rounding leaves past the end.
-  const float wf = cand ? fmaxf(keep ? pc : 0.0f, 1e-9f) : 0.0f;
-  double incl, excl, tot;
-  wave_scan_d((double)wf, incl, excl, tot);
-  const double tgt = u01 * tot;
-  double start;
-  const int pl = wave_claim((double)wf, excl, incl, tgt, start);
-  tok = __builtin_amdgcn_readlane(se, pl);
-  tok_bits = (uint32_t)__builtin_amdgcn_readlane((int)sb, pl);
-  const float wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wf), pl));
-  logq = (float)(log((double)wp) - log(tot));
+  __syncthreads();
+  tok = ss.tok;
+  logq = ss.logq;
+  tok_bits = ss.bits;
 }
 
 template <class Tag, int SL>
@@ -1257,9 +1320,7 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   __shared__ float sh_m[SWAVES], sh_s[SWAVES];
   __shared__ int sh_i[SWAVES];
   __shared__ u32x4 arg_row[SL];  // the argmax lane's registers (sweep C)
-  __shared__ int sh_tok;         // a short list's draw (wave_list_draw)
-  __shared__ float sh_logq;
-  __shared__ uint32_t sh_bits;
+  __shared__ SmallShared ss;     // a short list's pairwise sums (small_list_draw)
 
   const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1412,23 +1473,9 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   const uint32_t max_key = float_key<KB>(Bits<Tag>::bits_of(M));
   uint32_t tok_bits;
   if (n <= 64) {
-    // A list of one wave's size (top-k up to a few dozen, as usual): wave 0
-    // finishes it alone, without workgroup barriers.
-    if (wave == 0) {
-      int t;
-      float q;
-      uint32_t tb;
-      wave_list_draw<Tag>(cs, n, kq, use_p, a.top_p, iT, M * iT, max_key, u01, t, q, tb);
-      if (lane == 0) {
-        sh_tok = t;
-        sh_logq = q;
-        sh_bits = tb;
-      }
-    }
-    __syncthreads();
-    tok = sh_tok;
-    logq = sh_logq;
-    tok_bits = sh_bits;
+    // A list of one wave's size (top-k up to a few dozen, as usual).
+    small_list_draw<Tag>(cs, ss, n, kq, use_p, a.top_p, iT, M * iT, max_key, u01, tok, logq,
+                         tok_bits);
   } else {
   // The exact k-th key: the entry with fewer than k keys above it and at
   // least k at or above it (every such entry writes the same values).
