@@ -80,7 +80,6 @@ struct SampleArgs {
   double top_p;     // active iff 0 < top_p < 1
   int greedy;
   uint64_t seed, offset;
-  int fill_in;      // sample_kernel only redoes rows whose token is -1
   int64_t* token;
   float* logp;
   float* logq;
@@ -567,14 +566,16 @@ __device__ __forceinline__ void list_draw(CandShared& cs, float* sh_s, int n, ui
   __syncthreads();
 }
 
+// One row of the streaming path, by the whole workgroup (every thread calls
+// it): sample_kernel's body, and the register-resident top-k kernel's path
+// for a row whose candidate list overflows.  cs and hist: the caller's LDS.
 template <class Tag>
-__global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
+__device__ __forceinline__ void sample_row(const SampleArgs& a, const int64_t r, CandShared& cs,
+                                           uint32_t* hist) {
   using S = typename Tag::S;
   constexpr int VEC = Tag::VEC;
   constexpr int KB = Bits<Tag>::KB;
   __shared__ SearchShared sh;
-  __shared__ CandShared cs;
-  __shared__ uint32_t hist[256];
   __shared__ unsigned long long histm[256];
   __shared__ float sh_s[2 * SWAVES];
   __shared__ float sh_x[SWAVES];
@@ -583,10 +584,6 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   __shared__ int sh_found;
   __shared__ unsigned long long sh_above;
 
-  const int64_t r = blockIdx.x;
-  if (r >= a.B) return;
-  // After the register-resident kernel, only the rows it handed back.
-  if (a.fill_in && a.token[r] != -1) return;
   const S* row = static_cast<const S*>(a.logits) + r * a.stride;
   const int V = (int)a.V;  // at most SNT * VEC * MAX_SLABS (checked on the host)
   const bool al16 = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
@@ -977,6 +974,15 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
 }
 
 template <class Tag>
+__global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
+  __shared__ CandShared cs;
+  __shared__ uint32_t hist[256];
+  const int64_t r = blockIdx.x;
+  if (r >= a.B) return;
+  sample_row<Tag>(a, r, cs, hist);
+}
+
+template <class Tag>
 int launch_sample(const SampleArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((sample_kernel<Tag>), dim3((unsigned)a.B), dim3(SNT), 0, st, a);
   return check_launch("sample_kernel");
@@ -998,7 +1004,8 @@ int launch_sample(const SampleArgs& a, hipStream_t st) {
 //      key on the list, then list_draw (ties, top-p, the draw), by wave 0
 //      with the work split for a short list (small_list_draw) when the list holds
 //      at most 64 entries; a row
-//      whose list overflows gets token -1 for sample_kernel's fill-in launch;
+//      whose list overflows takes the streaming path (sample_row) in the same
+//      launch;
 //   C. the sampled token's S_other: for the argmax, the sum over every other
 //      entry relative to the row maximum, formed by the argmax lane's wave
 //      (the other lanes' sweep-A sums, the argmax lane's entries shared out
@@ -1431,7 +1438,7 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   // above it.  Those entries (a float compare: a superset of the keys >= t0
   // when -0 and +0 meet) go to the LDS list; the exact k-th key, its ties,
   // top-p and the draw are found on the list.  A row whose list overflows
-  // gets token -1 and is redone by sample_kernel.
+  // takes the streaming path (sample_row) in the same launch.
   const int kq = (int)a.top_k;
   constexpr int KB = Bits<Tag>::KB;
   const uint32_t t0 = block_kth_key16(float_key<KB>(Bits<Tag>::bits_of(lm)), tid < nvec, kq,
@@ -1466,7 +1473,10 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   __syncthreads();
   const int n = cs.n;
   if (n > KCAP) {
-    if (tid == 0) a.token[r] = -1;
+    // The list overflows (coarse logits, many ties at the threshold): this
+    // row takes the streaming path, re-reading it from memory, in this
+    // launch.  (The registers' row is not needed past the gather.)
+    sample_row<Tag>(a, r, cs, hist);
     return;
   }
   const bool use_p = a.top_p > 0.0 && a.top_p < 1.0;
@@ -1980,13 +1990,10 @@ extern "C" int rrl_sample_logprobs(const void* logits, int32_t logits_dtype, int
     if (!res_topk)
       return logits_dtype == RRL_BF16 ? launch_sample_blocks<TagBF16>(a, nslab, st)
                                       : launch_sample_blocks<TagF16>(a, nslab, st);
-    const int rc = logits_dtype == RRL_BF16 ? launch_sample_resident<TagBF16>(a, nslab, st)
-                                            : launch_sample_resident<TagF16>(a, nslab, st);
-    if (rc != RRL_OK) return rc;
-    // Rows whose candidate list overflowed (token -1) go through the
-    // streaming kernel, which returns at once for every other row.
-    a.fill_in = 1;
-    return logits_dtype == RRL_BF16 ? launch_sample<TagBF16>(a, st) : launch_sample<TagF16>(a, st);
+    // A row whose candidate list overflows takes the streaming path inside
+    // the same launch.
+    return logits_dtype == RRL_BF16 ? launch_sample_resident<TagBF16>(a, nslab, st)
+                                    : launch_sample_resident<TagF16>(a, nslab, st);
   }
   switch (logits_dtype) {
     case RRL_BF16: return launch_sample<TagBF16>(a, st);

@@ -2,7 +2,7 @@
 (MI355X): bf16, f16 and float32 rows; vocabularies from 1 to 163840 entries
 (whole and partial slabs, V % 8 != 0); contiguous, row-strided, stride-0 and
 16-byte-misaligned views; greedy decoding, temperature, top-k (including lists
-that overflow into the streaming fill-in), top-p and both together; peaked,
+that overflow into the streaming path), top-p and both together; peaked,
 flat and coarse (tie-heavy) logits.  Every call takes one of the two kernels
 (register-resident or streaming) by its shape and settings, so the sweep holds
 both to the oracle.  Bars as in test_gpu_sampler: tokens equal wherever the
