@@ -199,9 +199,9 @@ def test_resident_rows_match_oracle_and_streamed(device, dtype, V, kw):
 @pytest.mark.parametrize("top_k,top_p", [(10, 1.0), (600, 0.9)])
 def test_resident_topk_list_overflow(device, top_k, top_p):
     """Rows whose entries at or above the k-th largest lane maximum exceed the
-    1024-entry list (here 2000 copies of the maximum, or coarse logits) are
-    handed to the streaming kernel in the same call; the other rows of the
-    batch stay with the register-resident kernel.  All follow the oracle."""
+    1024-entry list (here 2000 copies of the maximum, or coarse logits) take
+    the streaming row path inside the register-resident launch; the other
+    rows of the batch stay in registers.  All follow the oracle."""
 
     B, V = 12, 32768
     g = torch.Generator().manual_seed(41)
