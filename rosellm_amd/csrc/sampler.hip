@@ -1788,21 +1788,27 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
     // the excess, a sum of at most V * 1e-9, by parts in 1e6).
     auto pf = [&](float v) { return exp2_hw(__builtin_fmaf(v, c2, -K)); };
     auto g_of = [&](float v) { return fmaxf(1e-9f - pf(v), 0.0f); };
+    // min(p 1e9, 1) in one exponential: the clamp to [0, 1] is exp2's
+    // output modifier (1e9 = 2^29.897352853986263)
+    const float Kc = uni(K - 29.897352853986263f);
+    auto pc = [&](float v) {
+      return __builtin_amdgcn_fmed3f(exp2_hw(__builtin_fmaf(v, c2, -Kc)), 0.0f, 1.0f);
+    };
     const bool want_q = a.logq != nullptr;
     const bool near = u1 < (double)V * 1.001e-9;
     double G = 0.0;
     if (want_q || near) {
-      float gs = 0.0f;
+      float gs = 0.0f;  // in units of 1e-9
 #pragma unroll
       for (int k = 0; k < SL; ++k) {
         if (k < nslab) {
           float v[8];
           unpack8<Tag>(x[k], v);
-          // sum of max(1e-9 - p, 0) = 8e-9 - sum of min(p, 1e-9)
+          // sum of max(1e-9 - p, 0) = 1e-9 (8 - sum of min(p 1e9, 1))
           float m[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) m[i] = fminf(pf(v[i]), 1e-9f);
-          float f = 8.0f * 1e-9f - sum8(m);
+          for (int i = 0; i < 8; ++i) m[i] = pc(v[i]);
+          float f = 8.0f - sum8(m);
           if (k >= nfull) {
             asm volatile("");
             if (k * SNT + tid >= nvec) f = 0.0f;  // -inf past the row's end is not floored
@@ -1810,13 +1816,13 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
           gs += f;
           if (near) {
             const float s = wave_sum_dpp(f);
-            if (lane == 0) blk_s[k][wave] = s;
+            if (lane == 0) blk_s[k][wave] = s * 1e-9f;
           }
         }
       }
       double t[1] = {(double)gs};
       block_sum<SNT, 1, double>(t, red_ws);
-      G = uni(t[0]);
+      G = uni(t[0]) * 1e-9;
     }
     const bool use_g = near && u1 < G / (1.0 + G);
     if (use_g) {
