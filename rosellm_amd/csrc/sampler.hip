@@ -1351,6 +1351,9 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   // fmaxf skips NaN; NaN and +inf reach the sum and flag the row.
   float lm = NEG, ls = 0.0f;
   int lk = 0;
+  // Each slab's lane maximum (a value of the row, so 16 bits hold it
+  // exactly), two slabs per register: the top-k gather tests these first.
+  uint32_t mk[(SL + 1) / 2] = {};
 #pragma unroll
   for (int k = 0; k < SL; ++k) {
     if (k < nslab) {
@@ -1365,6 +1368,7 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
       float v[8];
       unpack8<Tag>(x[k], v);
       const float mc = max8(v);
+      mk[k >> 1] |= (Bits<Tag>::bits_of(mc) & 0xffffu) << (16 * (k & 1));
       lk = mc > lm ? k : lk;
       const float mn = fmaxf(lm, mc);
       const float mg = fmaxf(mn, -__FLT_MAX__);
@@ -1449,13 +1453,13 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
 #pragma unroll
   for (int k = 0; k < SL; ++k) {
     if (k < nslab) {
-      float v[8];
-      unpack8<Tag>(x[k], v);
+      // The slab's lane maximum decides whether any of its 8 entries is
+      // listed (the row holds no NaN here: a NaN row left through its sum).
+      const float mc = Bits<Tag>::val((mk[k >> 1] >> (16 * (k & 1))) & 0xffffu);
       const bool inside = k * SNT + tid < nvec;
-      bool any = false;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) any = any || v[i] >= t0f;
-      if (inside && any) {
+      if (inside && mc >= t0f) {
+        float v[8];
+        unpack8<Tag>(x[k], v);
         const uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
