@@ -462,28 +462,105 @@ __device__ __forceinline__ int vocab_search(const typename Tag::S* row, int V, b
 // maximum, which is always kept), and the token is drawn by inverse CDF over
 // the floored q in vocabulary order with the uniform u01.  Every thread
 // returns the token, log q(token) and the token's stored bits.
+// Top-p's threshold group over a candidate list: the key t (KB-bit order
+// key ck of the threads with mine set, fixed-point mass ms) whose group
+// holds P, A <= P < A + M, with A the mass of the keys above t and M the
+// group's own (the groups' [A, A + M) tile [0, total mass), so at most one
+// does).  MSB-first radix select, 8 bits per pass, over 256-bin histograms
+// of mass and count (exact integer sums, in any order); cs.mass and cs.key
+// serve as the bins.  Returns false when P lies past the total (every
+// candidate kept); else cs.pth, cs.A, cs.M and cs.C describe the group.
+template <int KB>
+__device__ __forceinline__ bool mass_threshold(bool mine, uint32_t ck, unsigned long long ms,
+                                               unsigned long long P, CandShared& cs) {
+  static_assert(KB == 16 || KB == 32, "16- or 32-bit keys");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  unsigned long long* hm = cs.mass;
+  uint32_t* hc = cs.key;
+  uint32_t prefix = 0, pmask = 0;
+  unsigned long long Pr = P, A = 0;
+#pragma unroll
+  for (int pass = 0; pass < KB / 8; ++pass) {
+    const int shift = KB - 8 - 8 * pass;
+    if (tid < 256) {
+      hm[tid] = 0ull;
+      hc[tid] = 0u;
+    }
+    if (tid == 0) cs.found = 0;
+    __syncthreads();
+    if (mine && (ck & pmask) == prefix) {
+      const uint32_t d = (ck >> shift) & 255u;
+      atomicAdd(&hm[d], ms);
+      atomicAdd(&hc[d], 1u);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      // lane l owns bins 4l..4l+3; the mass above a bin is a suffix sum.
+      unsigned long long c[4];
+      for (int b = 0; b < 4; ++b) c[b] = hm[4 * lane + b];
+      const unsigned long long t = c[0] + c[1] + c[2] + c[3];
+      unsigned long long incl = t;
+      for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long y = __shfl_down(incl, o, 64);
+        if (lane + o < 64) incl += y;
+      }
+      unsigned long long above = incl - t;
+      for (int b = 3; b >= 0; --b) {
+        if (above <= Pr && Pr - above < c[b]) {
+          cs.found = 1;
+          cs.pth = 4 * lane + b;
+          cs.A = above;
+          cs.M = c[b];
+          cs.C = (int)hc[4 * lane + b];
+        }
+        above += c[b];
+      }
+    }
+    __syncthreads();
+    const bool found = cs.found != 0;
+    const uint32_t d = cs.pth;
+    const unsigned long long ab = cs.A;
+    __syncthreads();  // the next pass clears what was just read
+    if (!found) return false;
+    Pr -= ab;
+    A += ab;
+    prefix |= d << shift;
+    pmask |= 255u << shift;
+  }
+  // cs.M and cs.C are the last pass's bin: the group itself.
+  if (tid == 0) {
+    cs.pth = prefix;
+    cs.A = A;
+  }
+  __syncthreads();
+  return true;
+}
+
 template <class Tag>
 __device__ __forceinline__ void list_draw(CandShared& cs, float* sh_s, int n, uint32_t kth,
                                           int need_k, bool use_p, double top_p, float iT,
                                           float m, uint32_t max_key, double u01, int& tok,
-                                          float& logq, uint32_t& tok_bits) {
+                                          float& logq, uint32_t& tok_bits, bool sorted = false) {
   constexpr int KB = Bits<Tag>::KB;
   const int tid = threadIdx.x;
-  // Sort by vocabulary index: an entry's rank is the number of smaller
+  // Sort by vocabulary index into sidx / sbits (unless the caller listed
+  // idx / bits in that order): an entry's rank is the number of smaller
   // indices.
-  if (tid < n) {
-    const int e = cs.idx[tid];
-    int rank = 0;
-    for (int j = 0; j < n; ++j) rank += cs.idx[j] < e ? 1 : 0;
-    cs.sidx[rank] = e;
-    cs.sbits[rank] = cs.bits[tid];
+  if (!sorted) {
+    if (tid < n) {
+      const int e = cs.idx[tid];
+      int rank = 0;
+      for (int j = 0; j < n; ++j) rank += cs.idx[j] < e ? 1 : 0;
+      cs.sidx[rank] = e;
+      cs.sbits[rank] = cs.bits[tid];
+    }
+    __syncthreads();
   }
-  __syncthreads();
   // The k candidates: every entry above the k-th key and the first need_k
   // entries at it, lowest index first; relaid densely in index order.
   const bool have = tid < n;
-  const int se = have ? cs.sidx[tid] : 0;
-  const uint32_t sb = have ? cs.sbits[tid] : 0u;
+  const int se = have ? (sorted ? cs.idx[tid] : cs.sidx[tid]) : 0;
+  const uint32_t sb = have ? (sorted ? cs.bits[tid] : cs.sbits[tid]) : 0u;
   const uint32_t skey = float_key<KB>(sb);
   const bool tie = have && skey == kth;
   int ntie = 0;
@@ -510,35 +587,13 @@ __device__ __forceinline__ void list_draw(CandShared& cs, float* sh_s, int n, ui
   bool keep = true;
   if (use_p) {
     const unsigned long long P = (unsigned long long)(top_p * kMassScale);
-    cs.mass[tid] = mine ? (unsigned long long)((double)pc * kMassScale) : 0ull;
-    cs.key[tid] = ck;
-    if (tid == 0) cs.found = 0;
-    __syncthreads();
-    unsigned long long A = 0, M = 0;
-    int C = 0, tr = 0;
-    if (mine) {
-      for (int j = 0; j < kc; ++j) {
-        const uint32_t kj = cs.key[j];
-        const unsigned long long mj = cs.mass[j];
-        const bool same = kj == ck;
-        A += kj > ck ? mj : 0ull;
-        M += same ? mj : 0ull;
-        C += same ? 1 : 0;
-        tr += (same && j < tid) ? 1 : 0;
-      }
-      if (M > 0 && A <= P && P < A + M) {  // every member writes the same values
-        cs.found = 1;
-        cs.pth = ck;
-        cs.A = A;
-        cs.M = M;
-        cs.C = C;
-      }
-    }
-    __syncthreads();
-    if (cs.found) {
+    const unsigned long long ms = mine ? (unsigned long long)((double)pc * kMassScale) : 0ull;
+    if (mass_threshold<KB>(mine, ck, ms, P, cs)) {
       const uint32_t pth = cs.pth;
       const unsigned long long A0 = cs.A, C0 = (unsigned long long)cs.C;
       const unsigned long long each = cs.M / C0;  // equal keys, equal mass
+      int ntie = 0;
+      const int tr = block_excl_count(mine && ck == pth, cs.wave_cnt, ntie);  // index order
       unsigned long long n_keep = each > 0 ? (P - A0) / each : C0;
       // The first token in descending order (the row maximum) is always kept.
       if (pth == max_key && n_keep == 0) n_keep = 1;
@@ -1321,8 +1376,8 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   static_assert(Tag::VEC == 8, "16-bit rows");
   __shared__ CandShared cs;  // top-k's candidate list
   __shared__ uint32_t hist[256];
-  __shared__ uint32_t sh_digit, sh_above, sh_kth;
-  __shared__ int sh_need;
+  __shared__ uint32_t sh_digit, sh_above;
+  __shared__ int blk_base[SL * SWAVES];  // a longer list's block counts, then bases
   __shared__ float sh_z[SWAVES];
   __shared__ float sh_m[SWAVES], sh_s[SWAVES];
   __shared__ int sh_i[SWAVES];
@@ -1491,24 +1546,64 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
     small_list_draw<Tag>(cs, ss, n, kq, use_p, a.top_p, iT, M * iT, max_key, u01, tok, logq,
                          tok_bits);
   } else {
-  // The exact k-th key: the entry with fewer than k keys above it and at
-  // least k at or above it (every such entry writes the same values).
-  if (tid < n) {
-    const uint32_t ki = float_key<KB>(cs.bits[tid]);
-    int gt = 0, eq = 0;
-    for (int j = 0; j < n; ++j) {
-      const uint32_t kj = float_key<KB>(cs.bits[j]);
-      gt += kj > ki ? 1 : 0;
-      eq += kj == ki ? 1 : 0;
+    // A longer list is put in vocabulary order by a counting sort on the
+    // 512-entry block an index lies in (idx >> 9: bins in row order, a few
+    // entries each), then a rank by index inside the bin.
+    const int nb = (V + 511) >> 9;  // <= nslab * 16 entries of blk_base
+    const bool have = tid < n;
+    const int ei = have ? cs.idx[tid] : 0;
+    const uint32_t eb = have ? cs.bits[tid] : 0u;
+    for (int b = tid; b < nb; b += SNT) blk_base[b] = 0;
+    __syncthreads();
+    const int slot = have ? atomicAdd(&blk_base[ei >> 9], 1) : 0;
+    __syncthreads();
+    if (wave == 0) {
+      constexpr int PER = (SL * SWAVES + 63) / 64;
+      int c[PER], lsum = 0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int e = lane * PER + j;
+        c[j] = e < nb ? blk_base[e] : 0;
+        lsum += c[j];
+      }
+      int incl = lsum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+      }
+      int run = incl - lsum;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int e = lane * PER + j;
+        if (e < nb) blk_base[e] = run;
+        run += c[j];
+      }
     }
-    if (gt < kq && kq <= gt + eq) {
-      sh_kth = ki;
-      sh_need = kq - gt;
+    __syncthreads();
+    int b0 = 0, b1 = 0;
+    if (have) {
+      const int bin = ei >> 9;
+      b0 = blk_base[bin];
+      b1 = bin + 1 < nb ? blk_base[bin + 1] : n;
+      cs.sidx[b0 + slot] = ei;
     }
-  }
-  __syncthreads();
-  list_draw<Tag>(cs, sh_z, n, sh_kth, sh_need, use_p, a.top_p, iT, M * iT, max_key, u01, tok,
-                 logq, tok_bits);
+    __syncthreads();
+    if (have) {
+      int rank = b0;
+      for (int j = b0; j < b1; ++j) rank += cs.sidx[j] < ei ? 1 : 0;
+      cs.idx[rank] = ei;
+      cs.bits[rank] = eb;
+    }
+    __syncthreads();
+    // The exact k-th key of the list (which holds every entry at or above
+    // it), and how many of its ties the top k keep.
+    const uint32_t key = float_key<KB>(eb);
+    const uint32_t kth = block_kth_key16(key, have, kq, hist, &sh_digit, &sh_above);
+    int n_above = 0;
+    (void)block_excl_count(have && key > kth, cs.wave_cnt, n_above);
+    list_draw<Tag>(cs, sh_z, n, kth, kq - n_above, use_p, a.top_p, iT, M * iT, max_key, u01,
+                   tok, logq, tok_bits, true);
   }
   const float xt_raw = Bits<Tag>::val(tok_bits);
 
