@@ -242,6 +242,9 @@ struct SearchShared {
 
 // Top-k candidates held in LDS, one per thread (top_k <= KCAP).
 constexpr int KCAP = SNT;
+// The register-resident top-k gather's tail past KCAP (in LDS a short list's
+// draw uses otherwise).
+constexpr int OVF = 3 * SNT;
 
 struct CandShared {
   int n;                          // entries gathered (may exceed KCAP: then unused)
@@ -1088,19 +1091,23 @@ __device__ __forceinline__ float sum8(const float (&e)[8]) {
   return ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
 }
 
-// The k-th largest of one 16-bit key per thread (threads with valid = false
-// take no part; 1 <= k <= the number of valid threads): MSB-first radix
+// The k-th largest of NK 16-bit keys per thread (keys whose valid flag is
+// false take no part; 1 <= k <= the number of valid keys): MSB-first radix
 // select, 8 bits per pass, over an LDS histogram of 256 bins.
-__device__ __forceinline__ uint32_t block_kth_key16(uint32_t key, bool valid, int k,
-                                                    uint32_t* hist, uint32_t* sh_digit,
-                                                    uint32_t* sh_above) {
+template <int NK>
+__device__ __forceinline__ uint32_t block_kth_keys16(const uint32_t (&key)[NK],
+                                                     const bool (&valid)[NK], int k,
+                                                     uint32_t* hist, uint32_t* sh_digit,
+                                                     uint32_t* sh_above) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint32_t prefix = 0, pmask = 0;
   uint32_t kk = (uint32_t)k;
   for (int shift = 8; shift >= 0; shift -= 8) {
     if (tid < 256) hist[tid] = 0;
     __syncthreads();
-    if (valid && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+#pragma unroll
+    for (int j = 0; j < NK; ++j)
+      if (valid[j] && (key[j] & pmask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
     __syncthreads();
     if (wave == 0) {
       // lane l owns bins 4l..4l+3; the count above a bin is a suffix sum.
@@ -1129,6 +1136,13 @@ __device__ __forceinline__ uint32_t block_kth_key16(uint32_t key, bool valid, in
     __syncthreads();
   }
   return prefix;
+}
+__device__ __forceinline__ uint32_t block_kth_key16(uint32_t key, bool valid, int k,
+                                                    uint32_t* hist, uint32_t* sh_digit,
+                                                    uint32_t* sh_above) {
+  const uint32_t ks[1] = {key};
+  const bool vs[1] = {valid};
+  return block_kth_keys16<1>(ks, vs, k, hist, sh_digit, sh_above);
 }
 
 // A value known to be the same in every active lane, moved to scalar
@@ -1382,7 +1396,16 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   __shared__ float sh_m[SWAVES], sh_s[SWAVES];
   __shared__ int sh_i[SWAVES];
   __shared__ u32x4 arg_row[SL];  // the argmax lane's registers (sweep C)
-  __shared__ SmallShared ss;     // a short list's pairwise sums (small_list_draw)
+  // A short list's pairwise sums (small_list_draw), or an overflowing
+  // gather's tail (rs.ovf): never both in one row.
+  __shared__ union {
+    SmallShared ss;
+    struct {
+      int idx[OVF];
+      uint32_t bits[OVF];
+    } ovf;
+  } rs;
+  SmallShared& ss = rs.ss;
 
   const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1502,7 +1525,10 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
   constexpr int KB = Bits<Tag>::KB;
   const uint32_t t0 = block_kth_key16(float_key<KB>(Bits<Tag>::bits_of(lm)), tid < nvec, kq,
                                       hist, &sh_digit, &sh_above);
+  const uint32_t max_key = float_key<KB>(Bits<Tag>::bits_of(M));
   const float t0f = Bits<Tag>::val(key_bits<KB>(t0));
+  // Every entry at or above t0, to the list in any order: the first KCAP in
+  // cs, the next OVF in rs.ovf (free until a short list's draw).
   if (tid == 0) cs.n = 0;
   __syncthreads();
 #pragma unroll
@@ -1520,9 +1546,14 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
         for (int i = 0; i < 8; ++i) {
           if (v[i] >= t0f) {
             const int p = atomicAdd(&cs.n, 1);
+            const int e = (k * SNT + tid) * 8 + i;
+            const uint32_t b = (w[i >> 1] >> (16 * (i & 1))) & 0xffffu;
             if (p < KCAP) {
-              cs.idx[p] = (k * SNT + tid) * 8 + i;
-              cs.bits[p] = (w[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+              cs.idx[p] = e;
+              cs.bits[p] = b;
+            } else if (p < KCAP + OVF) {
+              rs.ovf.idx[p - KCAP] = e;
+              rs.ovf.bits[p - KCAP] = b;
             }
           }
         }
@@ -1530,16 +1561,48 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
     }
   }
   __syncthreads();
-  const int n = cs.n;
+  int n = cs.n;
+  if (n > KCAP && n <= KCAP + OVF) {
+    // The list overflows (top_k in the hundreds, where the k-th lane maximum
+    // lies well below the k-th entry) but fits with its tail: the exact k-th
+    // key over all n entries (up to four per thread), then the entries at
+    // or above it back into cs.
+    constexpr int NE = (KCAP + OVF + SNT - 1) / SNT;
+    int ei[NE];
+    uint32_t eb[NE], ek[NE];
+    bool ev[NE];
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+      const int q = tid + SNT * j;
+      ev[j] = q < n;
+      ei[j] = !ev[j] ? 0 : (q < KCAP ? cs.idx[q] : rs.ovf.idx[q - KCAP]);
+      eb[j] = !ev[j] ? 0u : (q < KCAP ? cs.bits[q] : rs.ovf.bits[q - KCAP]);
+      ek[j] = float_key<KB>(eb[j]);
+    }
+    const uint32_t kth = block_kth_keys16<NE>(ek, ev, kq, hist, &sh_digit, &sh_above);
+    if (tid == 0) cs.n = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+      if (ev[j] && ek[j] >= kth) {
+        const int p = atomicAdd(&cs.n, 1);
+        if (p < KCAP) {
+          cs.idx[p] = ei[j];
+          cs.bits[p] = eb[j];
+        }
+      }
+    }
+    __syncthreads();
+    n = cs.n;  // past KCAP only through ties at the k-th key
+  }
   if (n > KCAP) {
-    // The list overflows (coarse logits, many ties at the threshold): this
-    // row takes the streaming path, re-reading it from memory, in this
+    // The list still overflows (coarse logits, many ties at the threshold):
+    // this row takes the streaming path, re-reading it from memory, in this
     // launch.  (The registers' row is not needed past the gather.)
     sample_row<Tag>(a, r, cs, hist);
     return;
   }
   const bool use_p = a.top_p > 0.0 && a.top_p < 1.0;
-  const uint32_t max_key = float_key<KB>(Bits<Tag>::bits_of(M));
   uint32_t tok_bits;
   if (n <= 64) {
     // A list of one wave's size (top-k up to a few dozen, as usual).

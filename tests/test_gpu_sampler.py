@@ -216,6 +216,28 @@ def test_resident_topk_list_overflow(device, top_k, top_p):
         _check(x, out, seed=13, offset=off, what=f"overflow k={top_k} off={off}", **kw)
 
 
+@pytest.mark.parametrize("top_k,top_p", [(700, 1.0), (900, 0.9), (1024, 1.0)])
+def test_resident_topk_exact_kth_relist(device, top_k, top_p):
+    """top_k in the hundreds: the entries at or above the k-th largest lane
+    maximum overflow the 1024-entry list into its 3072-entry tail, so the
+    kernel takes the exact k-th key over all of them and keeps the entries at
+    or above it.  Rows: N(0, 3), a spike of 4000, a grid of quarters (ties at
+    the k-th key: past 1024 entries at top_k 1024, the streaming path),
+    N(0, 1)."""
+
+    B, V = 6, 151936
+    g = torch.Generator().manual_seed(43)
+    x = torch.randn(B, V, generator=g) * 3.0
+    x[1, 11] = 4000.0
+    x[2] = torch.round(x[2] * 4.0) / 4.0                 # quarters: ties
+    x[4] = x[4] / 3.0
+    x = x.to(torch.bfloat16)
+    kw = dict(temperature=1.0, top_k=top_k, top_p=top_p, do_sample=True)
+    for off in range(2):
+        out = RI.sample_next_token_batch(x.to(device), seed=17, offset=off, **kw)
+        _check(x, out, seed=17, offset=off, what=f"relist k={top_k} off={off}", **kw)
+
+
 @pytest.mark.parametrize("case", ["spike", "cold", "masked_head"])
 @pytest.mark.parametrize("do_sample", [True, False])
 def test_block_sums_against_far_references(device, case, do_sample):
