@@ -862,7 +862,11 @@ SAMPLE_VARIANTS = {"default": dict(temperature=1.0, top_k=0, top_p=1.0, do_sampl
                                                  do_sample=True, sampling_logprobs=False),
                    "topk50_topp0.9_T0.7": dict(temperature=0.7, top_k=50, top_p=0.9,
                                                do_sample=True),
-                   "greedy": dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=False)}
+                   "greedy": dict(temperature=1.0, top_k=0, top_p=1.0, do_sample=False),
+                   # longer top-k lists: 65-1024 entries, and a gather past 1024
+                   "topk200_T1": dict(temperature=1.0, top_k=200, top_p=1.0, do_sample=True),
+                   "topk700_topp0.9": dict(temperature=1.0, top_k=700, top_p=0.9,
+                                           do_sample=True)}
 
 
 def bench_sample(args, steps, warmup, with_cpu):

@@ -1058,12 +1058,14 @@ int launch_sample(const SampleArgs& a, hipStream_t st) {
 //      its online sum of exp((x - max) / T); one LDS exchange gives the row
 //      maximum, Z and the lowest-index argmax;
 //   K. the k-th largest lane maximum t0 (a radix select over the 1024 lane
-//      maxima), every entry >= t0 gathered into the LDS list, the exact k-th
-//      key on the list, then list_draw (ties, top-p, the draw), by wave 0
-//      with the work split for a short list (small_list_draw) when the list holds
-//      at most 64 entries; a row
-//      whose list overflows takes the streaming path (sample_row) in the same
-//      launch;
+//      maxima), every entry >= t0 gathered into the LDS list (past 1024
+//      entries into a 3072-entry tail, then cut at the exact k-th key over
+//      all of them); a list of at most 64 entries is drawn with the work
+//      split for a short list (small_list_draw), a longer one is put in
+//      vocabulary order (counting sort by 512-entry block), its exact k-th
+//      key taken by a radix select, and list_draw applies the ties, top-p
+//      and the draw; a row whose list still overflows takes the streaming
+//      path (sample_row) in the same launch;
 //   C. the sampled token's S_other: for the argmax, the sum over every other
 //      entry relative to the row maximum, formed by the argmax lane's wave
 //      (the other lanes' sweep-A sums, the argmax lane's entries shared out
