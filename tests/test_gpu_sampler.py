@@ -238,6 +238,31 @@ def test_resident_topk_exact_kth_relist(device, top_k, top_p):
         _check(x, out, seed=17, offset=off, what=f"relist k={top_k} off={off}", **kw)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("top_k,top_p", [(100, 0.305), (400, 0.7537), (90, 0.999)])
+def test_long_list_top_p_ties(device, dtype, top_k, top_p):
+    """Lists of 65-1024 candidates with many equal keys: logits on a grid of
+    halves, so the k-th key and top-p's threshold group each hold many tied
+    entries (kept lowest index first, the group cut by its equal masses).
+    16-bit rows take the register-resident list path (counting sort, radix
+    select, mass histograms); float32 rows the streaming kernel's list with
+    32-bit keys; row 2's 5002 tied maxima the streaming path.  top_p is kept
+    off exact multiples of a tied group's probability (0.3 = 30 x 0.01
+    exactly: the kernels' fixed-point cut keeps 30 there, the oracle's
+    float64 cumsum, 0.30000000000000004 > 0.3, keeps 29)."""
+
+    B, V = 8, 40000
+    g = torch.Generator().manual_seed(47)
+    x = torch.round(torch.randn(B, V, generator=g) * 4.0) / 2.0
+    x[1] = torch.round(x[1])                              # coarser: more ties
+    x[2, :5000] = x[2].max()                              # tied maxima past the list
+    x = x.to(dtype)
+    kw = dict(temperature=1.0, top_k=top_k, top_p=top_p, do_sample=True)
+    for off in range(3):
+        out = RI.sample_next_token_batch(x.to(device), seed=19, offset=off, **kw)
+        _check(x, out, seed=19, offset=off, what=f"ties {dtype} k={top_k} p={top_p} off={off}", **kw)
+
+
 @pytest.mark.parametrize("case", ["spike", "cold", "masked_head"])
 @pytest.mark.parametrize("do_sample", [True, False])
 def test_block_sums_against_far_references(device, case, do_sample):
