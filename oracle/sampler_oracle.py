@@ -138,19 +138,49 @@ def sampling_distribution(x: np.ndarray, temperature: float, top_k: int, top_p: 
     return q, cand
 
 
+def top_p_margin(x: np.ndarray, temperature: float, top_k: int, top_p: float) -> float:
+    """Distance of top_p from the cumulative masses on either side of the
+    nucleus cut (the last kept candidate's and the first dropped one's),
+    in probability; inf without top-p.  A cut closer than float32 rounding
+    of the probabilities (the kernels form them in float32, as the
+    reference's softmax does) can keep one token more or less."""
+
+    if not 0.0 < top_p < 1.0:
+        return math.inf
+    V = x.size
+    s = x.astype(np.float64) / float(temperature)
+    cand = np.ones(V, dtype=bool)
+    if 0 < top_k < V:
+        cand[:] = False
+        cand[_descending(s)[:top_k]] = True
+    m = s[cand].max()
+    e = np.where(cand, np.exp(np.where(cand, s - m, 0.0)), 0.0)
+    p = e / e.sum()
+    order = _descending(s)
+    order = order[cand[order]]
+    cum = np.cumsum(p[order])
+    drop = np.nonzero(cum > top_p)[0]
+    near = [cum[drop[0]]] if drop.size else []
+    if drop.size and drop[0] > 0:
+        near.append(cum[drop[0] - 1])
+    return float(min((abs(c - top_p) for c in near), default=math.inf))
+
+
 def sample_rows(logits: np.ndarray, *, temperature: float, top_k: int, top_p: float,
                 do_sample: bool, seed: int, offset: int) -> Dict[str, np.ndarray]:
     """Per row: token, logp = log_softmax(x/T)[token] (T = 1 when greedy),
-    logq = log(q[token]/sum q) (0 when greedy), and margin = the distance of
+    logq = log(q[token]/sum q) (0 when greedy), margin = the distance of
     the draw's target to the nearest cumulative boundary relative to the
-    total drawn over, or of u1 to the mixture's pi relative to pi (decisions
-    closer than float32 rounding can go either way)."""
+    total drawn over, or of u1 to the mixture's pi relative to pi, and
+    p_margin = top_p_margin (decisions closer than float32 rounding can go
+    either way)."""
 
     x = np.asarray(logits, dtype=np.float64)
     B, V = x.shape
     greedy = (not do_sample) or temperature <= 0.0
     T = 1.0 if greedy else float(temperature)
     out = {k: np.zeros(B) for k in ("logp", "logq", "margin")}
+    out["p_margin"] = np.full(B, math.inf)
     out["token"] = np.zeros(B, dtype=np.int64)
     for r in range(B):
         row = x[r]
@@ -167,6 +197,7 @@ def sample_rows(logits: np.ndarray, *, temperature: float, top_k: int, top_p: fl
                 e = np.exp(s - s.max())
                 tok, margin = mixture_draw(e / e.sum(), u, u1)
             out["margin"][r] = margin
+            out["p_margin"][r] = top_p_margin(row, T, top_k, top_p)
             out["logq"][r] = math.log(q[tok] / q.sum())
         s = row / T
         mx = s.max()

@@ -23,6 +23,7 @@ from rosellm_amd import roserlhf as R
 pytestmark = pytest.mark.gpu
 
 MARGIN = 1e-5
+P_MARGIN = 1e-6  # a top-p cut this close to top_p (in probability) may move by a token
 
 
 def _check(logits, out, *, temperature, top_k, top_p, do_sample, seed, offset, what):
@@ -30,18 +31,20 @@ def _check(logits, out, *, temperature, top_k, top_p, do_sample, seed, offset, w
     want = so.sample_rows(x, temperature=temperature, top_k=top_k, top_p=top_p,
                           do_sample=do_sample, seed=seed, offset=offset)
     tok = out.token_ids.cpu().numpy()
-    sure = want["margin"] > MARGIN
+    cut = want["p_margin"] > P_MARGIN
+    sure = (want["margin"] > MARGIN) & cut
     diff = (tok != want["token"]) & sure
     print(f"{what}: {int(sure.sum())}/{len(tok)} rows decided, {int((~sure).sum())} within "
-          f"{MARGIN} of a boundary", flush=True)
+          f"{MARGIN} of a boundary or {P_MARGIN} of the top-p cut", flush=True)
     assert not diff.any(), (what, np.nonzero(diff)[0][:5], tok[diff][:5], want["token"][diff][:5])
     same = tok == want["token"]
     lp = out.logprobs.cpu().double().numpy()
     err = np.abs(lp - want["logp"])[same]
     assert (err <= 1e-5 * np.abs(want["logp"][same]) + 1e-6).all(), (what, err.max())
     lq = out.sampling_logprobs.cpu().double().numpy()
-    errq = np.abs(lq - want["logq"])[same]
-    assert (errq <= 1e-5 * np.abs(want["logq"][same]) + 1e-6).all(), (what, errq.max())
+    sq = same & cut  # log q's normaliser moves with the cut
+    errq = np.abs(lq - want["logq"])[sq]
+    assert (errq <= 1e-5 * np.abs(want["logq"][sq]) + 1e-6).all(), (what, errq.max())
     return tok
 
 
@@ -186,7 +189,7 @@ def test_resident_rows_match_oracle_and_streamed(device, dtype, V, kw):
         tok = _check(x, res, seed=99, offset=off, what=f"resident V={V} off={off}", **kw)
         _check(x, st, seed=99, offset=off, what=f"streamed V={V} off={off}", **kw)
         want = so.sample_rows(x.float().numpy(), seed=99, offset=off, **kw)
-        sure = want["margin"] > MARGIN
+        sure = (want["margin"] > MARGIN) & (want["p_margin"] > P_MARGIN)
         assert (tok[sure] == st.token_ids.cpu().numpy()[sure]).all()
         if temperature == 1.0:
             lp = R.gather_token_logprobs(xd, res.token_ids).cpu().double()

@@ -1,8 +1,9 @@
 """Seeded random sweep of the next-token sampler against the CPU oracle
 (MI355X): bf16, f16 and float32 rows; vocabularies from 1 to 163840 entries
 (whole and partial slabs, V % 8 != 0); contiguous, row-strided, stride-0 and
-16-byte-misaligned views; greedy decoding, temperature, top-k (including lists
-that overflow into the streaming path), top-p and both together; peaked,
+16-byte-misaligned views; greedy decoding, temperature, top-k (short lists,
+lists of 65-1024 entries, gathers into the list's tail and lists that overflow
+into the streaming path), top-p and both together; peaked,
 flat and coarse (tie-heavy) logits.  Every call takes one of the two kernels
 (register-resident or streaming) by its shape and settings, so the sweep holds
 both to the oracle.  Bars as in test_gpu_sampler: tokens equal wherever the
@@ -32,6 +33,8 @@ SETTINGS = [
     dict(temperature=0.8, top_k=700, top_p=0.95, do_sample=True),
     dict(temperature=1.3, top_k=0, top_p=0.7, do_sample=True),
     dict(temperature=1.0, top_k=1, top_p=1.0, do_sample=True),
+    dict(temperature=1.0, top_k=150, top_p=0.8, do_sample=True),
+    dict(temperature=0.9, top_k=400, top_p=1.0, do_sample=True),
 ]
 
 
@@ -43,7 +46,7 @@ def _case(i):
                 logits=rng.choice(["peaked", "flat", "coarse"]))
 
 
-CASES = [_case(i) for i in range(84)]
+CASES = [_case(i) for i in range(108)]
 
 
 def _ids(c):

@@ -211,3 +211,23 @@ def test_greedy_and_first_token_rules():
     # top-k ties: lowest index first
     _, cand = so.sampling_distribution(np.array([1.0, 5.0, 1.0, 1.0, 0.0]), 1.0, 3, 1.0)
     assert cand.tolist() == [True, True, True, False, False]
+
+
+def test_top_p_margin():
+    """Distance of top_p from the cumulative masses either side of the cut,
+    on hand-computed distributions."""
+    x = np.log(np.array([0.5, 0.3, 0.2]))
+    assert so.top_p_margin(x, 1.0, 0, 1.0) == math.inf
+    # cum 0.5 | 0.8 | 1.0: at 0.7 the cut lies between 0.5 (kept) and 0.8
+    assert math.isclose(so.top_p_margin(x, 1.0, 0, 0.7), 0.1, rel_tol=1e-9)
+    # top_p on a cumulative mass: the cut is undecided
+    assert so.top_p_margin(x, 1.0, 0, 0.8) < 1e-12
+    # top-k 2 renormalises 0.4, 0.3 to 4/7, 3/7: at 0.6 the nearest is 4/7
+    x = np.log(np.array([0.1, 0.4, 0.2, 0.3]))
+    assert math.isclose(so.top_p_margin(x, 1.0, 2, 0.6), 0.6 - 4 / 7, rel_tol=1e-9)
+    # temperature 2 flattens 0.5/0.3/0.2 before the cut
+    x = np.log(np.array([0.5, 0.3, 0.2]))
+    p = np.sqrt([0.5, 0.3, 0.2]); p /= p.sum()
+    assert math.isclose(so.top_p_margin(x, 2.0, 0, 0.5), min(p[0] + p[1] - 0.5, 0.5 - p[0]),
+                        rel_tol=1e-9)
+
