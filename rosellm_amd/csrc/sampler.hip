@@ -245,6 +245,8 @@ constexpr int KCAP = SNT;
 // The register-resident top-k gather's tail past KCAP (in LDS a short list's
 // draw uses otherwise).
 constexpr int OVF = 3 * SNT;
+// Keys counted by the register-resident top-p path (16 KB of LDS).
+constexpr int TOPP_BINS = 4 * SNT;
 
 struct CandShared {
   int n;                          // entries gathered (may exceed KCAP: then unused)
@@ -1740,7 +1742,7 @@ __global__ __launch_bounds__(SNT) void sample_resident_kernel(SampleArgs a) {
 //   C. S_other of the token: for the argmax, Z less its own block's weight
 //      (in float64) plus that block recomputed without it, so a dominant
 //      token keeps its relative precision; any other token: Z - e_tok.
-template <class Tag, int SL>
+template <class Tag, int SL, bool TOPP>
 __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
   static_assert(Tag::VEC == 8, "16-bit rows");
   static_assert(SL <= 64, "one lane per slab in wave 0's scan");
@@ -1944,6 +1946,267 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
   float logq = 0.0f;
   float xt_raw = M;  // the token's logit
   if (!a.greedy) {
+    if constexpr (TOPP) {
+      // P. Top-p without top-k (bfloat16 rows; every entry a candidate, so
+      // those outside the nucleus keep the floor 1e-9).  The cut lies at or
+      // above x_lo, where the mass of all V entries below it would be under
+      // (1 - top_p) / 2.  One count per key from x_lo's up (LDS atomics, no
+      // exponentials); the keys' fixed-point masses count * floor(p 2^52),
+      // scanned in descending key order, give the threshold group as the
+      // streaming kernel's radix select does; its ties are kept lowest index
+      // first (the n_keep-th found from block counts in vocabulary order).
+      // Block sums of the floored weights then place the draw as for plain
+      // sampling.  A row whose keys from x_lo up outnumber the counts takes
+      // the streaming path in this launch.
+      constexpr int KB = Bits<Tag>::KB;
+      constexpr int NB = TOPP_BINS;
+      __shared__ uint32_t bins[NB];
+      __shared__ unsigned long long red_u[SWAVES];
+      __shared__ double blk_w[SL][SWAVES];
+      __shared__ double slab_w[SL];
+      __shared__ int cnt_b[SL * SWAVES];
+      __shared__ int sh_found, sh_cut, sh_blk, sh_off;
+      __shared__ uint32_t sh_pth;
+      __shared__ unsigned long long sh_a0, sh_c0, sh_each;
+      __shared__ double sh_tot;
+      __shared__ float sh_lq;
+      __shared__ CandShared cs_f;
+      __shared__ uint32_t hist_f[256];
+      const float lz = uni(log2f((float)Zd));
+      auto pn = [&](float v) { return exp2_hw(__builtin_fmaf(v - M, c2, -lz)); };  // p
+      const uint32_t kmax = float_key<KB>(Bits<Tag>::bits_of(M));
+      const float xlo =
+          uni(M + (float)(log2((1.0 - a.top_p) * Zd / (2.0 * (double)V)) / (double)c2));
+      // a key at or below x_lo's (the conversion truncates by less than one step)
+      uint32_t klo = xlo > -__FLT_MAX__ ? float_key<KB>(Bits<Tag>::bits_of(xlo)) : 0u;
+      klo = klo > 0u ? klo - 1u : 0u;
+      if (klo == 0u || kmax < klo || kmax - klo >= (uint32_t)NB) {
+        sample_row<Tag>(a, r, cs_f, hist_f);
+        return;
+      }
+      const uint32_t R = kmax - klo + 1u;
+      const float flo = Bits<Tag>::val(key_bits<KB>(klo));
+      for (int i = tid; i < (int)R; i += SNT) bins[i] = 0u;
+      if (tid == 0) {
+        sh_found = 0;
+        sh_cut = 0x7fffffff;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < SL; ++k) {
+        if (k < nslab) {
+          const bool inside = k * SNT + tid < nvec;
+          float v[8];
+          unpack8<Tag>(x[k], v);
+          const uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (inside && v[i] >= flo) {
+              const uint32_t b = (w[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+              atomicAdd(&bins[float_key<KB>(b) - klo], 1u);
+            }
+          }
+        }
+      }
+      __syncthreads();
+      // Thread t holds descending positions 4t..4t+3 (key kmax - position).
+      const unsigned long long P = (unsigned long long)(a.top_p * kMassScale);
+      auto fx = [&](int d) {  // the fixed-point mass of one entry at position d
+        return (unsigned long long)((double)pn(Bits<Tag>::val(key_bits<KB>(kmax - (uint32_t)d))) *
+                                    kMassScale);
+      };
+      uint32_t c4[NB / SNT];
+      unsigned long long lsum = 0;
+#pragma unroll
+      for (int j = 0; j < NB / SNT; ++j) {
+        const int d = tid * (NB / SNT) + j;
+        c4[j] = d < (int)R ? bins[R - 1 - d] : 0u;
+        lsum += c4[j] ? c4[j] * fx(d) : 0ull;
+      }
+      unsigned long long inc = lsum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long y = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += y;
+      }
+      if (lane == 63) red_u[wave] = inc;
+      __syncthreads();
+      unsigned long long above = inc - lsum;
+      for (int w = 0; w < wave; ++w) above += red_u[w];
+#pragma unroll
+      for (int j = 0; j < NB / SNT; ++j) {
+        const int d = tid * (NB / SNT) + j;
+        const unsigned long long f = c4[j] ? fx(d) : 0ull, m = c4[j] * f;
+        if (c4[j] > 0 && above <= P && P - above < m) {  // one bin: the group holding P
+          sh_found = 1;
+          sh_pth = kmax - (uint32_t)d;
+          sh_a0 = above;
+          sh_c0 = c4[j];
+          sh_each = f;
+        }
+        above += m;
+      }
+      __syncthreads();
+      const bool found = sh_found != 0;
+      const float fth = Bits<Tag>::val(key_bits<KB>(sh_pth));
+      const unsigned long long C0 = sh_c0, each = sh_each;
+      unsigned long long n_keep = found ? (each > 0 ? (P - sh_a0) / each : C0) : 0;
+      // The first token in descending order (the row maximum) is always kept.
+      if (found && sh_pth == kmax && n_keep == 0) n_keep = 1;
+      if (found && n_keep > 0 && n_keep < C0) {
+        // The n_keep-th entry of the group in vocabulary order: block (k, w)
+        // counts, their scan, then the block's lanes.
+#pragma unroll
+        for (int k = 0; k < SL; ++k) {
+          if (k < nslab) {
+            const bool inside = k * SNT + tid < nvec;
+            float v[8];
+            unpack8<Tag>(x[k], v);
+            int tot = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) tot += __popcll(__ballot(inside && v[i] == fth));
+            if (lane == 0) cnt_b[k * SWAVES + wave] = tot;
+          }
+        }
+        __syncthreads();
+        if (wave == 0) {
+          constexpr int PER = (SL * SWAVES + 63) / 64;
+          const int E = nslab * SWAVES;
+          const long long t = (long long)n_keep - 1;
+          int c[PER], ls_ = 0;
+#pragma unroll
+          for (int j = 0; j < PER; ++j) {
+            const int e = lane * PER + j;
+            c[j] = e < E ? cnt_b[e] : 0;
+            ls_ += c[j];
+          }
+          int incl = ls_;
+#pragma unroll
+          for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+          }
+          int run = incl - ls_;
+#pragma unroll
+          for (int j = 0; j < PER; ++j) {
+            if (c[j] > 0 && run <= t && t < run + c[j]) {
+              sh_blk = lane * PER + j;
+              sh_off = (int)(t - run);
+            }
+            run += c[j];
+          }
+        }
+        __syncthreads();
+        const int kb2 = sh_blk / SWAVES, wb2 = sh_blk % SWAVES, off = sh_off;
+        if (wave == wb2) {
+          u32x4 xv = x[0];
+#pragma unroll
+          for (int k = 1; k < SL; ++k) xv = k == kb2 ? x[k] : xv;
+          float v[8];
+          unpack8<Tag>(xv, v);
+          const bool inside = kb2 * SNT + tid < nvec;
+          uint32_t below = 0;
+          int h = 0;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const unsigned long long m = __ballot(inside && v[i] == fth);
+            below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                              __builtin_amdgcn_mbcnt_lo((uint32_t)m, below));
+            h += (int)((m >> lane) & 1ull);
+          }
+          if ((int)below <= off && off < (int)below + h) {
+            int seen = (int)below;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              if (inside && v[i] == fth) {
+                if (seen == off) sh_cut = (kb2 * SNT + tid) * 8 + i;
+                ++seen;
+              }
+            }
+          }
+        }
+        __syncthreads();
+      }
+      const int cut = sh_cut;
+      // floored weight of entry e (logit v): p if kept, else 1e-9
+      auto wq = [&](int e, float v) {
+        const bool kept =
+            !found || v > fth || (v == fth && (n_keep >= C0 || (n_keep > 0 && e <= cut)));
+        return kept ? fmaxf(pn(v), 1e-9f) : 1e-9f;
+      };
+#pragma unroll
+      for (int k = 0; k < SL; ++k) {
+        if (k < nslab) {
+          const bool inside = k * SNT + tid < nvec;
+          float v[8];
+          unpack8<Tag>(x[k], v);
+          float w8[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) w8[i] = inside ? wq((k * SNT + tid) * 8 + i, v[i]) : 0.0f;
+          const float sw = wave_sum_dpp(sum8(w8));
+          if (lane == 0) blk_w[k][wave] = (double)sw;
+        }
+      }
+      __syncthreads();
+      if (tid < nslab * SWAVES) {
+        const int k = tid >> 4;
+        const double T = row_scan_d(blk_w[k][lane & 15]);
+        if ((lane & 15) == 15) slab_w[k] = T;
+      }
+      __syncthreads();
+      if (wave == 0) {
+        const double tot = locate(slab_w, [&](int k, int w) { return blk_w[k][w]; });
+        if (lane == 0) sh_tot = tot;
+      }
+      __syncthreads();
+      const int ks = uni(sh_ks), wsel = uni(sh_ws);
+      if (wave == wsel) {
+        const double run = uni(sh_run), target = uni(sh_tgt);
+        u32x4 xv = x[0];
+#pragma unroll
+        for (int k = 1; k < SL; ++k) xv = k == ks ? x[k] : xv;
+        float v[8];
+        unpack8<Tag>(xv, v);
+        const bool inside = ks * SNT + tid < nvec;
+        float w8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w8[i] = inside ? wq((ks * SNT + tid) * 8 + i, v[i]) : 0.0f;
+        const double lw = (double)sum8(w8);
+        double incl, excl, total;
+        wave_scan_d(lw, incl, excl, total);
+        double lstart;
+        const int lc = wave_claim(lw, run + excl, run + incl, target, lstart);
+        if (lane == lc) {
+          double cum = lstart;
+          int pick = -1, lastp = 7;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            if (w8[i] > 0.0f) {
+              lastp = i;
+              if (pick < 0 && cum + (double)w8[i] > target) pick = i;
+            }
+            cum += (double)w8[i];
+          }
+          pick = pick >= 0 ? pick : lastp;
+          float xp = v[0], wp = w8[0];
+#pragma unroll
+          for (int i = 1; i < 8; ++i) {
+            xp = i == pick ? v[i] : xp;
+            wp = i == pick ? w8[i] : wp;
+          }
+          sh_sel = (ks * SNT + tid) * 8 + pick;
+          sh_x = xp;
+          sh_lq = (float)(log((double)wp) - log(sh_tot));
+        }
+      }
+      __syncthreads();
+      const int sel = sh_sel;
+      if (sel >= 0) {  // else (not reached: every total is positive) the argmax
+        tok = sel;
+        xt_raw = sh_x;
+        logq = sh_lq;
+      }
+    } else {
     const float lz = uni(log2f((float)Zd));
     const float K = uni(__builtin_fmaf(M, c2, lz));
     auto rho = [&](float v) { return exp2_hw((v - M) * c2); };                   // Z p
@@ -2050,6 +2313,7 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
     }
     // log q(token) = log(max(p_tok, 1e-9)) - log(1 + G).
     if (want_q) logq = (float)(log((double)fmaxf(pn(xt_raw), 1e-9f)) - log1p(G));
+    }
   }
 
   // C. S_other of the token and its log-prob.
@@ -2095,19 +2359,20 @@ int launch_sample_resident(const SampleArgs& a, int nslab, hipStream_t st) {
   return launch_resident_sl<Tag, RES_MAX_SLABS>(a, st);
 }
 
-template <class Tag, int SL>
+template <class Tag, int SL, bool TOPP>
 int launch_blocks_sl(const SampleArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((sample_blocks_kernel<Tag, SL>), dim3((unsigned)a.B), dim3(SNT), 0, st, a);
+  hipLaunchKernelGGL((sample_blocks_kernel<Tag, SL, TOPP>), dim3((unsigned)a.B), dim3(SNT), 0, st,
+                     a);
   return check_launch("sample_blocks_kernel");
 }
 
-template <class Tag>
+template <class Tag, bool TOPP>
 int launch_sample_blocks(const SampleArgs& a, int nslab, hipStream_t st) {
-  if (nslab <= 4) return launch_blocks_sl<Tag, 4>(a, st);
-  if (nslab <= 8) return launch_blocks_sl<Tag, 8>(a, st);
-  if (nslab <= 12) return launch_blocks_sl<Tag, 12>(a, st);
-  if (nslab <= 16) return launch_blocks_sl<Tag, 16>(a, st);
-  return launch_blocks_sl<Tag, RES_MAX_SLABS>(a, st);
+  if (nslab <= 4) return launch_blocks_sl<Tag, 4, TOPP>(a, st);
+  if (nslab <= 8) return launch_blocks_sl<Tag, 8, TOPP>(a, st);
+  if (nslab <= 12) return launch_blocks_sl<Tag, 12, TOPP>(a, st);
+  if (nslab <= 16) return launch_blocks_sl<Tag, 16, TOPP>(a, st);
+  return launch_blocks_sl<Tag, RES_MAX_SLABS, TOPP>(a, st);
 }
 
 }  // namespace
@@ -2153,13 +2418,17 @@ extern "C" int rrl_sample_logprobs(const void* logits, int32_t logits_dtype, int
   const int64_t nvec = V / 8;
   // Top-k in registers needs every one of the k-th largest lane maxima.
   const bool res_topk = !greedy && use_k && top_k <= std::min<int64_t>(nvec, SNT);
-  if (logits_dtype != RRL_F32 && (greedy || (!use_k && !use_p) || res_topk) && V % 8 == 0 &&
-      nvec <= (int64_t)SNT * RES_MAX_SLABS && ((uintptr_t)logits & 15u) == 0 &&
+  // The nucleus alone in registers: bfloat16 rows (128 keys per binade; a
+  // float16 row's keys from the cut's lower bound up rarely fit the counts).
+  const bool res_topp = !greedy && !use_k && use_p && logits_dtype == RRL_BF16;
+  if (logits_dtype != RRL_F32 && (greedy || (!use_k && !use_p) || res_topk || res_topp) &&
+      V % 8 == 0 && nvec <= (int64_t)SNT * RES_MAX_SLABS && ((uintptr_t)logits & 15u) == 0 &&
       (B == 1 || row_stride % 8 == 0)) {
     const int nslab = (int)((nvec + SNT - 1) / SNT);
+    if (res_topp) return launch_sample_blocks<TagBF16, true>(a, nslab, st);
     if (!res_topk)
-      return logits_dtype == RRL_BF16 ? launch_sample_blocks<TagBF16>(a, nslab, st)
-                                      : launch_sample_blocks<TagF16>(a, nslab, st);
+      return logits_dtype == RRL_BF16 ? launch_sample_blocks<TagBF16, false>(a, nslab, st)
+                                      : launch_sample_blocks<TagF16, false>(a, nslab, st);
     // A row whose candidate list overflows takes the streaming path inside
     // the same launch.
     return logits_dtype == RRL_BF16 ? launch_sample_resident<TagBF16>(a, nslab, st)
