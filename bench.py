@@ -866,7 +866,9 @@ SAMPLE_VARIANTS = {"default": dict(temperature=1.0, top_k=0, top_p=1.0, do_sampl
                    # longer top-k lists: 65-1024 entries, and a gather past 1024
                    "topk200_T1": dict(temperature=1.0, top_k=200, top_p=1.0, do_sample=True),
                    "topk700_topp0.9": dict(temperature=1.0, top_k=700, top_p=0.9,
-                                           do_sample=True)}
+                                           do_sample=True),
+                   # the nucleus alone (counts per key in registers, then a fill-in launch)
+                   "topp0.9": dict(temperature=1.0, top_k=0, top_p=0.9, do_sample=True)}
 
 
 def bench_sample(args, steps, warmup, with_cpu):

@@ -84,6 +84,7 @@ struct SampleArgs {
   float* logp;
   float* logq;
   int32_t* status;
+  int fill_in;  // sample_kernel: only the rows whose token slot holds -1
 };
 
 // Order-preserving unsigned key of a float's bit pattern (16- or 32-bit).
@@ -1039,6 +1040,9 @@ __global__ __launch_bounds__(SNT) void sample_kernel(SampleArgs a) {
   __shared__ uint32_t hist[256];
   const int64_t r = blockIdx.x;
   if (r >= a.B) return;
+  // A fill-in launch redoes the rows the register-resident nucleus path
+  // handed over (token slot -1); the others return at once.
+  if (a.fill_in && __builtin_nontemporal_load(&a.token[r]) != -1) return;
   sample_row<Tag>(a, r, cs, hist);
 }
 
@@ -1970,8 +1974,6 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
       __shared__ unsigned long long sh_a0, sh_c0, sh_each;
       __shared__ double sh_tot;
       __shared__ float sh_lq;
-      __shared__ CandShared cs_f;
-      __shared__ uint32_t hist_f[256];
       const float lz = uni(log2f((float)Zd));
       auto pn = [&](float v) { return exp2_hw(__builtin_fmaf(v - M, c2, -lz)); };  // p
       const uint32_t kmax = float_key<KB>(Bits<Tag>::bits_of(M));
@@ -1981,7 +1983,9 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
       uint32_t klo = xlo > -__FLT_MAX__ ? float_key<KB>(Bits<Tag>::bits_of(xlo)) : 0u;
       klo = klo > 0u ? klo - 1u : 0u;
       if (klo == 0u || kmax < klo || kmax - klo >= (uint32_t)NB) {
-        sample_row<Tag>(a, r, cs_f, hist_f);
+        // The keys from x_lo up outnumber the counts (a flat row over many
+        // binades): the fill-in launch that follows takes this row.
+        if (tid == 0) a.token[r] = -1;
         return;
       }
       const uint32_t R = kmax - klo + 1u;
@@ -2425,7 +2429,15 @@ extern "C" int rrl_sample_logprobs(const void* logits, int32_t logits_dtype, int
       V % 8 == 0 && nvec <= (int64_t)SNT * RES_MAX_SLABS && ((uintptr_t)logits & 15u) == 0 &&
       (B == 1 || row_stride % 8 == 0)) {
     const int nslab = (int)((nvec + SNT - 1) / SNT);
-    if (res_topp) return launch_sample_blocks<TagBF16, true>(a, nslab, st);
+    if (res_topp) {
+      // Rows past the nucleus path's counts are left with token -1 for a
+      // fill-in launch of the streaming kernel (its other workgroups return).
+      const int rc = launch_sample_blocks<TagBF16, true>(a, nslab, st);
+      if (rc != RRL_OK) return rc;
+      SampleArgs f = a;
+      f.fill_in = 1;
+      return launch_sample<TagBF16>(f, st);
+    }
     if (!res_topk)
       return logits_dtype == RRL_BF16 ? launch_sample_blocks<TagBF16, false>(a, nslab, st)
                                       : launch_sample_blocks<TagF16, false>(a, nslab, st);

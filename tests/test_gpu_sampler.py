@@ -266,6 +266,30 @@ def test_long_list_top_p_ties(device, dtype, top_k, top_p):
         _check(x, out, seed=19, offset=off, what=f"ties {dtype} k={top_k} p={top_p} off={off}", **kw)
 
 
+@pytest.mark.parametrize("top_p", [0.5, 0.9, 0.999])
+def test_resident_nucleus_rows(device, top_p):
+    """top_p without top-k on bfloat16 rows: counts per key from the cut's
+    lower bound up in registers.  Rows: N(0, 3); a dominant token; ties on a
+    grid of halves (the threshold group's lowest indices kept); a flat row of
+    N(0, 0.01), whose keys from the lower bound up span most binades near
+    zero, so the row is handed to the fill-in launch of the streaming kernel
+    (token slot -1 in between)."""
+
+    B, V = 8, 151936
+    g = torch.Generator().manual_seed(53)
+    x = torch.randn(B, V, generator=g) * 3.0
+    x[1, 777] += 25.0
+    x[2] = torch.round(x[2] * 2.0) / 2.0
+    x[3] = torch.randn(V, generator=g) * 0.01
+    x[5] = torch.round(x[5]) / 4.0
+    x = x.to(torch.bfloat16)
+    kw = dict(temperature=1.0, top_k=0, top_p=top_p, do_sample=True)
+    for off in range(3):
+        out = RI.sample_next_token_batch(x.to(device), seed=23, offset=off, **kw)
+        tok = _check(x, out, seed=23, offset=off, what=f"nucleus p={top_p} off={off}", **kw)
+        assert (tok >= 0).all() and (tok < V).all()
+
+
 @pytest.mark.parametrize("case", ["spike", "cold", "masked_head"])
 @pytest.mark.parametrize("do_sample", [True, False])
 def test_block_sums_against_far_references(device, case, do_sample):
