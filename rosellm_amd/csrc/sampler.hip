@@ -8,7 +8,8 @@
 // Row layout: slab k, lane j holds elements (k*1024 + j)*VEC .. +VEC-1 (VEC =
 // 16 bytes of logits), so every pass moves the row with coalesced 16-byte
 // loads, and vocabulary order is (slab, lane, element).  Three kernels:
-//   * sample_blocks_kernel (plain sampling and greedy decoding) and
+//   * sample_blocks_kernel (plain sampling, greedy decoding, and top-p
+//     without top-k on bfloat16 rows) and
 //     sample_resident_kernel (top-k with or without top-p), both for 16-bit
 //     rows made of whole, aligned 16-byte vectors: the row stays in VGPRs
 //     and is read from memory once; their sweeps are described at their
