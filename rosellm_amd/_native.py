@@ -174,6 +174,37 @@ def _event() -> "torch.cuda.Event":
     return _event_pool.pop() if _event_pool else torch.cuda.Event(enable_timing=True)
 
 
+class _TimedSpan:
+    """HIP event pair around a block of torch work (a library GEMM) when
+    ``name`` is being recorded by ``time_calls``."""
+
+    __slots__ = ("events", "start")
+
+    def __init__(self, name: str):
+        self.events = _timed.get(name) if _timed else None
+        self.start = None
+
+    def __enter__(self):
+        if self.events is not None:
+            self.start = _event()
+            self.start.record()
+        return self
+
+    def __exit__(self, *exc):
+        if self.events is not None:
+            end = _event()
+            end.record()
+            self.events.append((self.start, end))
+        return False
+
+
+def timed(name: str) -> _TimedSpan:
+    """Context manager: ``with timed("lm_logits_gemm"): torch.mm(...)`` records
+    the span under that name while ``time_calls`` records it."""
+
+    return _TimedSpan(name)
+
+
 def call(name: str, *args, timed: bool = True) -> None:
     """Call an entry point and raise on a non-zero return code.  ``timed=False``
     keeps the call out of ``time_calls``' records: a launch that is not the

@@ -1,4 +1,4 @@
-"""Fused LM-head + token log-prob + policy objective, without the logits tensor.
+"""Fused LM-head + token log-prob + policy objective (config 5).
 
 The neighbour of the hot path on the producer side: the reference forms
 ``logits = lm_head(hidden)`` (``rosetrainer/model.py:499,641``,
@@ -7,24 +7,33 @@ The neighbour of the hot path on the producer side: the reference forms
 holding the whole ``[tokens, V]`` logits tensor (79.7 GB at 262,144 tokens x
 151,936 vocab in bf16) plus its gradient.
 
-Here the hidden x vocabulary product runs on the gfx950 matrix cores in
-hand-written kernels (``csrc/lm_head.hip``) that never hold more than a
-32 x 64 logits tile:
+Two implementations sit behind one API (``impl``):
 
-* the forward streams the vocabulary past 64-token blocks, keeping an online
-  softmax per token, and forms in the same pass ``obar_n = sum_{v != a_n}
-  p_nv W_v`` (an attention-shaped product with keys = values = the weight
-  rows);
-* ``dhidden_n = g_n ((1 - p_target) W[a_n] - obar_n)`` is then an elementwise
-  kernel, with ``g = d loss / d logp`` from the objective's own backward;
-* ``dW`` streams the tokens past 64-row blocks of the weight, recomputing each
-  logits tile from the saved log-sum-exp (``dW_v = sum_n g_n ([v == a_n] -
-  p_nv) hidden_n``), accumulating in float32 registers and writing once.
+* ``"chunked"`` (what ``"auto"`` selects): the tokens go through in row
+  blocks of at most ``row_block`` tokens, the logits of one block at a time
+  in one reused buffer.  The three products are plain GEMMs (the GEMM library
+  through ``torch.mm``); the work between them is this package's row kernels
+  on the block: log-sum-exp and log-probs, the objective's d loss / d logp
+  and dlogits written over the block's logits.  Only tokens whose
+  d loss / d logp can be non-zero (mask weight != 0) go through the gradient
+  products; the others take a log-sum-exp pass alone.  Every logit is the
+  GEMM's, rounded to the weight dtype as the reference's ``F.linear`` leaves
+  it.  For the token-local objectives (PPO/GRPO clip, SAO, SAPO) one sweep
+  of each block of active tokens does everything, so every logit is formed
+  once; GSPO's sequence ratio needs every log-prob before any gradient, and
+  its backward forms the active blocks' logits a second time.  Any float
+  dtype, any hidden size.
+* ``"tiles"``: hand-written gfx950 MFMA kernels (``csrc/lm_head.hip``) that
+  never hold more than a 32 x 64 logits tile.  The forward streams the
+  vocabulary past 64-token blocks with an online softmax per token and forms
+  ``obar_n = sum_{v != a_n} p_nv W_v`` in the same pass; ``dhidden_n =
+  g_n ((1 - p_target) W[a_n] - obar_n)`` is an elementwise kernel; ``dW``
+  streams the tokens past 64-row blocks of the weight, recomputing each
+  logits tile from the saved log-sum-exp.  bfloat16, hidden sizes that are
+  multiples of 128 up to 1024.  4 x 2·N·H·V flops for an all-active batch.
 
-That is 4 x 2·N·H·V flops per step (the forward's two products and the dW
-pass's two) and no HBM traffic proportional to N·V.  Any objective of the
-package composes with it through autograd: the log-probs are an ordinary
-differentiable tensor.
+Both compose with any objective of the package through autograd: the
+log-probs are an ordinary differentiable tensor.
 """
 
 from __future__ import annotations
@@ -40,12 +49,12 @@ from . import losses as L
 
 __all__ = ["fused_linear_policy_loss", "linear_token_logprobs"]
 
-# Accepted for compatibility with callers that sized the logits they could
-# afford; the matrix-core path never forms more than a 32 x 64 logits tile.
+# Tokens per row block of the chunked path (5 GB of bf16 logits at V = 151,936).
 DEFAULT_ROW_BLOCK = 16384
+IMPLS = ("auto", "chunked", "tiles")
 
-# The softmax weights pass through the MFMA as 16-bit values: bfloat16 holds
-# weights of order 1/V; float16's normal range stops at 6.1e-5.
+# The tile path's softmax weights pass through the MFMA as 16-bit values:
+# bfloat16 holds weights of order 1/V; float16's normal range stops at 6.1e-5.
 _MFMA_DTYPES = (torch.bfloat16,)
 
 
@@ -78,6 +87,20 @@ def _check_mfma(hidden: Tensor) -> None:
                          f"in [128, 1024], got {H}")
 
 
+def _resolve_impl(impl: str, hidden: Tensor) -> str:
+    if impl not in IMPLS:
+        raise ValueError(f"unknown impl {impl!r}; expected one of {IMPLS}")
+    if impl == "tiles":
+        _check_mfma(hidden)
+        return "tiles"
+    return "chunked"
+
+
+def _check_row_block(row_block: int) -> None:
+    if row_block < 1:
+        raise ValueError("row_block must be positive")
+
+
 def _rows2d(t: Tensor, n: int, h: int) -> Tensor:
     """[n, h] rows with one row stride (a multiple of 8 elements, 16-byte
     aligned base), copying only when the view has no such layout."""
@@ -91,6 +114,425 @@ def _rows2d(t: Tensor, n: int, h: int) -> Tensor:
 
 def _targets_i32(target_ids: Tensor, n: int) -> Tensor:
     return target_ids.reshape(n).to(torch.int32).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# Chunked path: library GEMMs per row block + the package's row kernels
+# ---------------------------------------------------------------------------
+
+
+_TAP: Optional[list] = None
+
+
+class record_logits:
+    """Testing aid for the chunked path: while active, every row block's
+    logits (the GEMM's output, before the row kernels write over them) are
+    kept in ``blocks`` as (token rows, logits) pairs, so that a check can run
+    its oracle on exactly the logits the path consumed."""
+
+    def __enter__(self):
+        global _TAP
+        self.blocks = []
+        _TAP = self.blocks
+        return self
+
+    def __exit__(self, *exc):
+        global _TAP
+        _TAP = None
+        return False
+
+
+class _Blocks:
+    """Row blocks of at most ``row_block`` tokens and one reused logits
+    buffer ([row_block, V] in the weight dtype)."""
+
+    def __init__(self, w: Tensor, row_block: int, n_rows: int):
+        self.w = w
+        self.V = w.shape[0]
+        self.cap = max(1, min(int(row_block), int(n_rows)))
+        self._buf: Optional[Tensor] = None
+
+    def spans(self, n: int):
+        return ((c0, min(n, c0 + self.cap)) for c0 in range(0, n, self.cap))
+
+    def logits(self, x: Tensor, rows: Tensor) -> Tensor:
+        """x [n, H], the hidden states of token rows ``rows`` -> the block's
+        logits x @ W^T, [n, V] (the buffer's rows)."""
+
+        n = x.shape[0]
+        if self._buf is None:
+            self._buf = torch.empty((self.cap, self.V), dtype=self.w.dtype, device=self.w.device)
+        out = self._buf[:n]
+        with nat.timed("lm_logits_gemm"):
+            torch.mm(x, self.w.t(), out=out)
+        if _TAP is not None:
+            _TAP.append((rows.clone(), out.clone()))
+        return out
+
+
+_ADDMM_OUT_DTYPE: Optional[bool] = None
+
+
+def _addmm_into(acc: Tensor, a: Tensor, b: Tensor) -> None:
+    """acc += a @ b, with 16-bit a, b accumulated into a float32 acc."""
+
+    global _ADDMM_OUT_DTYPE
+    if acc.dtype == a.dtype:
+        torch.addmm(acc, a, b, out=acc)
+        return
+    if _ADDMM_OUT_DTYPE is not False:
+        try:
+            torch.addmm(acc, a, b, out_dtype=acc.dtype, out=acc)
+            _ADDMM_OUT_DTYPE = True
+            return
+        except (RuntimeError, TypeError):
+            _ADDMM_OUT_DTYPE = False
+    acc.add_(torch.mm(a, b).to(acc.dtype))
+
+
+class _Grads:
+    """d hidden rows and the d weight accumulator of one chunked backward."""
+
+    def __init__(self, h2: Tensor, w: Tensor, need_h: bool, need_w: bool):
+        self.w = w
+        self.dh = torch.zeros_like(h2, memory_format=torch.contiguous_format) if need_h else None
+        wide = w.dtype in (torch.bfloat16, torch.float16)
+        self.dw = (torch.zeros(w.shape, dtype=torch.float32 if wide else w.dtype, device=w.device)
+                   if need_w else None)
+
+    def add_block(self, dl: Tensor, x_rows: Tensor, rows: Tensor) -> None:
+        """dl [n, V] = d loss / d logits of the token rows ``rows``; x_rows
+        their hidden states [n, H]."""
+
+        if self.dh is not None:
+            with nat.timed("lm_dhidden_gemm"):
+                self.dh.index_copy_(0, rows, torch.mm(dl, self.w))
+        if self.dw is not None:
+            with nat.timed("lm_dweight_gemm"):
+                _addmm_into(self.dw, dl.t(), x_rows)
+
+    def finish(self) -> Tuple[Optional[Tensor], Optional[Tensor]]:
+        dw = self.dw
+        if dw is not None and dw.dtype != self.w.dtype:
+            dw = dw.to(self.w.dtype)
+        return self.dh, dw
+
+
+def _logprob_rows(h2: Tensor, w: Tensor, tflat: Tensor, rows: Optional[Tensor], lse: Tensor,
+                  logp: Tensor, status: Tensor, row_block: int) -> None:
+    """lse and logp of the token rows ``rows`` (all when None), written into
+    the [N] outputs: per row block the GEMM's logits, then rrl_logprob_fwd
+    (the logits rounded to the weight dtype, as the reference's F.linear
+    leaves them, for every token of the chunked path alike)."""
+
+    dev = h2.device
+    N = h2.shape[0]
+    V = w.shape[0]
+    n = N if rows is None else rows.numel()
+    if n == 0:
+        return
+    x_all = h2 if rows is None else h2.index_select(0, rows)
+    t_all = tflat if rows is None else tflat.index_select(0, rows)
+    stream = nat.stream_ptr(dev)
+    acc = lse.dtype
+    blocks = _Blocks(w, row_block, n)
+    lse_r = lse if rows is None else torch.empty(n, dtype=acc, device=dev)
+    lp_r = logp if rows is None else torch.empty(n, dtype=acc, device=dev)
+    for c0, c1 in blocks.spans(n):
+        x = blocks.logits(x_all[c0:c1],
+                          torch.arange(c0, c1, device=dev) if rows is None else rows[c0:c1])
+        tv, _tk = nat.rows_view(t_all[c0:c1], 1, c1 - c0)
+        nat.call("rrl_logprob_fwd", x.data_ptr(), nat.dtype_code(x.dtype), 1, c1 - c0, V, 0, V,
+                 tv, lp_r[c0:].data_ptr(), nat.dtype_code(acc), lse_r[c0:].data_ptr(),
+                 status.data_ptr(), stream)
+    if rows is not None:
+        lse.index_copy_(0, rows, lse_r)
+        logp.index_copy_(0, rows, lp_r)
+
+
+def _chunked_backward(h2: Tensor, w: Tensor, tflat: Tensor, lse: Tensor, logp: Tensor, g: Tensor,
+                      need_h: bool, need_w: bool, row_block: int):
+    """d hidden [N, H] and d weight [V, H] for d loss / d logp = g ([N], acc):
+    the rows with g != 0 per row block: their logits again, dlogits written
+    over them by rrl_logprob_bwd, then the two products."""
+
+    dev = h2.device
+    V = w.shape[0]
+    grads = _Grads(h2, w, need_h, need_w)
+    rows = torch.nonzero(g != 0).reshape(-1)
+    n = rows.numel()
+    if n:
+        stream = nat.stream_ptr(dev)
+        blocks = _Blocks(w, row_block, n)
+        acc_code = nat.dtype_code(g.dtype)
+        for c0, c1 in blocks.spans(n):
+            idx = rows[c0:c1]
+            xr = h2.index_select(0, idx)
+            x = blocks.logits(xr, idx)
+            tv, _tk = nat.rows_view(tflat.index_select(0, idx), 1, c1 - c0)
+            lse_c = lse.index_select(0, idx)
+            lp_c = logp.index_select(0, idx)
+            g_c = g.index_select(0, idx)
+            nat.call("rrl_logprob_bwd", x.data_ptr(), nat.dtype_code(x.dtype), 1, c1 - c0, V, 0, V,
+                     tv, lse_c.data_ptr(), lp_c.data_ptr(), g_c.data_ptr(), x.data_ptr(),
+                     nat.dtype_code(x.dtype), 0, V, 0, stream)
+            del lse_c, lp_c, g_c
+            grads.add_block(x, xr, idx)
+    return grads.finish()
+
+
+class _ChunkedLinearLogprobs(torch.autograd.Function):
+    """log_softmax(hidden @ weight.T)[target] through row blocks of library
+    GEMMs; the backward forms the logits of the rows with a non-zero gradient
+    again.
+
+    ``check``: the objective parameters whose target rule applies (any id
+    outside [0, V) raises, as torch.gather does, except NLL's ignore_index,
+    whose tokens get no target and log-prob 0).  ``weight_mask`` with
+    ``skip_masked``: tokens of zero mask weight are not computed (log-prob 0);
+    NLL passes labels != ignore_index, so ignored labels never are."""
+
+    @staticmethod
+    def forward(ctx, check: nat.RrlPolicyParams, skip_masked: bool, row_block: int,
+                hidden: Tensor, weight: Tensor, target_ids: Tensor,
+                weight_mask: Optional[Tensor] = None):
+        dev = nat.require_device(hidden, weight, target_ids)
+        B, T = _prepare(hidden, weight, target_ids)
+        N, H = B * T, hidden.shape[-1]
+        V = weight.shape[0]
+        h2 = _rows2d(hidden, N, H)
+        w = _rows2d(weight, V, H)
+        tflat = target_ids.reshape(N)
+        acc = nat.acc_dtype(hidden.dtype)
+        status = nat.new_status(dev)
+        tv, _keep = nat.rows_view(target_ids.reshape(B, T), B, T)
+        nat.call("rrl_check_targets", L.ctypes_ref(check), B, T, V, tv, status.data_ptr(),
+                 nat.stream_ptr(dev))
+        L._raise_flags(nat.read_status(status) & nat.FLAG_TARGET_RANGE, check.kind)
+        lse = torch.zeros(N, dtype=acc, device=dev)
+        logp = torch.zeros(N, dtype=acc, device=dev)
+        if weight_mask is None:
+            _logprob_rows(h2, w, tflat, None, lse, logp, status, row_block)
+        else:
+            # The live tokens first, in the same row blocks with or without
+            # skip_masked (a GEMM's rounding may depend on its block's other
+            # rows), so that skipping the masked ones changes no live result.
+            live = weight_mask.reshape(N) != 0
+            _logprob_rows(h2, w, tflat, torch.nonzero(live).reshape(-1), lse, logp, status,
+                          row_block)
+            if not (skip_masked or check.kind == nat.OBJ_NLL):
+                _logprob_rows(h2, w, tflat, torch.nonzero(~live).reshape(-1), lse, logp, status,
+                              row_block)
+        if nat.read_status(status) & nat.FLAG_TARGET_RANGE:
+            L._raise_flags(nat.FLAG_TARGET_RANGE, check.kind)
+        ctx.save_for_backward(h2, w, tflat, lse, logp)
+        ctx.meta = (hidden.shape, row_block)
+        ctx.set_materialize_grads(False)
+        return logp.view(hidden.shape[:-1])
+
+    @staticmethod
+    def backward(ctx, g):
+        need_h, need_w = ctx.needs_input_grad[3], ctx.needs_input_grad[4]
+        nones = (None, None, None)
+        if g is None or not (need_h or need_w):
+            return (*nones, None, None, None, None)
+        h2, w, tflat, lse, logp = ctx.saved_tensors
+        shape, row_block = ctx.meta
+        gc = g.reshape(-1).to(lse.dtype).contiguous()
+        dh, dw = _chunked_backward(h2, w, tflat, lse, logp, gc, need_h, need_w, row_block)
+        return (*nones, (dh.view(shape) if dh is not None else None), dw, None, None)
+
+
+class _ChunkedLinearPolicy(torch.autograd.Function):
+    """A token-local objective (PPO/GRPO clip, SAO, SAPO) behind the LM head
+    in one sweep per row block of active tokens: logits (GEMM), then
+    rrl_fused_logprob_policy (log-prob, lse, dlogits over the logits for an
+    upstream d loss = 1), then the d hidden rows and the block's share of
+    d weight (GEMMs).  Tokens of zero mask weight take the log-sum-exp pass
+    only (log-prob 0 with ``skip_masked``).  Without gradients every token
+    takes that pass.  The backward rescales the stored gradients when
+    autograd hands another scale, and runs the general chunked backward when
+    diagnostics also receive gradients.  Outputs as ``_FusedPolicy``."""
+
+    @staticmethod
+    def forward(ctx, params: nat.RrlPolicyParams, skip_masked: bool, row_block: int,
+                hidden: Tensor, weight: Tensor, target_ids: Tensor, old: Tensor, adv: Tensor,
+                mask: Tensor):
+        kind = params.kind
+        dev = nat.require_device(hidden, weight, target_ids, old, adv, mask)
+        B, T = _prepare(hidden, weight, target_ids)
+        N, H = B * T, hidden.shape[-1]
+        V = weight.shape[0]
+        h2 = _rows2d(hidden, N, H)
+        w = _rows2d(weight, V, H)
+        acc = nat.acc_dtype(hidden.dtype, old.dtype, adv.dtype)
+        acc_code = nat.dtype_code(acc)
+        stream = nat.stream_ptr(dev)
+        pref = L.ctypes_ref(params)
+        tview, tkeep = nat.rows_view(target_ids, B, T)
+        ov, ok = nat.rows_view(old, B, T)
+        av, ak = nat.rows_view(adv, B, T)
+        mv, mk = nat.rows_view(mask, B, T)
+        ws = torch.empty(nat.lib().rrl_policy_workspace_bytes(B, acc_code), dtype=torch.uint8,
+                         device=dev)
+        coef = torch.empty(B, dtype=acc, device=dev)
+        status = nat.new_status(dev)
+        # Every data error is known before the sweep: the row coefficients flag
+        # empty masks, rrl_check_targets the targets.
+        nat.call("rrl_policy_row_coef", pref, B, T, mv, acc_code, coef.data_ptr(), ws.data_ptr(),
+                 status.data_ptr(), stream)
+        nat.call("rrl_check_targets", pref, B, T, V, tview, status.data_ptr(), stream)
+        L._raise_flags(nat.read_status(status), kind)
+
+        need_h, need_w = ctx.needs_input_grad[3], ctx.needs_input_grad[4]
+        eager = torch.is_grad_enabled() and (need_h or need_w)
+        tflat = tkeep.reshape(N)
+        lse = torch.zeros(N, dtype=acc, device=dev)
+        logp = torch.zeros(N, dtype=acc, device=dev)
+        grads = None
+        if eager:
+            live = mk.reshape(N) != 0
+            act = torch.nonzero(live).reshape(-1)
+            if not skip_masked:
+                _logprob_rows(h2, w, tflat, torch.nonzero(~live).reshape(-1), lse, logp, status,
+                              row_block)
+            grads = _ChunkedLinearPolicy._sweep(params, h2, w, tflat, ok, ak, mk, coef, act, T,
+                                                lse, logp, need_h, need_w, row_block, status)
+            flags = nat.read_status(status)
+            if flags & nat.FLAG_FAST_RANGE:
+                # A row's log-sum-exp beyond the register-resident kernel's
+                # exponent range (bf16 logits near 2e38): redo the sweep on the
+                # generic row kernel (the block's logits were overwritten).
+                generic = nat.RrlPolicyParams.from_buffer_copy(params)
+                generic.flags |= nat.POLICY_GENERIC
+                status.zero_()
+                grads = _ChunkedLinearPolicy._sweep(generic, h2, w, tflat, ok, ak, mk, coef, act,
+                                                    T, lse, logp, need_h, need_w, row_block,
+                                                    status)
+        else:
+            live = mk.reshape(N) != 0
+            _logprob_rows(h2, w, tflat, torch.nonzero(live).reshape(-1), lse, logp, status,
+                          row_block)
+            if not skip_masked:
+                _logprob_rows(h2, w, tflat, torch.nonzero(~live).reshape(-1), lse, logp, status,
+                              row_block)
+        scal = torch.empty(nat.NSCALARS, dtype=acc, device=dev)
+        trusted = torch.empty(N if kind == nat.OBJ_SAO else 0, dtype=torch.bool, device=dev)
+        lview = nat.RrlView(logp.data_ptr(), acc_code, T, 1)
+        nat.call("rrl_policy_fwd", pref, B, T, lview, ov, av, mv, acc_code, ws.data_ptr(),
+                 scal.data_ptr(), None, nat.ptr(trusted) if trusted.numel() else None,
+                 status.data_ptr(), stream)
+        L._raise_flags(nat.read_status(status) & ~nat.FLAG_FAST_RANGE, kind)
+
+        ctx.params = params
+        ctx.grads = grads
+        ctx.meta = (B, T, acc, hidden.shape, row_block)
+        ctx.save_for_backward(h2, w, tflat, ok, ak, mk, lse, logp, ws)
+        ctx.set_materialize_grads(False)
+        dts = L._scalar_dtypes(kind, logp, old, adv)
+        outs = [scal[k].to(dts[k], copy=True) for k in range(4)]
+        logp_out = logp.view(hidden.shape[:-1])
+        trusted_out = trusted.view(hidden.shape[:-1]) if kind == nat.OBJ_SAO else trusted
+        if kind in (nat.OBJ_PPO, nat.OBJ_SAO):
+            ctx.mark_non_differentiable(outs[2], logp_out, trusted_out)
+        else:
+            ctx.mark_non_differentiable(logp_out, trusted_out)
+        return outs[0], outs[1], outs[2], outs[3], logp_out, trusted_out
+
+    @staticmethod
+    def _sweep(params, h2, w, tflat, ok, ak, mk, coef, act, T, lse, logp, need_h, need_w,
+               row_block, status):
+        """The single sweep over the active rows ``act``, in row blocks."""
+
+        dev = h2.device
+        N = h2.shape[0]
+        V = w.shape[0]
+        stream = nat.stream_ptr(dev)
+        pref = L.ctypes_ref(params)
+        grads = _Grads(h2, w, need_h, need_w)
+        n = act.numel()
+        if n == 0:
+            return grads.finish()
+        blocks = _Blocks(w, row_block, n)
+        acc = lse.dtype
+        oflat, aflat, mflat = ok.reshape(N), ak.reshape(N), mk.reshape(N)
+        seq_of = act // T
+        dt = nat.dtype_code(w.dtype)
+        records = torch.empty(nat.lib().rrl_fused_records_bytes(blocks.cap, 1), dtype=torch.uint8,
+                              device=dev)
+        lp_c = torch.empty(blocks.cap, dtype=acc, device=dev)
+        lse_c = torch.empty(blocks.cap, dtype=acc, device=dev)
+        for c0, c1 in blocks.spans(n):
+            idx = act[c0:c1]
+            m = c1 - c0
+            xr = h2.index_select(0, idx)
+            x = blocks.logits(xr, idx)
+            # one token per row: [m, 1] views of the block's side data
+            tv, tk = nat.rows_view(tflat.index_select(0, idx), m, 1)
+            ov, okb = nat.rows_view(oflat.index_select(0, idx), m, 1)
+            av, akb = nat.rows_view(aflat.index_select(0, idx), m, 1)
+            mv, mkb = nat.rows_view(mflat.index_select(0, idx), m, 1)
+            cc = coef.index_select(0, seq_of[c0:c1])
+            nat.call("rrl_fused_logprob_policy", pref, x.data_ptr(), dt, m, 1, V, V, V, tv, ov,
+                     av, mv, cc.data_ptr(), records.data_ptr(), lp_c.data_ptr(),
+                     lse_c.data_ptr(), x.data_ptr(), dt, V, V, status.data_ptr(), stream)
+            logp.index_copy_(0, idx, lp_c[:m])
+            lse.index_copy_(0, idx, lse_c[:m])
+            grads.add_block(x, xr, idx)
+            del tk, okb, akb, mkb, cc
+        return grads.finish()
+
+    @staticmethod
+    def backward(ctx, g0, g1, g2, g3, _glogp, _gtrusted):
+        need_h, need_w = ctx.needs_input_grad[3], ctx.needs_input_grad[4]
+        nones = (None, None, None)
+        if not (need_h or need_w):
+            return (*nones, None, None, None, None, None, None)
+        B, T, acc, shape, row_block = ctx.meta
+        params = ctx.params
+        h2, w, tflat, ok, ak, mk, lse, logp, ws = ctx.saved_tensors
+        dev = lse.device
+        stream = nat.stream_ptr(dev)
+        grads = ctx.grads
+        extra = any(g is not None for g in (g1, g3)) or (
+            params.kind == nat.OBJ_SAPO and g2 is not None)
+        if grads is not None and not extra:
+            # the stored gradients are those of d(-objective) = d loss
+            scale = (-g0).reshape(1).to(acc) if g0 is not None else torch.zeros(
+                1, dtype=acc, device=dev)
+            dh, dw = grads
+            out = []
+            for t in (dh, dw):
+                if t is not None:
+                    rows, width = t.shape
+                    nat.call("rrl_scale_rows", t.data_ptr(), nat.dtype_code(t.dtype), 1, rows,
+                             width, 0, width, scale.data_ptr(), nat.dtype_code(acc), 1.0, stream)
+                out.append(t)
+            ctx.grads = None
+            dh, dw = out
+            return (*nones, (dh.view(shape) if dh is not None and need_h else None),
+                    dw if need_w else None, None, None, None, None)
+        # General case: d loss / d logp from every differentiated output, then
+        # the chunked backward over the rows it reaches.
+        gs = torch.zeros(nat.NSCALARS, dtype=acc, device=dev)
+        for k, g in enumerate((g0, g1, g2, g3)):
+            if g is not None:
+                gs[k] = g.to(acc)
+        lview = nat.RrlView(logp.data_ptr(), nat.dtype_code(acc), T, 1)
+        ov, _ = nat.rows_view(ok, B, T)
+        av, _ = nat.rows_view(ak, B, T)
+        mv, _ = nat.rows_view(mk, B, T)
+        g = torch.empty(B * T, dtype=acc, device=dev)
+        nat.call("rrl_policy_bwd", L.ctypes_ref(params), B, T, lview, ov, av, mv,
+                 nat.dtype_code(acc), ws.data_ptr(), gs.data_ptr(), None, g.data_ptr(), stream)
+        ctx.grads = None
+        dh, dw = _chunked_backward(h2, w, tflat, lse, logp, g, need_h, need_w, row_block)
+        return (*nones, (dh.view(shape) if dh is not None else None), dw, None, None, None, None)
+
+
+# ---------------------------------------------------------------------------
+# Tile path: hand-written MFMA kernels, no logits beyond one tile
+# ---------------------------------------------------------------------------
 
 
 def lm_head_forward(h2: Tensor, w: Tensor, tgt32: Tensor, want_obar: bool, status: Tensor,
@@ -159,8 +601,9 @@ def lm_head_backward(h2: Tensor, w: Tensor, tgt32: Tensor, lse: Tensor, logp: Te
 
 
 class _LinearLogprobs(torch.autograd.Function):
-    """log_softmax(hidden @ weight.T)[target] on the matrix cores; the forward
-    keeps obar for d hidden, the backward recomputes logits tiles for d W.
+    """log_softmax(hidden @ weight.T)[target] on the hand-written matrix-core
+    kernels; the forward keeps obar for d hidden, the backward recomputes
+    logits tiles for d W.
 
     ``check``: the objective parameters whose target rule applies (any id
     outside [0, V) raises, as torch.gather does, except NLL's ignore_index,
@@ -217,26 +660,43 @@ class _LinearLogprobs(torch.autograd.Function):
                 None)
 
 
+# ---------------------------------------------------------------------------
+# Public API
+# ---------------------------------------------------------------------------
+
+
+def _linear_logprobs(check: nat.RrlPolicyParams, impl: str, row_block: int, hidden: Tensor,
+                     weight: Tensor, target_ids: Tensor, weight_mask: Optional[Tensor] = None,
+                     skip_masked: bool = False) -> Tensor:
+    _prepare(hidden, weight, target_ids)
+    if _resolve_impl(impl, hidden) == "tiles":
+        return _LinearLogprobs.apply(check, hidden, weight, target_ids, weight_mask, skip_masked)
+    return _ChunkedLinearLogprobs.apply(check, bool(skip_masked), int(row_block), hidden, weight,
+                                        target_ids, weight_mask)
+
+
 def linear_token_logprobs(hidden: Tensor, weight: Tensor, target_ids: Tensor, *,
-                          row_block: int = DEFAULT_ROW_BLOCK) -> Tensor:
-    """``gather_token_logprobs(hidden @ weight.T, target_ids)`` without the logits.
+                          row_block: int = DEFAULT_ROW_BLOCK, impl: str = "auto") -> Tensor:
+    """``gather_token_logprobs(hidden @ weight.T, target_ids)`` without the
+    whole logits tensor.
 
     ``hidden``: [..., H]; ``weight``: [V, H] (an LM head without bias, tied or
-    not), both bfloat16, H a multiple of 128 up to 1024;
-    ``target_ids``: hidden's prefix shape.  Returns float32 log-probs, as
+    not), one float dtype; ``target_ids``: hidden's prefix shape.  Returns
+    log-probs in float32 (float64 for float64 inputs), as
     ``gather_token_logprobs`` does for 16-bit logits.  Differentiable into
-    ``hidden`` and ``weight``.  ``row_block`` is accepted and unused: no more
-    than a 32 x 64 logits tile exists at a time.
+    ``hidden`` and ``weight``.  ``impl="chunked"`` (``"auto"``) holds at most
+    ``row_block`` rows of logits at a time; ``impl="tiles"`` (bfloat16, H a
+    multiple of 128 up to 1024) none beyond a 32 x 64 tile.
     """
 
-    if row_block < 1:
-        raise ValueError("row_block must be positive")
+    _check_row_block(row_block)
     return _cfg.as_reference_dtype(
-        _LinearLogprobs.apply(L._params(nat.OBJ_PPO), hidden, weight, target_ids), hidden)
+        _linear_logprobs(L._params(nat.OBJ_PPO), impl, row_block, hidden, weight, target_ids),
+        hidden)
 
 
-def linear_label_logprobs(hidden: Tensor, weight: Tensor, labels: Tensor,
-                          ignore_index: int) -> Tensor:
+def linear_label_logprobs(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int, *,
+                          row_block: int = DEFAULT_ROW_BLOCK, impl: str = "auto") -> Tensor:
     """:func:`linear_token_logprobs` for cross-entropy labels: a label equal to
     ``ignore_index`` has no target (log-prob 0, no gradient) and is exempt
     from the range check, whose failure raises IndexError as F.cross_entropy
@@ -245,7 +705,9 @@ def linear_label_logprobs(hidden: Tensor, weight: Tensor, labels: Tensor,
     p = nat.RrlPolicyParams()
     p.kind = nat.OBJ_NLL
     p.ignore_index = int(ignore_index)
-    return _LinearLogprobs.apply(p, hidden, weight, labels, labels != int(ignore_index))
+    _check_row_block(row_block)
+    return _linear_logprobs(p, impl, row_block, hidden, weight, labels,
+                            labels != int(ignore_index))
 
 
 def fused_linear_policy_loss(
@@ -266,21 +728,29 @@ def fused_linear_policy_loss(
     return_logprobs: bool = False,
     skip_masked_rows: bool = False,
     row_block: int = DEFAULT_ROW_BLOCK,
+    impl: str = "auto",
 ):
-    """``fused_policy_loss(hidden @ weight.T, ...)`` without the logits tensor.
+    """``fused_policy_loss(hidden @ weight.T, ...)`` without the whole logits
+    tensor.
 
     ``hidden``: [..., H] final hidden states at the positions that predict
     ``target_ids`` (already shifted); ``weight``: the LM head's [V, H] weight
     (no bias).  Objectives and options as :func:`fused_policy_loss`; the loss
-    is differentiable into ``hidden`` and ``weight``.  The log-probs come from
-    the matrix-core LM head (:func:`linear_token_logprobs`) and feed the
-    objective's kernels; its backward hands d loss / d logp back to the LM
-    head's backward.  ``skip_masked_rows=True`` (a training step, with
-    gradients asked for) leaves out every block of 64 consecutive tokens whose
-    mask weights are all 0: their log-probs are taken as 0, which a masked
-    token's term multiplies by 0, so the loss and the gradients are those of
-    the full computation, without the log-sum-exp pass over those blocks (no
-    reference counterpart).  ``row_block`` is accepted and unused.
+    is differentiable into ``hidden`` and ``weight``.
+
+    ``impl="chunked"`` (``"auto"``): row blocks of at most ``row_block``
+    tokens; for the token-local objectives one sweep per block of active
+    tokens forms their logits once and writes both gradients' shares then and
+    there (d hidden, d weight for an upstream d loss = 1, rescaled by the
+    backward).  ``impl="tiles"``: the hand-written MFMA kernels (bfloat16,
+    H a multiple of 128 up to 1024; no logits beyond one tile).
+
+    ``skip_masked_rows=True`` (a training step, with gradients asked for)
+    leaves out the tokens whose mask weight is 0 (the tile path: every block
+    of 64 such consecutive tokens): their log-probs are taken as 0, which a
+    masked token's term multiplies by 0, so the loss and the gradients are
+    those of the full computation, without the log-sum-exp pass over those
+    tokens (no reference counterpart).
     """
 
     if objective not in L._OBJECTIVES:
@@ -291,13 +761,13 @@ def fused_linear_policy_loss(
     if skip_masked_rows and return_logprobs:
         raise ValueError("skip_masked_rows=True leaves masked log-probs uncomputed; "
                          "it cannot be combined with return_logprobs=True")
-    if row_block < 1:
-        raise ValueError("row_block must be positive")
+    _check_row_block(row_block)
+    path = _resolve_impl(impl, hidden)
     mask = L._on_device(action_mask, hidden)
     ppo = L._params(nat.OBJ_PPO)
     if kind in (nat.OBJ_GSPO, nat.OBJ_GSPO_TOKEN):
-        logp = _LinearLogprobs.apply(ppo, hidden, weight, target_ids, mask,
-                                     bool(skip_masked_rows))
+        logp = _linear_logprobs(ppo, path, row_block, hidden, weight, target_ids,
+                                mask.expand(target_ids.shape), bool(skip_masked_rows))
         fn = L.gspo_policy_loss if kind == nat.OBJ_GSPO else L.gspo_token_policy_loss
         out = fn(logp, old_logprobs, advantages, action_mask, clip_low=clip_low,
                  clip_high=clip_low if clip_high is None else clip_high,
@@ -308,7 +778,17 @@ def fused_linear_policy_loss(
                               clip_low=clip_low, clip_high=clip_high,
                               max_log_ratio=max_log_ratio, detach_ratio=detach_ratio,
                               tau_positive=tau_positive, tau_negative=tau_negative)
-    logp = _LinearLogprobs.apply(ppo, hidden, weight, target_ids, mask, bool(skip_masked_rows))
-    obj, d1, d2, d3, _seq, trusted = L._objective(p, logp, old_logprobs, advantages, mask)
+    if path == "tiles":
+        logp = _LinearLogprobs.apply(ppo, hidden, weight, target_ids, mask,
+                                     bool(skip_masked_rows))
+        obj, d1, d2, d3, _seq, trusted = L._objective(p, logp, old_logprobs, advantages, mask)
+        out = L._token_local_output(kind, obj, d1, d2, d3, trusted)
+        return (out, _cfg.as_reference_dtype(logp.detach(), hidden)) if return_logprobs else out
+    prefix = hidden.shape[:-1]
+    old_d = L._on_device(old_logprobs, hidden)
+    adv_d = L._on_device(advantages, hidden)
+    obj, d1, d2, d3, logp, trusted = _ChunkedLinearPolicy.apply(
+        p, bool(skip_masked_rows), int(row_block), hidden, weight, target_ids,
+        old_d.expand(prefix), adv_d.expand(prefix), mask.expand(prefix))
     out = L._token_local_output(kind, obj, d1, d2, d3, trusted)
-    return (out, _cfg.as_reference_dtype(logp.detach(), hidden)) if return_logprobs else out
+    return (out, _cfg.as_reference_dtype(logp, hidden)) if return_logprobs else out

@@ -223,16 +223,20 @@ def causal_lm_loss(logits: Tensor, labels: Tensor, *, ignore_index: int = -100,
 
 def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, target: Tensor, *,
                                ignore_index: int = -100, reduction: str = "mean",
-                               row_block: int = _linear.DEFAULT_ROW_BLOCK) -> Tensor:
-    """``cross_entropy(hidden @ weight.T, target)`` without the logits tensor.
+                               row_block: int = _linear.DEFAULT_ROW_BLOCK,
+                               impl: str = "auto") -> Tensor:
+    """``cross_entropy(hidden @ weight.T, target)`` without the whole logits
+    tensor.
 
     ``hidden`` [..., H] (positions already aligned with ``target``),
     ``weight`` the LM head's [V, H] (no bias: rosetrainer/model.py:499,
-    qwen3.py:508), bfloat16 or float16.  The label log-probs come from the
-    matrix-core LM head (``linear_label_logprobs``: ignored labels have no
-    target), the loss from the NLL objective's kernels; the backward runs the
-    LM head's d hidden and d weight kernels.  ``row_block`` is accepted and
-    unused.
+    qwen3.py:508), one float dtype.  The label log-probs come from the LM head
+    (``linear_label_logprobs``: ignored labels have no target and are never
+    computed), the loss from the NLL objective's kernels.  ``impl``: as
+    ``fused_linear_policy_loss`` (``"chunked"``: row blocks of at most
+    ``row_block`` tokens of logits, any float dtype and hidden size;
+    ``"tiles"``: the hand-written MFMA kernels, bfloat16 with a hidden size
+    that is a multiple of 128 up to 1024).
     """
 
     _linear._prepare(hidden, weight, target)
@@ -241,7 +245,8 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, target: Tensor, *
     if row_block < 1:
         raise ValueError("row_block must be positive")
     dev = nat.require_device(hidden, weight, target)
-    logp = _linear.linear_label_logprobs(hidden, weight, target, ignore_index)
+    logp = _linear.linear_label_logprobs(hidden, weight, target, ignore_index,
+                                         row_block=row_block, impl=impl)
     unused = torch.zeros((), dtype=torch.float32, device=dev).expand(target.shape)
     obj = _losses._objective(p, logp, unused, unused, target)[0]
     return _cfg.as_reference_dtype(-obj, hidden)
@@ -249,7 +254,8 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, target: Tensor, *
 
 def linear_causal_lm_loss(hidden: Tensor, weight: Tensor, labels: Tensor, *,
                           ignore_index: int = -100, reduction: str = "mean",
-                          row_block: int = _linear.DEFAULT_ROW_BLOCK) -> Tensor:
+                          row_block: int = _linear.DEFAULT_ROW_BLOCK,
+                          impl: str = "auto") -> Tensor:
     """rosetrainer/model.py:641-649 from the final hidden states: the LM head,
     the causal shift and the cross-entropy, without the logits tensor.
     ``hidden`` [B, T, H], ``labels`` [B, T]."""
@@ -261,4 +267,4 @@ def linear_causal_lm_loss(hidden: Tensor, weight: Tensor, labels: Tensor, *,
             f"labels shape {tuple(labels.shape)} must match hidden prefix {tuple(hidden.shape[:2])}")
     return fused_linear_cross_entropy(hidden[:, :-1], weight, labels[:, 1:],
                                       ignore_index=ignore_index, reduction=reduction,
-                                      row_block=row_block)
+                                      row_block=row_block, impl=impl)

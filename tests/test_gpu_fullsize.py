@@ -1,7 +1,7 @@
 """The hot path at the benchmark configs' full sizes (configs 2, 3 and 4; config
-1 compared with the oracle on every row; config 5's fused LM head against the
-logits-level path on the same inputs), checked through what does not depend
-on size:
+1 compared with the oracle on every row; config 5's LM head, both
+implementations, against float64 pins formed without the kernels under
+test), checked through what does not depend on size:
 
 * a random sample of token rows against the float64 oracle (log-probs, and
   dlogits rebuilt from the oracle's d loss / d logp over the whole batch);
@@ -265,21 +265,27 @@ def _rows_close(a, b, tol, what, chunk=16384):
     return worst
 
 
-def test_config5_linear_fullsize_against_exact_rows(device):
+@pytest.mark.parametrize("impl", ["chunked", "tiles"])
+def test_config5_linear_fullsize_against_exact_rows(device, impl):
     """Config 5 in full (262144 tokens, hidden 1024, V = 151936 bf16) through
-    the matrix-core LM head, checked against float64 on samples that the
-    oracle can form exactly: the log-probs of 64 random tokens (their full
-    vocabulary rows of hidden @ W^T in float64), the d hidden rows of those
-    tokens, and the d weight rows of 8 random vocabulary entries (a sum over
-    all 262144 tokens, with each token's log-sum-exp taken from its exact
-    target logit and the kernel's log-prob).  d loss / d logp comes from the
-    objective's own backward.  Bars as in test_gpu_linear: log-probs within
-    1e-5 relative, bf16 rows within twice the propagated one-ulp bound of the
-    bf16 dlogits."""
+    both LM-head implementations, pinned without the kernels under test:
+
+    * every token's log-sum-exp and target logit come from float64 products
+      of the bf16 hidden states and weight, formed on the GPU with torch in
+      float64, 2048 tokens at a time (for the chunked path rounded to bf16
+      first, through float32 as its GEMM's float32 accumulator rounds them:
+      the logits it consumes);
+    * d loss / d logp comes from oracle.ppo_clip in float64 on the CPU, over
+      all 262144 tokens, on those log-probs.
+
+    Checks: every token's log-prob (the bars of test_gpu_linear for each
+    implementation); the d hidden rows of 64 random tokens and the d weight
+    rows of 8 random vocabulary entries (each a sum over all 262144 tokens)
+    within twice the propagated one-ulp bound of the bf16 dlogits."""
 
     from test_gpu_linear import _ulp16
 
-    print("[fullsize] config 5 matrix-core LM head vs exact rows", flush=True)
+    print(f"[fullsize] config 5 LM head ({impl}) vs float64 pins", flush=True)
     cfg = bench.CONFIGS["c5"]
     with torch.no_grad():
         inp = bench.make_inputs(cfg, device, 1234)
@@ -292,47 +298,75 @@ def test_config5_linear_fullsize_against_exact_rows(device):
     _free()
     N, H, V = B * T, h.shape[-1], w.shape[0]
     hd, wd = h.detach().clone().requires_grad_(), w.detach().clone().requires_grad_()
-    out, lp = R.fused_linear_policy_loss(hd, wd, t, old, adv, mask, return_logprobs=True, **kw)
+    out, lp = R.fused_linear_policy_loss(hd, wd, t, old, adv, mask, return_logprobs=True,
+                                         impl=impl, **kw)
     out.loss.backward()
     gh, gw = hd.grad, wd.grad
-    # d loss / d logp from the objective's own backward on the same log-probs
-    leaf = lp.detach().clone().requires_grad_()
-    R.clipped_policy_loss(leaf, old, adv, mask, **kw).loss.backward()
-    g = leaf.grad.reshape(-1).double().cpu()
+    del hd, wd, out
+    _free()
     gen = torch.Generator().manual_seed(77)
-    h64 = h.reshape(N, H).cpu().double()
-    w64 = w.cpu().double()
-    t64 = t.reshape(-1).cpu()
-    lp64 = lp.reshape(-1).cpu().double()
-    # 1. log-probs and d hidden rows of 64 tokens
     idx = torch.randperm(N, generator=gen)[:64]
-    x = h64[idx] @ w64.t()
-    lpe = torch.log_softmax(x, dim=-1).gather(1, t64[idx][:, None]).squeeze(1)
-    err = (lp64[idx] - lpe).abs()
-    assert bool((err <= 1e-5 * lpe.abs() + 1e-6).all()), float(err.max())
-    p = torch.softmax(x, dim=-1)
-    oh = torch.zeros_like(p).scatter_(1, t64[idx][:, None], 1.0)
-    dl16 = (g[idx][:, None] * (oh - p)).to(torch.bfloat16).double()
-    ref = dl16 @ w64
-    prop = _ulp16(dl16) @ w64.abs()
-    got = gh.reshape(N, H)[idx.to(device)].cpu().double()
-    excess = float(((got - ref).abs() / (2 * prop + _ulp16(ref.abs() + prop) + 1e-30)).max())
-    print(f"[fullsize] c5 logp max abs err {float(err.max()):.2e}; d hidden rows "
-          f"max |err|/bound {excess:.3f}", flush=True)
-    assert excess <= 1.0
-    # 2. d weight rows of 8 vocabulary entries, summed over every token
     vs = torch.randperm(V, generator=gen)[:8]
-    xt = (h64 * w64[t64]).sum(dim=1)             # exact target logits
-    lse = xt - lp64                               # the kernel's log-sum-exp
-    xv = h64 @ w64[vs].t()                        # [N, 8]
-    pv = torch.exp(xv - lse[:, None])
-    ohv = (t64[:, None] == vs[None, :]).double()
-    dlv = (g[:, None] * (ohv - pv)).to(torch.bfloat16).double()
-    refw = dlv.t() @ h64
-    propw = _ulp16(dlv).t() @ h64.abs()
-    gotw = gw[vs.to(device)].cpu().double()
-    excess_w = float(((gotw - refw).abs() / (2 * propw + _ulp16(refw.abs() + propw) + 1e-30)).max())
-    print(f"[fullsize] c5 d weight rows max |err|/bound {excess_w:.3f}", flush=True)
-    assert excess_w <= 1.0
-    del gh, gw, hd, wd, h, w, out, lp
+    idx_d, vs_d = idx.to(device), vs.to(device)
+    t_flat = t.reshape(-1)
+    with torch.no_grad():
+        h64 = h.reshape(N, H).double()
+        w64 = w.double()
+        lse64 = torch.empty(N, dtype=torch.float64, device=device)
+        xt64 = torch.empty(N, dtype=torch.float64, device=device)
+        xmax = torch.empty(N, dtype=torch.float64, device=device)
+        xv64 = torch.empty(N, 8, dtype=torch.float64, device=device)
+        rows64 = torch.empty(64, V, dtype=torch.float64, device=device)
+        for r0 in range(0, N, 2048):
+            r1 = min(N, r0 + 2048)
+            x = h64[r0:r1] @ w64.t()
+            if impl == "chunked":
+                x = x.float().to(torch.bfloat16).double()
+            lse64[r0:r1] = torch.logsumexp(x, dim=-1)
+            xt64[r0:r1] = x.gather(1, t_flat[r0:r1, None]).squeeze(1)
+            xmax[r0:r1] = x.abs().amax(dim=-1)
+            xv64[r0:r1] = x[:, vs_d]
+            sel = torch.nonzero((idx_d >= r0) & (idx_d < r1)).reshape(-1)
+            if sel.numel():
+                rows64[sel] = x[idx_d[sel] - r0]
+            del x
+        lp_ref = xt64 - lse64
+        # 1. every token's log-prob
+        err = (lp.reshape(-1).double() - lp_ref).abs()
+        bound = 1e-5 * lp_ref.abs() + 1e-6
+        if impl == "chunked":
+            bound = bound + _ulp16(xt64.abs().cpu()).to(device) + _ulp16(xmax.cpu()).to(device)
+        worst = float((err / bound).max())
+        print(f"[fullsize] c5 {impl}: every log-prob, max err/bound {worst:.3f} "
+              f"(max abs err {float(err.max()):.2e})", flush=True)
+        assert worst <= 1.0
+    # d loss / d logp from the float64 oracle on the CPU
+    cur = lp_ref.cpu().view(B, T).requires_grad_()
+    res = o.ppo_clip(cur, old.double().cpu(), adv.double().cpu(), mask.cpu(), **kw)
+    res["loss"].backward()
+    g = cur.grad.reshape(-1).to(device)
+    with torch.no_grad():
+        # 2. d hidden rows of 64 tokens
+        p = torch.exp(rows64 - lse64[idx_d, None])
+        oh = torch.zeros_like(p).scatter_(1, t_flat[idx_d][:, None], 1.0)
+        dl16 = (g[idx_d][:, None] * (oh - p)).to(torch.bfloat16).double()
+        ref = dl16 @ w64
+        prop = _ulp16(dl16.cpu()).to(device) @ w64.abs()
+        got = gh.reshape(N, H)[idx_d].double()
+        den = 2 * prop + _ulp16((ref.abs() + prop).cpu()).to(device) + 1e-30
+        excess = float(((got - ref).abs() / den).max())
+        print(f"[fullsize] c5 {impl}: d hidden rows max |err|/bound {excess:.3f}", flush=True)
+        assert excess <= 1.0
+        # 3. d weight rows of 8 vocabulary entries, summed over every token
+        pv = torch.exp(xv64 - lse64[:, None])
+        ohv = (t_flat[:, None] == vs_d[None, :]).double()
+        dlv = (g[:, None] * (ohv - pv)).to(torch.bfloat16).double()
+        refw = dlv.t() @ h64
+        propw = _ulp16(dlv.cpu()).to(device).t() @ h64.abs()
+        gotw = gw[vs_d].double()
+        denw = 2 * propw + _ulp16((refw.abs() + propw).cpu()).to(device) + 1e-30
+        excess_w = float(((gotw - refw).abs() / denw).max())
+        print(f"[fullsize] c5 {impl}: d weight rows max |err|/bound {excess_w:.3f}", flush=True)
+        assert excess_w <= 1.0
+    del gh, gw, h, w, lp, h64, w64, lse64, xt64, xmax, xv64, rows64, g
     _free()

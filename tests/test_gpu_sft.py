@@ -19,7 +19,7 @@ import torch
 from oracle import roserlhf_oracle as o
 from rosellm_amd import rosetrainer as RT
 
-from test_gpu_linear import _product_check
+from test_gpu_linear import _consumed, _product_check, _tap
 from test_gpu_parity import _close_rows_by_g, _rownorm16, _ulp16
 
 pytestmark = pytest.mark.gpu
@@ -194,13 +194,16 @@ def test_inplace_strided_views_upstream_scale(device, layout):
     assert same >= 0.98, same
 
 
+@pytest.mark.parametrize("impl", ["tiles", "chunked"])
 @pytest.mark.parametrize("ignore_index", [-100, 0])
-def test_linear_causal_lm_loss(device, ignore_index):
-    """LM head + shift + cross-entropy without logits: loss vs the float64
-    chain on the exact products; dhidden and dW within the propagated bound
-    of the bf16 dlogits; ignored labels carry nothing."""
+def test_linear_causal_lm_loss(device, ignore_index, impl):
+    """LM head + shift + cross-entropy without the whole logits tensor: loss
+    vs the float64 chain on the logits the implementation consumed (the exact
+    products for the tile path; the chunked path's bf16 GEMM outputs, recorded
+    and pinned to the exact products); dhidden and dW within the propagated
+    bound of the bf16 dlogits; ignored labels carry nothing."""
 
-    print(f"[sft-linear] ignore_index={ignore_index}", flush=True)
+    print(f"[sft-linear] impl={impl} ignore_index={ignore_index}", flush=True)
     g = _gen(106)
     B, T, H, V = 4, 97, 256, 8256
     h = torch.randn(B, T, H, generator=g).to(torch.bfloat16)
@@ -208,12 +211,17 @@ def test_linear_causal_lm_loss(device, ignore_index):
     y = _labels(g, (B, T), V, ignore=ignore_index)
     hd = h.to(device).requires_grad_()
     wd = w.to(device).requires_grad_()
-    loss = RT.linear_causal_lm_loss(hd, wd, y.to(device), ignore_index=ignore_index)
-    loss.backward()
+    with _tap(impl) as rec:
+        loss = RT.linear_causal_lm_loss(hd, wd, y.to(device), ignore_index=ignore_index,
+                                        impl=impl)
+        loss.backward()
     hs = h[:, :-1].contiguous()
-    x = hs.double() @ w.double().t()
+    x, xb = _consumed(impl, rec, hs.double() @ w.double().t(), hs, w)
     want, dl = o.sft_step(x, y[:, 1:], causal=False, ignore_index=ignore_index, exact=True)
     assert abs(loss.item() - want.item()) <= 1e-5 * abs(want.item())
+    if xb is not x:  # the backward's own recomputed logits
+        _want_b, dl = o.sft_step(xb, y[:, 1:], causal=False, ignore_index=ignore_index,
+                                 exact=True)
     dl = dl.double().reshape(-1, V)
     assert (hd.grad[:, -1] == 0).all()
     _product_check(hd.grad[:, :-1].reshape(-1, H), dl, w, "dhidden", transpose=False)

@@ -31,6 +31,14 @@ def test_validation_messages():
                                    return_logprobs=True)
     with pytest.raises(ValueError, match="row_block must be positive"):
         R.linear_token_logprobs(h, w, t, row_block=0)
+    with pytest.raises(ValueError, match="unknown impl"):
+        R.linear_token_logprobs(h, w, t, impl="cublas")
+    # the tile path's own limits are checked on the host, before any device work
+    with pytest.raises(TypeError, match="bfloat16"):
+        R.fused_linear_policy_loss(h, w, t, z, z, z.bool(), impl="tiles")
+    hb, wb = h.bfloat16(), w.bfloat16()
+    with pytest.raises(ValueError, match="multiple of 128"):
+        R.linear_token_logprobs(hb, wb, t, impl="tiles")
 
 
 def test_no_cpu_fallback():
