@@ -101,6 +101,13 @@ CONFIGS["sft"] = dict(CONFIGS["c2"], objective="nll", kw={}, sft=True,
                       workload="SFT: next-token cross-entropy fwd+bwd (rosetrainer/model.py:"
                                "643-649), 256x1024 tokens, V=151936 bf16")
 SFT_SIDE_BYTES = 12  # per row: 8 label + 4 logp out
+# Config 5's default (chunked) LM head: the library GEMMs, timed by HIP events
+# around each call, and the row kernels between them.
+LM_CHUNKED_KERNELS = ["lm_logits_gemm", "lm_dhidden_gemm", "lm_dweight_gemm",
+                      "rrl_fused_logprob_policy", "rrl_logprob_fwd"]
+LM_GEMMS = LM_CHUNKED_KERNELS[:3]
+# impl="tiles": the hand-written MFMA kernels
+LM_TILE_KERNELS = ["rrl_lm_head_fwd", "rrl_lm_head_dweight", "rrl_lm_head_dhidden"]
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 # Sequences of the CPU plan's sub-batch per config (C1 whole; C4's are 8192 long).
 CPU_SEQS = {"c1": 32, "c2": 16, "c3": 16, "sft": 16, "c4": 2, "c5": 16}
@@ -225,11 +232,12 @@ def _watch(lp, probe):
         lp.register_hook(lambda g: probe.__setitem__("active", int((g != 0).sum().item())))
 
 
-def make_step(inp, cfg, path, objective, skip_masked=False, probe=None):
+def make_step(inp, cfg, path, objective, skip_masked=False, probe=None, impl="auto"):
     """One timed step of the config's training-step hot path.  With ``probe``
     (a dict; composed path only, never in a timed step) the step also records
     how many token rows receive a non-zero d loss / d logp: the backward
-    kernel reads the logits of those rows only."""
+    kernel reads the logits of those rows only.  ``impl`` picks config 5's
+    LM-head implementation ("auto" = chunked, or "tiles")."""
 
     from rosellm_amd import roserlhf as R
 
@@ -253,7 +261,8 @@ def make_step(inp, cfg, path, objective, skip_masked=False, probe=None):
             a = R.group_standardized_advantages(rewards).reshape(-1)[:, None].expand(B, T)
             if path == "fused":
                 out = R.fused_linear_policy_loss(hidden, weight, actions, old, a, mask,
-                                                 skip_masked_rows=skip_masked, **kw)
+                                                 skip_masked_rows=skip_masked, impl=impl,
+                                                 **kw)
             else:
                 lp = R.gather_token_logprobs(F.linear(hidden, weight), actions)
                 _watch(lp, probe)
@@ -500,6 +509,26 @@ def cpu_baseline_lm_head(inp, cfg, n_seq, runs):
               "loss_rel_err": abs(lg - lc) / max(abs(lc), 1e-30),
               "dhidden": _err(hg.grad, dh_c), "dweight": _err(wg.grad, dw_c)}
     del hg, wg
+    # The reference's own chain on the GPU in bf16 (F.linear, log_softmax of
+    # the float32 upcast, gather, clipped objective, autograd: bf16 dlogits,
+    # bf16 products), against the same float32 CPU chain.
+    import torch.nn.functional as F
+
+    hr = inp["hidden"].detach()[:n_seq].clone().requires_grad_()
+    wr = inp["weight"].detach().clone().requires_grad_()
+    x = F.linear(hr, wr)
+    lp = F.log_softmax(x.float(), dim=-1).gather(-1, d(t).unsqueeze(-1)).squeeze(-1)
+    del x
+    out_r = o.ppo_clip(lp, d(old).float(), d(adv).float(), d(mask), **cfg["kw"])
+    out_r["loss"].backward()
+    torch.cuda.synchronize()
+    parity["torch_bf16_chain"] = {
+        "loss_rel_err": abs(float(out_r["loss"]) - lc) / max(abs(lc), 1e-30),
+        "dhidden": _err(hr.grad, dh_c), "dweight": _err(wr.grad, dw_c),
+        "note": "F.linear -> log_softmax(float32) -> gather -> clip -> autograd on the GPU "
+                "in bf16, against the float32 CPU chain"}
+    del hr, wr, lp, out_r
+    torch.cuda.empty_cache()
     rows = n_seq * T
     return {
         "value": round(rows / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
@@ -557,7 +586,7 @@ def timed_steps(step, steps, kernels, prepare=None):
         step_ms.append(ev[2 * steps - 2].elapsed_time(ev[2 * steps - 1]))
     else:
         step_ms = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(steps)]
-    timed = nat.time_calls(*kernels, capacity=steps * 32)
+    timed = nat.time_calls(*kernels, capacity=steps * 64)
     for _ in range(steps):
         if prepare is not None:
             prepare()
@@ -565,6 +594,18 @@ def timed_steps(step, steps, kernels, prepare=None):
     torch.cuda.synchronize()
     nat.time_calls()
     return {"wall_s": wall, "step_ms": step_ms, "out": out, "launches": timed}
+
+
+def kernel_stats(launches, kernels, steps):
+    """{kernel: (average ms per launch, launches per step)} of the recorded
+    launches (kernels never launched are left out)."""
+
+    stats = {}
+    for k in kernels:
+        kms = [s.elapsed_time(e) for s, e in launches.get(k, [])]
+        if kms:
+            stats[k] = (sum(kms) / len(kms), len(kms) / steps)
+    return stats
 
 
 def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
@@ -610,7 +651,7 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
     log(f"[bench] {warmup} warm-up steps done")
 
     if cfg.get("lm_head"):
-        kernels = ["rrl_lm_head_fwd", "rrl_lm_head_dweight", "rrl_lm_head_dhidden"]
+        kernels = list(LM_CHUNKED_KERNELS)
     elif path == "fused" and not gspo_like:
         kernels = ["rrl_fused_logprob_policy"]
     else:
@@ -645,11 +686,7 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
         active = probe["active"]
         alg["rrl_logprob_bwd"] = N * V * in_b + active * V * in_b + N * (8 + 4 + 4 + 4)
         log(f"[bench] backward reads the logits of {active} of {N} rows")
-    kstats = {}
-    for k in kernels:
-        kms = [s.elapsed_time(e) for s, e in res["launches"][k]]
-        if kms:
-            kstats[k] = (sum(kms) / len(kms), len(kms) / steps)
+    kstats = kernel_stats(res["launches"], kernels, steps)
     kernels = [k for k in kernels if k in kstats]
     kernel = max(kernels, key=lambda k: kstats[k][0] * kstats[k][1])  # the dominant kernel
     k_avg = kstats[kernel][0]
@@ -659,7 +696,7 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
         + f"; loss {out.loss.item():.6g}")
     workload_key = f"{name}-{path}" + (f"-{objective}" if name == "c3" else "")
     if cfg.get("lm_head"):
-        roofline = lm_head_roofline(inp, cfg, kstats, ms_step)
+        roofline = lm_head_roofline(inp, kstats, ms_step)
     else:
         achieved = alg[kernel] / (k_avg * 1e-3) / 1e9
         roofline = {
@@ -715,37 +752,48 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
         log(f"[bench] skip_masked_rows: {v_el * 1e3 / steps:.3f} ms/step, kernels "
             + ", ".join(f"{k} {v:.3f} ms" for k, v in vavg.items()))
     if skip_masked_variant and path == "fused" and cfg.get("lm_head"):
-        # Config 5 with skip_masked_rows=True: the forward leaves out the
-        # 64-token blocks whose tokens are all masked (no log-sum-exp pass);
-        # loss and gradients are those of the headline step.
+        # Config 5 with skip_masked_rows=True: the tokens of zero mask weight
+        # are never formed (no logits, no log-sum-exp); loss and gradients are
+        # those of the headline step.
         vstep = make_step(inp, cfg, path, objective, skip_masked=True)
         for _ in range(warmup):
             vstep()
-        vk = ["rrl_lm_head_fwd", "rrl_lm_head_dweight", "rrl_lm_head_dhidden"]
-        vres = timed_steps(vstep, steps, vk)
-        v_el = vres["wall_s"]
-        vavg = {k: sum(s.elapsed_time(e) for s, e in vres["launches"][k])
-                / len(vres["launches"][k]) for k in vk}
+        vres = timed_steps(vstep, steps, LM_CHUNKED_KERNELS)
+        v_ms = vres["wall_s"] * 1e3 / steps
         assert vres["out"].loss.item() == out.loss.item(), "skip_masked_rows changed the loss"
-        H = inp["hidden"].shape[-1]
-        obar_blocks = roofline["fwd_obar_blocks"]
-        fwd_exec = 2 * 2 * obar_blocks * 64 * H * V
-        model = 3 * 2 * N * H * V
-        v_ms = v_el * 1e3 / steps
+        vroof = lm_head_roofline(inp, kernel_stats(vres["launches"], LM_CHUNKED_KERNELS, steps),
+                                 v_ms, skip=True)
         variants["skip_masked_rows"] = {
-            "value": round(N / (v_el / steps), 1),
+            "value": round(N / (v_ms * 1e-3), 1),
             "ms_per_step": round(v_ms, 4),
             "ms_per_step_median": round(statistics.median(vres["step_ms"]), 4),
-            "kernels_ms": {k: round(v, 4) for k, v in vavg.items()},
-            "fwd_executed_flops": fwd_exec,
-            "fwd_TFLOPs": round(fwd_exec / (vavg["rrl_lm_head_fwd"] * 1e-3) / 1e12, 1),
-            "step_TFLOPs_model": round(model / (v_ms * 1e-3) / 1e12, 1),
-            "step_frac": round(model / (v_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-            "note": "fully masked 64-token blocks skipped in the forward; step_frac on the "
-                    "model's 3*2*N*H*V flops",
+            "step": vroof["step"],
+            "kernels": vroof["kernels"],
+            "other_ms_per_step": vroof["other_ms_per_step"],
+            "note": "tokens of zero mask weight never formed; step frac on the model's "
+                    "3*2*N*H*V flops",
         }
-        log(f"[bench] skip_masked_rows: {v_ms:.3f} ms/step, kernels "
-            + ", ".join(f"{k} {v:.3f} ms" for k, v in vavg.items()))
+        del vstep, vres
+        log(f"[bench] skip_masked_rows: {v_ms:.3f} ms/step")
+        # impl="tiles": the hand-written MFMA kernels, no logits beyond one tile
+        tstep = make_step(inp, cfg, path, objective, impl="tiles")
+        for _ in range(warmup):
+            tstep()
+        tres = timed_steps(tstep, steps, LM_TILE_KERNELS)
+        t_ms = tres["wall_s"] * 1e3 / steps
+        troof = lm_head_tiles_roofline(inp, kernel_stats(tres["launches"], LM_TILE_KERNELS,
+                                                         steps), t_ms)
+        variants["tiles"] = {
+            "value": round(N / (t_ms * 1e-3), 1),
+            "ms_per_step": round(t_ms, 4),
+            "ms_per_step_median": round(statistics.median(tres["step_ms"]), 4),
+            "loss": tres["out"].loss.item(),
+            "roofline": troof,
+            "note": "impl='tiles': the hand-written MFMA LM-head kernels",
+        }
+        del tstep, tres
+        log(f"[bench] tiles: {t_ms:.3f} ms/step, "
+            + ", ".join(f"{k} {v:.3f} ms" for k, v in troof["kernels_ms"].items()))
     if skip_masked_variant and path == "fused" and objective == "clipped" \
             and not cfg.get("lm_head"):
         # The same step with skip_masked_rows=True (zero-weight rows are never
@@ -815,12 +863,76 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
     return result
 
 
-def lm_head_roofline(inp, cfg, kstats, ms_step):
-    """Config 5: the step against the dense bf16 MFMA peak on the reference's
-    three products (3 x 2*N*H*V, the model's flops), and each kernel's
-    executed flops (the work skipping is exact: blocks of 64 tokens none of
-    which needs obar run the log-sum-exp pass only, and the dW pass visits
-    the 32-token tiles holding a token with a non-zero gradient)."""
+def lm_head_roofline(inp, kstats, ms_step, skip=False):
+    """Config 5 on the chunked LM head: the step against the dense bf16 MFMA
+    peak on the reference's three products (3 x 2*N*H*V, the model's flops);
+    each GEMM's flops (logits of every token, or of the masked-in tokens
+    with ``skip``; d hidden and d weight of the masked-in tokens) over its
+    launches' time; each row kernel's algorithmic bytes (the fused kernel
+    reads a masked-in row's bf16 logits and writes its bf16 dlogits in place;
+    the log-prob pass reads the other rows) over its launches' time.  The
+    roofline is the GEMM with the most time per step."""
+
+    N = inp["B"] * inp["T"]
+    V, H = inp["V"], inp["hidden"].shape[-1]
+    in_b = inp["hidden"].element_size()
+    n_act = int((inp["mask"] != 0).sum().item())
+    rows_fwd = n_act if skip else N
+    flops = {"lm_logits_gemm": 2 * rows_fwd * H * V, "lm_dhidden_gemm": 2 * n_act * H * V,
+             "lm_dweight_gemm": 2 * n_act * H * V}
+    hbm = {"rrl_fused_logprob_policy": n_act * (V * (in_b + in_b) + SIDE_BYTES + 4),
+           "rrl_logprob_fwd": (rows_fwd - n_act) * (V * in_b + 8 + 4 + 4)}
+    per = {}
+    timed_ms = 0.0
+    for k, (avg, per_step) in kstats.items():
+        ms = avg * per_step
+        timed_ms += ms
+        e = {"ms_per_launch": round(avg, 4), "launches_per_step": round(per_step, 3),
+             "ms_per_step": round(ms, 3)}
+        if k in flops:
+            tf = flops[k] / (ms * 1e-3) / 1e12
+            e.update(flops_per_step=flops[k], TFLOPs=round(tf, 1),
+                     frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4))
+        elif k in hbm:
+            gbs = hbm[k] / (ms * 1e-3) / 1e9
+            e.update(alg_bytes_per_step=hbm[k], GBs=round(gbs, 1),
+                     frac=round(gbs / HBM_PEAK_GBS, 4))
+        per[k] = e
+    gemms = [k for k in LM_GEMMS if k in kstats]
+    dom = max(gemms, key=lambda k: per[k]["ms_per_step"])
+    avg, per_step = kstats[dom]
+    model = 3 * 2 * N * H * V
+    step_tf = model / (ms_step * 1e-3) / 1e12
+    achieved = flops[dom] / (avg * per_step * 1e-3) / 1e12
+    return {
+        "bound": "mfma",
+        "kernel": dom,
+        "achieved": round(achieved, 1),
+        "peak": MFMA_BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+        "traffic": None,
+        "kernel_ms": round(avg, 4),
+        # launches differ in rows (row blocks of 16384 tokens and the last,
+        # shorter one): the mean over the step's launches
+        "alg_flops_per_launch": round(flops[dom] / per_step),
+        "step": {"model_flops": model, "achieved_TFLOPs": round(step_tf, 1),
+                 "frac": round(step_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                 "note": "the reference's three products 3*2*N*H*V over the step time"},
+        "kernels": per,
+        "other_ms_per_step": round(ms_step - timed_ms, 3),
+        "active_rows": n_act,
+        "kernels_ms": {k: round(v[0], 4) for k, v in kstats.items()},
+    }
+
+
+def lm_head_tiles_roofline(inp, kstats, ms_step):
+    """Config 5 on the hand-written tile kernels (impl="tiles"): the step
+    against the dense bf16 MFMA peak on the reference's three products
+    (3 x 2*N*H*V, the model's flops), and each kernel's executed flops (the
+    work skipping is exact: blocks of 64 tokens none of which needs obar run
+    the log-sum-exp pass only, and the dW pass visits the 32-token tiles
+    holding a token with a non-zero gradient)."""
 
     N = inp["B"] * inp["T"]
     V, H = inp["V"], inp["hidden"].shape[-1]
@@ -987,6 +1099,7 @@ def compact(r):
     keep["roofline"] = {k: rf.get(k) for k in ("bound", "kernel", "achieved", "peak", "unit",
                                                 "frac", "kernel_ms", "alg_bytes_per_launch",
                                                 "alg_flops_per_launch", "step", "dweight",
+                                                "kernels", "other_ms_per_step", "active_rows",
                                                 "kernels_ms") if k in rf}
     keep["cpu_baseline"] = r.get("cpu_baseline")
     if r.get("variants"):

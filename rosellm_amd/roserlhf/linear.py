@@ -355,9 +355,12 @@ class _ChunkedLinearPolicy(torch.autograd.Function):
     diagnostics also receive gradients.  Outputs as ``_FusedPolicy``."""
 
     @staticmethod
-    def forward(ctx, params: nat.RrlPolicyParams, skip_masked: bool, row_block: int,
+    def forward(ctx, params: nat.RrlPolicyParams, opts: Tuple[bool, bool], row_block: int,
                 hidden: Tensor, weight: Tensor, target_ids: Tensor, old: Tensor, adv: Tensor,
                 mask: Tensor):
+        # opts: (skip_masked, the caller's grad mode; forward itself runs with
+        # grad mode off)
+        skip_masked, grad_mode = opts
         kind = params.kind
         dev = nat.require_device(hidden, weight, target_ids, old, adv, mask)
         B, T = _prepare(hidden, weight, target_ids)
@@ -385,7 +388,7 @@ class _ChunkedLinearPolicy(torch.autograd.Function):
         L._raise_flags(nat.read_status(status), kind)
 
         need_h, need_w = ctx.needs_input_grad[3], ctx.needs_input_grad[4]
-        eager = torch.is_grad_enabled() and (need_h or need_w)
+        eager = grad_mode and (need_h or need_w)
         tflat = tkeep.reshape(N)
         lse = torch.zeros(N, dtype=acc, device=dev)
         logp = torch.zeros(N, dtype=acc, device=dev)
@@ -788,7 +791,8 @@ def fused_linear_policy_loss(
     old_d = L._on_device(old_logprobs, hidden)
     adv_d = L._on_device(advantages, hidden)
     obj, d1, d2, d3, logp, trusted = _ChunkedLinearPolicy.apply(
-        p, bool(skip_masked_rows), int(row_block), hidden, weight, target_ids,
+        p, (bool(skip_masked_rows), torch.is_grad_enabled()), int(row_block), hidden, weight,
+        target_ids,
         old_d.expand(prefix), adv_d.expand(prefix), mask.expand(prefix))
     out = L._token_local_output(kind, obj, d1, d2, d3, trusted)
     return (out, _cfg.as_reference_dtype(logp, hidden)) if return_logprobs else out
