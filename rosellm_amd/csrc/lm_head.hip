@@ -962,8 +962,9 @@ __global__ __launch_bounds__(256) void lm_token_records_kernel(int64_t n, int32_
   for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * 256) {
     const int32_t a = tgt[i];
-    const float gi = g[i];
     const bool ok = a >= 0 && a < V;
+    // a token without a valid target has no gradient, whatever g holds
+    const float gi = ok ? g[i] : 0.f;
     out[i] = make_float4(__int_as_float(ok ? a : -1), gi, lse[i] * kLog2e,
                          ok ? gi * -expm1f(logp[i]) : 0.f);
   }
@@ -1003,8 +1004,11 @@ __global__ __launch_bounds__(256) void lm_dhidden_kernel(int64_t n, int32_t H, i
                                                          int64_t dh_ld) {
   for (int64_t i = blockIdx.x; i < n; i += gridDim.x) {
     const int32_t a = tgt[i];
-    const float gi = g[i];
-    const bool ok = a >= 0 && a < V && gi != 0.f;
+    const bool valid = a >= 0 && a < V;
+    // a token without a valid target has no gradient (its obar row may be
+    // unwritten), whatever g holds
+    const float gi = valid ? g[i] : 0.f;
+    const bool ok = valid && gi != 0.f;
     const float ct = ok ? -expm1f(logp[i]) : 0.f;
     const uint16_t* wr = w + (int64_t)(ok ? a : 0) * w_ld;
     const float* orow = obar + i * obar_ld;

@@ -311,6 +311,7 @@ class _ChunkedLinearLogprobs(torch.autograd.Function):
         L._raise_flags(nat.read_status(status) & nat.FLAG_TARGET_RANGE, check.kind)
         lse = torch.zeros(N, dtype=acc, device=dev)
         logp = torch.zeros(N, dtype=acc, device=dev)
+        computed = None  # token rows whose lse exists (None: all)
         if weight_mask is None:
             _logprob_rows(h2, w, tflat, None, lse, logp, status, row_block)
         else:
@@ -323,8 +324,11 @@ class _ChunkedLinearLogprobs(torch.autograd.Function):
             if not (skip_masked or check.kind == nat.OBJ_NLL):
                 _logprob_rows(h2, w, tflat, torch.nonzero(~live).reshape(-1), lse, logp, status,
                               row_block)
+            else:
+                computed = live
         if nat.read_status(status) & nat.FLAG_TARGET_RANGE:
             L._raise_flags(nat.FLAG_TARGET_RANGE, check.kind)
+        ctx.computed = computed
         ctx.save_for_backward(h2, w, tflat, lse, logp)
         ctx.meta = (hidden.shape, row_block)
         ctx.set_materialize_grads(False)
@@ -339,6 +343,10 @@ class _ChunkedLinearLogprobs(torch.autograd.Function):
         h2, w, tflat, lse, logp = ctx.saved_tensors
         shape, row_block = ctx.meta
         gc = g.reshape(-1).to(lse.dtype).contiguous()
+        if ctx.computed is not None:
+            # an ignored label or a skipped token has a constant log-prob: no
+            # gradient, whatever the upstream gradient holds there
+            gc = torch.where(ctx.computed, gc, torch.zeros((), dtype=gc.dtype, device=gc.device))
         dh, dw = _chunked_backward(h2, w, tflat, lse, logp, gc, need_h, need_w, row_block)
         return (*nones, (dh.view(shape) if dh is not None else None), dw, None, None)
 
@@ -637,16 +645,19 @@ class _LinearLogprobs(torch.autograd.Function):
         # with skip_masked their log-probs are not needed either (value 2: a
         # block of 64 such tokens is not computed, its log-probs are 0).
         need_rows = None
+        computed = None  # token rows whose lse exists (None: all)
         if need and weight_mask is not None:
             live = weight_mask.reshape(N) != 0
             if skip_masked:
                 need_rows = torch.where(live, 1, 2).to(torch.uint8).contiguous()
+                computed = live
             else:
                 need_rows = live.to(torch.uint8).contiguous()
         lse, logp, obar, flags = lm_head_forward(h2, w, tgt32, need, status, need_rows)
         if flags & nat.FLAG_TARGET_RANGE:
             L._raise_flags(nat.FLAG_TARGET_RANGE, check.kind)
         ctx.save_for_backward(h2, w, tgt32, lse, logp, obar)
+        ctx.computed = computed
         ctx.hidden_shape = hidden.shape
         ctx.set_materialize_grads(False)
         return logp.view(hidden.shape[:-1])
@@ -658,6 +669,11 @@ class _LinearLogprobs(torch.autograd.Function):
             return None, None, None, None, None, None
         h2, w, tgt32, lse, logp, obar = ctx.saved_tensors
         gc = g.reshape(-1).to(torch.float32).contiguous()
+        if ctx.computed is not None:
+            # a skipped token's log-prob is the constant 0: no gradient (its
+            # lse and obar were never formed); ignored labels (target -1) are
+            # left out by the kernels themselves
+            gc = torch.where(ctx.computed, gc, torch.zeros((), dtype=gc.dtype, device=gc.device))
         dh, dw = lm_head_backward(h2, w, tgt32, lse, logp, obar, gc, need_h, need_w)
         return (None, (dh.view(ctx.hidden_shape) if dh is not None else None), dw, None, None,
                 None)

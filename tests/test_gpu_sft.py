@@ -226,3 +226,42 @@ def test_linear_causal_lm_loss(device, ignore_index, impl):
     assert (hd.grad[:, -1] == 0).all()
     _product_check(hd.grad[:, :-1].reshape(-1, H), dl, w, "dhidden", transpose=False)
     _product_check(wd.grad, dl, hs.reshape(-1, H), "dweight", transpose=True)
+
+
+@pytest.mark.parametrize("impl", ["tiles", "chunked"])
+def test_ignored_labels_take_no_gradient_from_upstream(device, impl):
+    """An ignored label's log-prob is the constant 0: a non-zero upstream
+    gradient there must reach neither d hidden nor d weight.  The same
+    backward with the upstream gradient zeroed on ignored labels is the
+    expectation (bit-identical d hidden; d weight within one bf16 ulp, as the
+    tile path's dW pass may visit, and split, different token tiles)."""
+
+    from rosellm_amd.roserlhf import linear as LIN
+
+    print(f"[sft-linear-ignored-g] impl={impl}", flush=True)
+    g = _gen(107)
+    B, T, H, V = 3, 130, 256, 4160
+    h = torch.randn(B, T, H, generator=g).to(torch.bfloat16)
+    w = (torch.randn(V, H, generator=g) * (2.0 / H ** 0.5)).to(torch.bfloat16)
+    y = _labels(g, (B, T), V, frac_ignored=0.3)
+    r = torch.randn(B, T, generator=g) + 2.0  # non-zero everywhere
+    keep = (y != -100).float()
+
+    def grads(up):
+        hd = h.to(device).requires_grad_()
+        wd = w.to(device).requires_grad_()
+        lp = LIN.linear_label_logprobs(hd, wd, y.to(device), -100, impl=impl)
+        (lp * up.to(device)).sum().backward()
+        return lp.detach().cpu(), hd.grad.cpu(), wd.grad.cpu()
+
+    lp_a, dh_a, dw_a = grads(r)
+    lp_b, dh_b, dw_b = grads(r * keep)
+    ign = y == -100
+    assert ign.any() and (lp_a[ign] == 0).all()
+    assert torch.equal(lp_a, lp_b)
+    assert (dh_a[ign] == 0).all(), "an ignored label passed gradient to d hidden"
+    assert torch.equal(dh_a, dh_b)
+    from test_gpu_linear import _ulp16 as _bf16_ulp
+
+    diff = (dw_a.double() - dw_b.double()).abs()
+    assert (diff <= _bf16_ulp(dw_b.double()).abs() + 1e-30).all(), float(diff.max())
