@@ -12,6 +12,8 @@ logits tie often) resolve lowest index first on both sides.
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -283,11 +285,45 @@ def test_resident_nucleus_rows(device, top_p):
     x[3] = torch.randn(V, generator=g) * 0.01
     x[5] = torch.round(x[5]) / 4.0
     x = x.to(torch.bfloat16)
+    # The hand-over is decided by the number of bfloat16 keys from the cut's
+    # lower bound x_lo up to the row maximum: more than the kernel's 4096
+    # counts sends the row to the fill-in launch.  Recomputed here with the
+    # kernel's formula: the flat row 3 lies far beyond (about 32000 keys), the
+    # N(0, 3) row 0 far inside when x_lo stays above zero (top_p 0.5, 0.9).
+    spans = [_nucleus_key_span(x[i], top_p) for i in range(B)]
+    print(f"[sampler] nucleus p={top_p}: keys from x_lo up per row {spans}", flush=True)
+    assert spans[3] >= 2 * 4096, "row 3 no longer reaches the fill-in launch"
+    if top_p < 0.99:
+        assert spans[0] <= 4096 // 2, "row 0 no longer takes the resident nucleus path"
     kw = dict(temperature=1.0, top_k=0, top_p=top_p, do_sample=True)
     for off in range(3):
         out = RI.sample_next_token_batch(x.to(device), seed=23, offset=off, **kw)
         tok = _check(x, out, seed=23, offset=off, what=f"nucleus p={top_p} off={off}", **kw)
         assert (tok >= 0).all() and (tok < V).all()
+
+
+def _bf16_key(v):
+    """The kernels' ordered 16-bit key of a value rounded toward zero to
+    bfloat16 (float_key: +-0 share a key; negative values below positive)."""
+
+    b = (int(torch.tensor([v], dtype=torch.float32).view(torch.int32).item()) >> 16) & 0xFFFF
+    if b & 0x7FFF == 0:
+        b = 0
+    return (~b & 0xFFFF) if b & 0x8000 else (b | 0x8000)
+
+
+def _nucleus_key_span(row, top_p, temperature=1.0):
+    """kmax - klo of the resident nucleus path for one bfloat16 row: x_lo =
+    M + log2((1 - top_p) Z / (2 V)) / c2 with Z = sum 2^((x - M) c2) and c2 =
+    log2(e) / T; klo is one key below x_lo's."""
+
+    r = row.double()
+    V = r.numel()
+    M = float(r.max())
+    c2 = math.log2(math.e) / temperature
+    Z = float(torch.exp2((r - M) * c2).sum())
+    xlo = M + math.log2((1.0 - top_p) * Z / (2.0 * V)) / c2
+    return _bf16_key(M) - max(_bf16_key(xlo) - 1, 0)
 
 
 @pytest.mark.parametrize("case", ["spike", "cold", "masked_head"])
