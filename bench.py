@@ -112,7 +112,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # Sequences of the CPU plan's sub-batch per config (C1 whole; C4's are 8192 long).
 CPU_SEQS = {"c1": 32, "c2": 16, "c3": 16, "sft": 16, "c4": 2, "c5": 16}
 # Configurations timed after the headline, reported under "variants".
-VARIANTS = ["c1", "c3", "c3_gspo_token", "c4", "sft", "sample", "c5"]
+VARIANTS = ["c1", "c3", "c3_gspo_token", "c4", "c4_tau_default", "sft", "sample", "c5"]
 
 
 def log(msg: str) -> None:
@@ -569,8 +569,10 @@ def timed_steps(step, steps, kernels, prepare=None):
     from rosellm_amd import _native as nat
 
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * steps)]
+    host = [0.0] * (steps + 1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    host[0] = t0
     out = None
     for i in range(steps):
         if prepare is not None:
@@ -578,8 +580,14 @@ def timed_steps(step, steps, kernels, prepare=None):
         ev[2 * i].record()
         out = step()
         ev[2 * i + 1].record()
+        host[i + 1] = time.perf_counter()
     torch.cuda.synchronize()
-    wall = None if prepare is not None else time.perf_counter() - t0
+    t1 = time.perf_counter()
+    wall = None if prepare is not None else t1 - t0
+    # host time from one step() call's return to the next one's (the last one
+    # up to the closing synchronisation)
+    host_ms = [(host[i + 1] - host[i]) * 1e3 for i in range(steps)]
+    host_ms[-1] += (t1 - host[steps]) * 1e3
     if prepare is None:
         # consecutive steps: the time from one step's start to the next one's
         step_ms = [ev[2 * i].elapsed_time(ev[2 * i + 2]) for i in range(steps - 1)]
@@ -593,7 +601,8 @@ def timed_steps(step, steps, kernels, prepare=None):
         step()
     torch.cuda.synchronize()
     nat.time_calls()
-    return {"wall_s": wall, "step_ms": step_ms, "out": out, "launches": timed}
+    return {"wall_s": wall, "step_ms": step_ms, "host_ms": host_ms, "out": out,
+            "launches": timed}
 
 
 def kernel_stats(launches, kernels, steps):
@@ -618,8 +627,12 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
     import torch
 
     objective_override = None
+    kw_override = None
     if name == "c3_gspo_token":
         name, objective_override = "c3", "gspo_token"
+    elif name == "c4_tau_default":
+        # SAPO at the reference's default temperatures (losses.py:361-362)
+        name, kw_override = "c4", dict(tau_positive=1.0, tau_negative=1.05)
     cfg = CONFIGS[name]
     log(f"[bench] config {name}{'/' + objective_override if objective_override else ''}: "
         f"generating inputs")
@@ -631,6 +644,12 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
     N, V = inp["B"] * inp["T"], inp["V"]
     objective = objective_override or cfg["objective"]
     cfg = dict(cfg, objective=objective)
+    if objective_override == "gspo_token":
+        cfg["workload"] = ("C3: GSPO-token objective fwd+bwd (losses.py:276-352), 256x1024 "
+                           "tokens, V=151936 bf16")
+    if kw_override is not None:
+        cfg["kw"] = dict(cfg["kw"], **kw_override)
+        cfg["workload"] = cfg["workload"] + ", SAPO tau (1.0, 1.05) (reference defaults)"
     # GSPO needs every token's log-prob before any gradient: its fused entry is
     # a forward sweep and a backward sweep (rrl_logprob_fwd, rrl_logprob_bwd).
     gspo_like = objective in ("gspo", "gspo_token")
@@ -839,6 +858,10 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
         "ms_per_step_median": round(ms_median, 4),
         "step_time": ("wall clock over the timed steps" if res["wall_s"] is not None else
                       "mean of per-step events (the logits are regenerated between steps)"),
+        # every timed step: device time from its start to the next step's
+        # start (events), and the host's time between step() returns
+        "per_step_ms": {"device": [round(v, 3) for v in step_ms],
+                        "host": [round(v, 3) for v in res["host_ms"]]},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
