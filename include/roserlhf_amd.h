@@ -392,6 +392,18 @@ RRL_API int rrl_lm_head_dweight(const void* hidden, const void* weight, int32_t 
                     const float* g, void* workspace, void* dweight, int32_t dw_dtype,
                     int64_t dw_ld, void* stream);
 
+/* ---- operand layout for the chunked LM head's library GEMMs ----
+ * No counterpart in the reference: the chunked path of the LM head
+ * (roserlhf/linear.py, standing in for rosetrainer/model.py:641's F.linear
+ * and its backward) hands the GEMM library the weight as a contiguous [H, V]
+ * copy for d hidden = dL W, the layout it runs fastest.
+ * rrl_transpose16: dst[c * dst_ld + r] = src[r * src_ld + c] for r < rows,
+ * c < cols, 2-byte elements (bf16/f16 bits copied unchanged), asynchronous on
+ * `stream`.  16-byte accesses when both bases are 16-byte aligned and both
+ * strides are multiples of 8 elements. */
+RRL_API int rrl_transpose16(const void* src, int64_t rows, int64_t cols, int64_t src_ld,
+                    void* dst, int64_t dst_ld, void* stream);
+
 /* ---- rollout side: next-token sampling with behaviour log-probs -------------
  * Replaces the token choice of roseinfer/engine.py:1103-1171
  * (InferenceEngine._sample_next_token_batch, its PyTorch path) and adds the

@@ -120,6 +120,7 @@ SIGNATURES = {
     "rrl_lm_head_dhidden": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P, _I64, _P]),
     "rrl_lm_head_dweight_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "rrl_lm_head_dweight": (ctypes.c_int, [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32, _I64, _P]),
+    "rrl_transpose16": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _I64, _P]),
     "rrl_philox4x32_10": (None, [ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32)]),
 }
 

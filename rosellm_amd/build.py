@@ -29,6 +29,7 @@ SOURCES = [
     "estimators.hip",
     "sampler.hip",
     "lm_head.hip",
+    "layout.hip",
 ]
 
 ARCH = os.environ.get("ROSELLM_AMD_ARCH", "gfx950")

@@ -283,3 +283,25 @@ def test_chunked_upstream_scale(device, objective):
         num, den = (a - b).norm(dim=-1), b.norm(dim=-1)
         worst = float(torch.where(den > 0, num / den.clamp_min(1e-30), num).max())
         assert worst <= 1e-5, f"{what}: row-norm rel diff {worst:.3e}"
+
+
+@pytest.mark.parametrize("rows,cols,pad,offset", [(151936 // 16, 1024, 0, 0), (1000, 1030, 0, 0),
+                                                  (777, 129, 24, 0), (300, 64, 8, 3),
+                                                  (65, 1, 0, 0), (1, 70, 0, 1)])
+def test_transpose16_is_exact(device, rows, cols, pad, offset):
+    """rrl_transpose16 (the weight's [H, V] copy for the d hidden GEMM) against
+    torch's transpose, bit for bit: partial 64 x 64 tiles on both sides,
+    padded source rows, and sources off 16-byte alignment (the element-wise
+    path)."""
+
+    from rosellm_amd import _native as nat
+
+    g = _gen(rows * 3 + cols)
+    base = torch.randn(rows * (cols + pad) + offset, generator=g).to(torch.bfloat16).to(device)
+    src = base[offset:].view(rows, cols + pad)[:, :cols]
+    dst = torch.full((cols, rows + 8), float("nan"), dtype=torch.bfloat16, device=device)
+    nat.call("rrl_transpose16", src.data_ptr(), rows, cols, src.stride(0), dst.data_ptr(),
+             dst.stride(0), nat.stream_ptr(device))
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:, :rows].view(torch.int16), src.t().contiguous().view(torch.int16))
+    assert torch.isnan(dst[:, rows:].float()).all(), "a store landed past the rows"
