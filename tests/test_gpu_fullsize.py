@@ -265,8 +265,9 @@ def _rows_close(a, b, tol, what, chunk=16384):
     return worst
 
 
-@pytest.mark.parametrize("impl", ["chunked", "tiles"])
-def test_config5_linear_fullsize_against_exact_rows(device, impl):
+@pytest.mark.parametrize("impl,objective", [("chunked", "clipped"), ("tiles", "clipped"),
+                                            ("chunked", "gspo")])
+def test_config5_linear_fullsize_against_exact_rows(device, impl, objective):
     """Config 5 in full (262144 tokens, hidden 1024, V = 151936 bf16) through
     both LM-head implementations, pinned without the kernels under test:
 
@@ -275,8 +276,11 @@ def test_config5_linear_fullsize_against_exact_rows(device, impl):
       float64, 2048 tokens at a time (for the chunked path rounded to bf16
       first, through float32 as its GEMM's float32 accumulator rounds them:
       the logits it consumes);
-    * d loss / d logp comes from oracle.ppo_clip in float64 on the CPU, over
-      all 262144 tokens, on those log-probs.
+    * d loss / d logp comes from oracle.ppo_clip (GSPO: oracle.gspo, config
+      3's clip band, per-sequence advantages) in float64 on the CPU, over all
+      262144 tokens, on those log-probs.  GSPO takes the chunked path's other
+      backward: every log-prob first, then the active blocks' logits formed
+      a second time.
 
     Checks: every token's log-prob (the bars of test_gpu_linear for each
     implementation); the d hidden rows of 64 random tokens and the d weight
@@ -285,21 +289,23 @@ def test_config5_linear_fullsize_against_exact_rows(device, impl):
 
     from test_gpu_linear import _ulp16
 
-    print(f"[fullsize] config 5 LM head ({impl}) vs float64 pins", flush=True)
+    print(f"[fullsize] config 5 LM head ({impl}, {objective}) vs float64 pins", flush=True)
     cfg = bench.CONFIGS["c5"]
     with torch.no_grad():
         inp = bench.make_inputs(cfg, device, 1234)
     B, T = inp["B"], inp["T"]
     h, w = inp["hidden"], inp["weight"]
     t, old, mask = inp["actions"], inp["old"], inp["mask"]
-    adv = R.group_standardized_advantages(inp["rewards"]).reshape(-1)[:, None].expand(B, T)
-    kw = cfg["kw"]
+    adv_seq = R.group_standardized_advantages(inp["rewards"]).reshape(-1)
+    adv = adv_seq[:, None].expand(B, T)
+    kw = cfg["kw"] if objective == "clipped" else bench.CONFIGS["c3"]["kw"]
+    adv_arg = adv if objective == "clipped" else adv_seq
     del inp
     _free()
     N, H, V = B * T, h.shape[-1], w.shape[0]
     hd, wd = h.detach().clone().requires_grad_(), w.detach().clone().requires_grad_()
-    out, lp = R.fused_linear_policy_loss(hd, wd, t, old, adv, mask, return_logprobs=True,
-                                         impl=impl, **kw)
+    out, lp = R.fused_linear_policy_loss(hd, wd, t, old, adv_arg, mask, return_logprobs=True,
+                                         impl=impl, objective=objective, **kw)
     out.loss.backward()
     gh, gw = hd.grad, wd.grad
     del hd, wd, out
@@ -337,12 +343,15 @@ def test_config5_linear_fullsize_against_exact_rows(device, impl):
         if impl == "chunked":
             bound = bound + _ulp16(xt64.abs().cpu()).to(device) + _ulp16(xmax.cpu()).to(device)
         worst = float((err / bound).max())
-        print(f"[fullsize] c5 {impl}: every log-prob, max err/bound {worst:.3f} "
+        print(f"[fullsize] c5 {impl} {objective}: every log-prob, max err/bound {worst:.3f} "
               f"(max abs err {float(err.max()):.2e})", flush=True)
         assert worst <= 1.0
     # d loss / d logp from the float64 oracle on the CPU
     cur = lp_ref.cpu().view(B, T).requires_grad_()
-    res = o.ppo_clip(cur, old.double().cpu(), adv.double().cpu(), mask.cpu(), **kw)
+    if objective == "clipped":
+        res = o.ppo_clip(cur, old.double().cpu(), adv.double().cpu(), mask.cpu(), **kw)
+    else:
+        res = o.gspo(cur, old.double().cpu(), adv_seq.double().cpu(), mask.cpu(), **kw)
     res["loss"].backward()
     g = cur.grad.reshape(-1).to(device)
     with torch.no_grad():
@@ -355,7 +364,8 @@ def test_config5_linear_fullsize_against_exact_rows(device, impl):
         got = gh.reshape(N, H)[idx_d].double()
         den = 2 * prop + _ulp16((ref.abs() + prop).cpu()).to(device) + 1e-30
         excess = float(((got - ref).abs() / den).max())
-        print(f"[fullsize] c5 {impl}: d hidden rows max |err|/bound {excess:.3f}", flush=True)
+        print(f"[fullsize] c5 {impl} {objective}: d hidden rows max |err|/bound {excess:.3f}",
+              flush=True)
         assert excess <= 1.0
         # 3. d weight rows of 8 vocabulary entries, summed over every token
         pv = torch.exp(xv64 - lse64[:, None])
@@ -366,7 +376,8 @@ def test_config5_linear_fullsize_against_exact_rows(device, impl):
         gotw = gw[vs_d].double()
         denw = 2 * propw + _ulp16((refw.abs() + propw).cpu()).to(device) + 1e-30
         excess_w = float(((gotw - refw).abs() / denw).max())
-        print(f"[fullsize] c5 {impl}: d weight rows max |err|/bound {excess_w:.3f}", flush=True)
+        print(f"[fullsize] c5 {impl} {objective}: d weight rows max |err|/bound {excess_w:.3f}",
+              flush=True)
         assert excess_w <= 1.0
     del gh, gw, h, w, lp, h64, w64, lse64, xt64, xmax, xv64, rows64, g
     _free()
