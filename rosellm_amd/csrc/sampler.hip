@@ -1096,6 +1096,24 @@ __device__ __forceinline__ float mx(float a, float b) { return __builtin_element
 __device__ __forceinline__ float max8(const float (&v)[8]) {
   return mx(mx(mx(v[0], v[1]), mx(v[2], v[3])), mx(mx(v[4], v[5]), mx(v[6], v[7])));
 }
+// 4 x the slot of 16-bit entry HI (the dword's high half) or low of w among
+// a top-p pass's per-key counts, in one multiply-add on the raw bits: POS,
+// bits * 4 + c (every counted key a positive number's); otherwise
+// (every counted key a negative number's) c - 4 * bits as a signed 16-bit
+// value.
+template <bool POS, bool HI>
+__device__ __forceinline__ uint32_t slot4(uint32_t w, uint32_t c) {
+  uint32_t r;
+  if constexpr (POS) {
+    if constexpr (HI) asm("v_mad_u32_u16 %0, %1, 4, %2 op_sel:[1,0,0,0]" : "=v"(r) : "v"(w), "v"(c));
+    else asm("v_mad_u32_u16 %0, %1, 4, %2" : "=v"(r) : "v"(w), "v"(c));
+  } else {
+    if constexpr (HI) asm("v_mad_i32_i16 %0, %1, -4, %2 op_sel:[1,0,0,0]" : "=v"(r) : "v"(w), "v"(c));
+    else asm("v_mad_i32_i16 %0, %1, -4, %2" : "=v"(r) : "v"(w), "v"(c));
+  }
+  return r;
+}
+
 __device__ __forceinline__ float sum8(const float (&e)[8]) {
   return ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
 }
@@ -1763,6 +1781,9 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
   __shared__ double sh_z, sh_run, sh_tgt;
   __shared__ int sh_ks, sh_ws, sh_sel;
   __shared__ float sh_x;
+  // Top-p: counts per key, later each key's weight, then two slots of
+  // fixed weights and a spare slot per lane
+  __shared__ uint32_t bins[TOPP ? TOPP_BINS + 2 + 64 : 1];
 
   const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1777,6 +1798,10 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
 #pragma unroll
   for (int k = 0; k < SL; ++k)
     x[k] = __builtin_amdgcn_raw_buffer_load_b128(src, tid * 16, k * SNT * 16, kAuxLoad);
+  if constexpr (TOPP) {
+    // the counts start at zero (ordered before their use by sweep A's barrier)
+    for (int i = tid; i < TOPP_BINS; i += SNT) bins[i] = 0u;
+  }
 
   const float iT = 1.0f / a.temp;
   const float c2 = iT * kLog2e;  // exp(y / T) = 2^(y * c2)
@@ -1960,12 +1985,13 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
       // scanned in descending key order, give the threshold group as the
       // streaming kernel's radix select does; its ties are kept lowest index
       // first (the n_keep-th found from block counts in vocabulary order).
-      // Block sums of the floored weights then place the draw as for plain
-      // sampling.  A row whose keys from x_lo up outnumber the counts takes
-      // the streaming path in this launch.
+      // The counts then become each key's floored weight, and the block sums
+      // of the weights (one LDS read per entry) place the draw as for plain
+      // sampling.  A row whose keys from x_lo up outnumber the counts is left
+      // to the fill-in launch.
       constexpr int KB = Bits<Tag>::KB;
       constexpr int NB = TOPP_BINS;
-      __shared__ uint32_t bins[NB];
+      constexpr int PB = NB / SNT;  // descending key positions per thread
       __shared__ unsigned long long red_u[SWAVES];
       __shared__ double blk_w[SL][SWAVES];
       __shared__ double slab_w[SL];
@@ -1983,50 +2009,83 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
       // a key at or below x_lo's (the conversion truncates by less than one step)
       uint32_t klo = xlo > -__FLT_MAX__ ? float_key<KB>(Bits<Tag>::bits_of(xlo)) : 0u;
       klo = klo > 0u ? klo - 1u : 0u;
-      if (klo == 0u || kmax < klo || kmax - klo >= (uint32_t)NB) {
+      // An entry's slot among the counts is its key - klo, counted when below
+      // R = kmax - klo + 1.  When every key from klo to kmax is a positive
+      // number's, the slot is the raw bits minus klo's; when every one is a
+      // negative number's, a constant minus the raw bits: (bits ^ m) + c
+      // either way.
+      const bool pos = klo > 0x8000u, neg = kmax < 0x8000u;
+      if (klo == 0u || kmax < klo || kmax - klo >= (uint32_t)NB || !(pos || neg)) {
         // The keys from x_lo up outnumber the counts (a flat row over many
-        // binades): the fill-in launch that follows takes this row.
+        // binades) or cross zero: the fill-in launch that follows takes this
+        // row.
         if (tid == 0) a.token[r] = -1;
         return;
       }
       const uint32_t R = kmax - klo + 1u;
-      const float flo = Bits<Tag>::val(key_bits<KB>(klo));
-      for (int i = tid; i < (int)R; i += SNT) bins[i] = 0u;
+      // 4 x the slot, from slot4's constant: POS 4 (0x8000 - klo), else
+      // 4 (-1 - klo); a lane past the row's end (the last slab) takes one
+      // that puts it far above 4 (R + 1).
+      const uint32_t c_in = pos ? 4u * (0x8000u - klo) : 4u * (0xffffffffu - klo);
+      const uint32_t c_out = pos ? 0xfff00000u : 0x80000000u;
       if (tid == 0) {
         sh_found = 0;
         sh_cut = 0x7fffffff;
       }
-      __syncthreads();
+      // body(slab k's vector, k, the lane inside the row, its constant), for
+      // every slab, with the two slot forms as template arguments.
+      auto pick = [](bool p, uint32_t u, uint32_t v) { return p ? u : v; };  // by value
+      auto each_slab = [&](auto body) __attribute__((always_inline)) {
 #pragma unroll
-      for (int k = 0; k < SL; ++k) {
-        if (k < nslab) {
-          const bool inside = k * SNT + tid < nvec;
-          float v[8];
-          unpack8<Tag>(x[k], v);
-          const uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            if (inside && v[i] >= flo) {
-              const uint32_t b = (w[i >> 1] >> (16 * (i & 1))) & 0xffffu;
-              atomicAdd(&bins[float_key<KB>(b) - klo], 1u);
-            }
+        for (int k = 0; k < SL; ++k) {
+          if (k < nslab) {
+            const bool in_row = k < nfull || k * SNT + tid < nvec;
+            body(x[k], k, in_row, pick(in_row, c_in, c_out));
           }
         }
-      }
+      };
+      auto slots8 = [](u32x4 xv, uint32_t c, uint32_t (&t)[8], auto ps) __attribute__((always_inline)) {
+        constexpr bool P_ = decltype(ps)::value;
+        const uint32_t w[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          t[2 * j] = slot4<P_, false>(w[j], c);
+          t[2 * j + 1] = slot4<P_, true>(w[j], c);
+        }
+      };
+      // Counts per key from klo up (the counts were cleared at the start).
+      const uint32_t R4 = 4u * R;
+      const uint32_t spare = 4u * (uint32_t)(TOPP_BINS + 2 + lane);
+      auto count = [&](auto ps) __attribute__((always_inline)) {
+        each_slab([&](u32x4 xv, int, bool, uint32_t c) __attribute__((always_inline)) {
+          uint32_t t[8];
+          slots8(xv, c, t, ps);
+          // Every lane adds: an entry outside the counts into the lane's own
+          // spare slot past them (no branch per entry, no shared address).
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            atomicAdd(reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(bins) +
+                                                  (t[i] < R4 ? t[i] : spare)),
+                      1u);
+        });
+      };
+      if (pos) count(std::true_type{});
+      else count(std::false_type{});
       __syncthreads();
       // Thread t holds descending positions 4t..4t+3 (key kmax - position).
       const unsigned long long P = (unsigned long long)(a.top_p * kMassScale);
-      auto fx = [&](int d) {  // the fixed-point mass of one entry at position d
-        return (unsigned long long)((double)pn(Bits<Tag>::val(key_bits<KB>(kmax - (uint32_t)d))) *
-                                    kMassScale);
+      auto pkey = [&](int d) {  // p of the key at position d
+        return pn(Bits<Tag>::val(key_bits<KB>(kmax - (uint32_t)d)));
       };
-      uint32_t c4[NB / SNT];
+      // its fixed-point mass floor(p 2^52)
+      auto fixed = [](float p) { return (unsigned long long)((double)p * kMassScale); };
+      uint32_t c4[PB];
       unsigned long long lsum = 0;
 #pragma unroll
-      for (int j = 0; j < NB / SNT; ++j) {
-        const int d = tid * (NB / SNT) + j;
+      for (int j = 0; j < PB; ++j) {
+        const int d = tid * PB + j;
         c4[j] = d < (int)R ? bins[R - 1 - d] : 0u;
-        lsum += c4[j] ? c4[j] * fx(d) : 0ull;
+        lsum += c4[j] ? c4[j] * fixed(pkey(d)) : 0ull;
       }
       unsigned long long inc = lsum;
 #pragma unroll
@@ -2036,123 +2095,176 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
       }
       if (lane == 63) red_u[wave] = inc;
       __syncthreads();
+      // The masses above each position give the threshold group (the one
+      // holding P) and, in place of the counts (every count has been read),
+      // each key's floored weight: p if kept, else 1e-9; the group's p if
+      // any of it is kept.  Slot R, where every entry below klo reads, holds
+      // 1e-9 and slot R + 1 zero.  Block sums of the weights then need one
+      // LDS read per entry instead of an exponential.
       unsigned long long above = inc - lsum;
       for (int w = 0; w < wave; ++w) above += red_u[w];
 #pragma unroll
-      for (int j = 0; j < NB / SNT; ++j) {
-        const int d = tid * (NB / SNT) + j;
-        const unsigned long long f = c4[j] ? fx(d) : 0ull, m = c4[j] * f;
-        if (c4[j] > 0 && above <= P && P - above < m) {  // one bin: the group holding P
+      for (int j = 0; j < PB; ++j) {
+        const int d = tid * PB + j;
+        const float pj = pkey(d);
+        const unsigned long long f = c4[j] ? fixed(pj) : 0ull, m = c4[j] * f;
+        float wk = 1e-9f;
+        if (above <= P && P - above >= m) {
+          wk = fmaxf(pj, 1e-9f);  // every entry at this key kept
+        } else if (c4[j] > 0 && above <= P) {  // one bin: the group holding P
+          unsigned long long nk = f > 0 ? (P - above) / f : c4[j];
+          if (d == 0 && nk == 0) nk = 1;  // the row maximum is always kept
+          wk = nk > 0 ? fmaxf(pj, 1e-9f) : 1e-9f;
           sh_found = 1;
           sh_pth = kmax - (uint32_t)d;
           sh_a0 = above;
           sh_c0 = c4[j];
           sh_each = f;
         }
+        if (d < (int)R) bins[R - 1 - d] = __float_as_uint(wk);
         above += m;
+      }
+      if (tid == 0) {
+        bins[R] = __float_as_uint(1e-9f);
+        bins[R + 1] = 0u;
       }
       __syncthreads();
       const bool found = sh_found != 0;
-      const float fth = Bits<Tag>::val(key_bits<KB>(sh_pth));
+      const uint32_t pth = sh_pth;
+      const float fth = Bits<Tag>::val(key_bits<KB>(pth));
       const unsigned long long C0 = sh_c0, each = sh_each;
       unsigned long long n_keep = found ? (each > 0 ? (P - sh_a0) / each : C0) : 0;
       // The first token in descending order (the row maximum) is always kept.
-      if (found && sh_pth == kmax && n_keep == 0) n_keep = 1;
-      if (found && n_keep > 0 && n_keep < C0) {
-        // The n_keep-th entry of the group in vocabulary order: block (k, w)
-        // counts, their scan, then the block's lanes.
+      if (found && pth == kmax && n_keep == 0) n_keep = 1;
+      // Some but not all of the threshold group kept: lowest index first.
+      const bool partial = found && n_keep > 0 && n_keep < C0;
+      // The floored weight of each key tied at the threshold, and of a kept one.
+      const float wth = n_keep > 0 ? fmaxf(pn(fth), 1e-9f) : 1e-9f;
+      if (found) {
+        // Block sums with every tie at wth (a lane past the row's end reads
+        // slot R + 1, zero), and each block's count of ties.
+        // Lane k keeps slab k's block sum and tie count until the end.
+        const uint32_t tt4 = 4u * (pth - klo);
+        float my_w = 0.0f;
+        int my_c = 0;
+        auto weigh = [&](auto ps) __attribute__((always_inline)) {
+          each_slab([&](u32x4 xv, int k, bool in_row, uint32_t c) __attribute__((always_inline)) {
+            const uint32_t Rk4 = in_row ? R4 : R4 + 4u;
+            uint32_t t[8];
+            slots8(xv, c, t, ps);
+            float w8[8];
+            int tot = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const uint32_t off = t[i] < Rk4 ? t[i] : Rk4;
+              w8[i] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(bins) + off);
+              tot += __popcll(__ballot(t[i] == tt4));
+            }
+            const float sw = wave_sum_dpp(sum8(w8));
+            my_w = lane == k ? sw : my_w;
+            my_c = lane == k ? tot : my_c;
+          });
+        };
+        if (pos) weigh(std::true_type{});
+        else weigh(std::false_type{});
+        if (lane < nslab) {
+          blk_w[lane][wave] = (double)my_w;
+          cnt_b[lane * SWAVES + wave] = my_c;
+        }
+        __syncthreads();
+        if (partial) {
+          // Wave 0: the ties before each block in vocabulary order; a block's
+          // ties past the n_keep-th drop from wth to 1e-9, and the block
+          // holding the n_keep-th is recorded.
+          if (wave == 0) {
+            constexpr int PER = (SL * SWAVES + 63) / 64;
+            const int E = nslab * SWAVES;
+            const long long tk = (long long)n_keep - 1;
+            const double drop = (double)wth - (double)1e-9f;
+            int c[PER], ls_ = 0;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+              const int e = lane * PER + j;
+              c[j] = e < E ? cnt_b[e] : 0;
+              ls_ += c[j];
+            }
+            int incl = ls_;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+              const int y = __shfl_up(incl, o, 64);
+              if (lane >= o) incl += y;
+            }
+            int run = incl - ls_;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+              const int e = lane * PER + j;
+              if (c[j] > 0) {
+                if (run <= tk && tk < run + c[j]) {
+                  sh_blk = e;
+                  sh_off = (int)(tk - run);
+                }
+                const long long kept =
+                    (long long)n_keep - run < 0 ? 0 : std::min<long long>((long long)n_keep - run, c[j]);
+                if (kept < c[j]) blk_w[e / SWAVES][e % SWAVES] -= (double)(c[j] - kept) * drop;
+              }
+              run += c[j];
+            }
+          }
+          __syncthreads();
+          // The n_keep-th tie itself: the recorded block's wave.
+          const int kb2 = sh_blk / SWAVES, wb2 = sh_blk % SWAVES, off = sh_off;
+          if (wave == wb2) {
+            u32x4 xv = x[0];
+#pragma unroll
+            for (int k = 1; k < SL; ++k) xv = k == kb2 ? x[k] : xv;
+            float v[8];
+            unpack8<Tag>(xv, v);
+            const bool inside = kb2 * SNT + tid < nvec;
+            uint32_t below = 0;
+            int h = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const unsigned long long m = __ballot(inside && v[i] == fth);
+              below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                __builtin_amdgcn_mbcnt_lo((uint32_t)m, below));
+              h += (int)((m >> lane) & 1ull);
+            }
+            if ((int)below <= off && off < (int)below + h) {
+              int seen = (int)below;
+#pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                if (inside && v[i] == fth) {
+                  if (seen == off) sh_cut = (kb2 * SNT + tid) * 8 + i;
+                  ++seen;
+                }
+              }
+            }
+          }
+        }
+      } else {
+        // No threshold group (the fixed-point masses fall short of top_p):
+        // every entry is kept.
 #pragma unroll
         for (int k = 0; k < SL; ++k) {
           if (k < nslab) {
             const bool inside = k * SNT + tid < nvec;
             float v[8];
             unpack8<Tag>(x[k], v);
-            int tot = 0;
+            float w8[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) tot += __popcll(__ballot(inside && v[i] == fth));
-            if (lane == 0) cnt_b[k * SWAVES + wave] = tot;
-          }
-        }
-        __syncthreads();
-        if (wave == 0) {
-          constexpr int PER = (SL * SWAVES + 63) / 64;
-          const int E = nslab * SWAVES;
-          const long long t = (long long)n_keep - 1;
-          int c[PER], ls_ = 0;
-#pragma unroll
-          for (int j = 0; j < PER; ++j) {
-            const int e = lane * PER + j;
-            c[j] = e < E ? cnt_b[e] : 0;
-            ls_ += c[j];
-          }
-          int incl = ls_;
-#pragma unroll
-          for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
-          }
-          int run = incl - ls_;
-#pragma unroll
-          for (int j = 0; j < PER; ++j) {
-            if (c[j] > 0 && run <= t && t < run + c[j]) {
-              sh_blk = lane * PER + j;
-              sh_off = (int)(t - run);
-            }
-            run += c[j];
-          }
-        }
-        __syncthreads();
-        const int kb2 = sh_blk / SWAVES, wb2 = sh_blk % SWAVES, off = sh_off;
-        if (wave == wb2) {
-          u32x4 xv = x[0];
-#pragma unroll
-          for (int k = 1; k < SL; ++k) xv = k == kb2 ? x[k] : xv;
-          float v[8];
-          unpack8<Tag>(xv, v);
-          const bool inside = kb2 * SNT + tid < nvec;
-          uint32_t below = 0;
-          int h = 0;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const unsigned long long m = __ballot(inside && v[i] == fth);
-            below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                              __builtin_amdgcn_mbcnt_lo((uint32_t)m, below));
-            h += (int)((m >> lane) & 1ull);
-          }
-          if ((int)below <= off && off < (int)below + h) {
-            int seen = (int)below;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              if (inside && v[i] == fth) {
-                if (seen == off) sh_cut = (kb2 * SNT + tid) * 8 + i;
-                ++seen;
-              }
-            }
+            for (int i = 0; i < 8; ++i) w8[i] = inside ? fmaxf(pn(v[i]), 1e-9f) : 0.0f;
+            const float sw = wave_sum_dpp(sum8(w8));
+            if (lane == 0) blk_w[k][wave] = (double)sw;
           }
         }
         __syncthreads();
       }
-      const int cut = sh_cut;
       // floored weight of entry e (logit v): p if kept, else 1e-9
       auto wq = [&](int e, float v) {
         const bool kept =
-            !found || v > fth || (v == fth && (n_keep >= C0 || (n_keep > 0 && e <= cut)));
+            !found || v > fth || (v == fth && (n_keep >= C0 || (n_keep > 0 && e <= sh_cut)));
         return kept ? fmaxf(pn(v), 1e-9f) : 1e-9f;
       };
-#pragma unroll
-      for (int k = 0; k < SL; ++k) {
-        if (k < nslab) {
-          const bool inside = k * SNT + tid < nvec;
-          float v[8];
-          unpack8<Tag>(x[k], v);
-          float w8[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) w8[i] = inside ? wq((k * SNT + tid) * 8 + i, v[i]) : 0.0f;
-          const float sw = wave_sum_dpp(sum8(w8));
-          if (lane == 0) blk_w[k][wave] = (double)sw;
-        }
-      }
-      __syncthreads();
       if (tid < nslab * SWAVES) {
         const int k = tid >> 4;
         const double T = row_scan_d(blk_w[k][lane & 15]);
@@ -2201,7 +2313,7 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
           }
           sh_sel = (ks * SNT + tid) * 8 + pick;
           sh_x = xp;
-          sh_lq = (float)(log((double)wp) - log(sh_tot));
+          sh_lq = logf((float)((double)wp / sh_tot));
         }
       }
       __syncthreads();
