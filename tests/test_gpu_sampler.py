@@ -268,37 +268,51 @@ def test_long_list_top_p_ties(device, dtype, top_k, top_p):
         _check(x, out, seed=19, offset=off, what=f"ties {dtype} k={top_k} p={top_p} off={off}", **kw)
 
 
+@pytest.mark.parametrize("V", [
+    151936,  # 19 slabs of the 20-slab variant, last one partial
+    128256,  # 16 whole slabs
+    98296,   # 12 slabs, last one partial
+    50264,   # 7 slabs of the 8-slab variant, last one partial
+    20000,   # 3 slabs of the 4-slab variant, 451 lanes of the last
+])
 @pytest.mark.parametrize("top_p", [0.5, 0.9, 0.999])
-def test_resident_nucleus_rows(device, top_p):
+def test_resident_nucleus_rows(device, top_p, V):
     """top_p without top-k on bfloat16 rows: counts per key from the cut's
     lower bound up in registers.  Rows: N(0, 3); a dominant token; ties on a
     grid of halves (the threshold group's lowest indices kept); a flat row of
     N(0, 0.01), whose keys from the lower bound up span most binades near
     zero, so the row is handed to the fill-in launch of the streaming kernel
-    (token slot -1 in between)."""
+    (token slot -1 in between); ties on a grid of quarters; an all-negative
+    row (log-probs: every counted key a negative number's, the other form of
+    the slot arithmetic)."""
 
-    B, V = 8, 151936
+    B = 8
     g = torch.Generator().manual_seed(53)
     x = torch.randn(B, V, generator=g) * 3.0
     x[1, 777] += 25.0
     x[2] = torch.round(x[2] * 2.0) / 2.0
     x[3] = torch.randn(V, generator=g) * 0.01
     x[5] = torch.round(x[5]) / 4.0
+    x[6] = torch.log_softmax(x[6], dim=0)
     x = x.to(torch.bfloat16)
+    assert float(x[6].float().max()) < 0.0
     # The hand-over is decided by the number of bfloat16 keys from the cut's
     # lower bound x_lo up to the row maximum: more than the kernel's 4096
     # counts sends the row to the fill-in launch.  Recomputed here with the
     # kernel's formula: the flat row 3 lies far beyond (about 32000 keys), the
-    # N(0, 3) row 0 far inside when x_lo stays above zero (top_p 0.5, 0.9).
+    # N(0, 3) row 0 far inside when x_lo stays above zero (top_p 0.5, 0.9),
+    # and so does the all-negative row 6.
     spans = [_nucleus_key_span(x[i], top_p) for i in range(B)]
-    print(f"[sampler] nucleus p={top_p}: keys from x_lo up per row {spans}", flush=True)
+    print(f"[sampler] nucleus V={V} p={top_p}: keys from x_lo up per row {spans}", flush=True)
     assert spans[3] >= 2 * 4096, "row 3 no longer reaches the fill-in launch"
-    if top_p < 0.99:
+    assert spans[6] <= 4096 // 2, "row 6 no longer takes the resident nucleus path"
+    if top_p < 0.99 and V >= 50000:
         assert spans[0] <= 4096 // 2, "row 0 no longer takes the resident nucleus path"
     kw = dict(temperature=1.0, top_k=0, top_p=top_p, do_sample=True)
     for off in range(3):
         out = RI.sample_next_token_batch(x.to(device), seed=23, offset=off, **kw)
-        tok = _check(x, out, seed=23, offset=off, what=f"nucleus p={top_p} off={off}", **kw)
+        tok = _check(x, out, seed=23, offset=off, what=f"nucleus V={V} p={top_p} off={off}",
+                     **kw)
         assert (tok >= 0).all() and (tok < V).all()
 
 
