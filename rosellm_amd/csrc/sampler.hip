@@ -1974,6 +1974,8 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
 
   int tok = bi;
   float logq = 0.0f;
+  bool q_from_p = false;  // log q from the token's log-prob and G
+  float q_g = 0.0f;
   float xt_raw = M;  // the token's logit
   if (!a.greedy) {
     if constexpr (TOPP) {
@@ -2326,8 +2328,7 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
     } else {
     const float lz = uni(log2f((float)Zd));
     const float K = uni(__builtin_fmaf(M, c2, lz));
-    auto rho = [&](float v) { return exp2_hw((v - M) * c2); };                   // Z p
-    auto pn = [&](float v) { return exp2_hw(__builtin_fmaf(v - M, c2, -lz)); };  // p
+    auto rho = [&](float v) { return exp2_hw((v - M) * c2); };  // Z p
     // The floor's side: p = 2^(x c2 - K) in one fma (its rounding only moves
     // the excess, a sum of at most V * 1e-9, by parts in 1e6).
     auto pf = [&](float v) { return exp2_hw(__builtin_fmaf(v, c2, -K)); };
@@ -2340,9 +2341,10 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
     };
     const bool want_q = a.logq != nullptr;
     const bool near = u1 < (double)V * 1.001e-9;
-    double G = 0.0;
-    if (want_q || near) {
-      float gs = 0.0f;  // in units of 1e-9
+    // The excess's total G over this thread's entries, in units of 1e-9
+    // (with the block sums of the near case).
+    auto g_part = [&]() __attribute__((always_inline)) {
+      float gs = 0.0f;
 #pragma unroll
       for (int k = 0; k < SL; ++k) {
         if (k < nslab) {
@@ -2364,34 +2366,25 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
           }
         }
       }
-      double t[1] = {(double)gs};
-      block_sum<SNT, 1, double>(t, red_ws);
-      G = uni(t[0]) * 1e-9;
-    }
-    const bool use_g = near && u1 < G / (1.0 + G);
-    if (use_g) {
-      // The excess's block sums (written in the G pass) and slab totals,
-      // then the same search over them.
-      if (tid < nslab * SWAVES) {
-        const int k = tid >> 4;
-        const double t = (double)blk_s[k][lane & 15];
-        blk_g[k][lane & 15] = t;
-        const double T = row_scan_d(t);
-        if ((lane & 15) == 15) slab_g[k] = T;
-      }
-      __syncthreads();
-      if (wave == 0) locate(slab_g, [&](int k, int w) { return blk_g[k][w]; });
-      __syncthreads();
-    }
+      return gs;
+    };
     // The block's wave: its lanes' sums of the entry weights (0 past the
     // row's end), a float64 scan from the block's start, and the claiming
-    // lane's own 8 entries.
-    const int ks = uni(sh_ks), wsel = uni(sh_ws);
-    if (wave == wsel) {
+    // lane's own 8 entries, into sh_sel and sh_x.
+    auto draw_in_block = [&](bool use_g) __attribute__((always_inline)) {
+      const int ks = uni(sh_ks);
       const double run = uni(sh_run), target = uni(sh_tgt);
-      u32x4 xv = x[0];
+      // slab ks's vector, as masked ors (a chain of selects here would be
+      // folded into a dynamic index into the registers, i.e. scratch)
+      u32x4 xv = {0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int k = 1; k < SL; ++k) xv = k == ks ? x[k] : xv;
+      for (int k = 0; k < SL; ++k) {
+        const uint32_t m = k == ks ? 0xffffffffu : 0u;
+        xv.x |= x[k].x & m;
+        xv.y |= x[k].y & m;
+        xv.z |= x[k].z & m;
+        xv.w |= x[k].w & m;
+      }
       float v[8];
       unpack8<Tag>(xv, v);
       const bool inside = ks * SNT + tid < nvec;
@@ -2421,15 +2414,49 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
         sh_sel = (ks * SNT + tid) * 8 + pick;
         sh_x = xp;
       }
+    };
+    double G = 0.0;
+    bool use_g = false;
+    if (near) {
+      // The draw may fall on the excess: G and its block sums first.
+      double t[1] = {(double)g_part()};
+      block_sum<SNT, 1, double>(t, red_ws);
+      G = uni(t[0]) * 1e-9;
+      use_g = u1 < G / (1.0 + G);
+      if (use_g) {
+        // The excess's block sums (written in the G pass) and slab totals,
+        // then the same search over them.
+        if (tid < nslab * SWAVES) {
+          const int k = tid >> 4;
+          const double tk = (double)blk_s[k][lane & 15];
+          blk_g[k][lane & 15] = tk;
+          const double T = row_scan_d(tk);
+          if ((lane & 15) == 15) slab_g[k] = T;
+        }
+        __syncthreads();
+        if (wave == 0) locate(slab_g, [&](int k, int w) { return blk_g[k][w]; });
+        __syncthreads();
+      }
     }
-    __syncthreads();
+    if (wave == uni(sh_ws)) draw_in_block(use_g);
+    if (!near && want_q) {
+      // The draw needed p only, so the other waves summed the excess
+      // meanwhile; G's barrier also publishes the draw.
+      double t[1] = {(double)g_part()};
+      block_sum<SNT, 1, double>(t, red_ws);
+      G = uni(t[0]) * 1e-9;
+    } else {
+      __syncthreads();
+    }
     const int sel = sh_sel;
     if (sel >= 0) {  // else (not reached: every total is positive) the argmax
       tok = sel;
       xt_raw = sh_x;
     }
-    // log q(token) = log(max(p_tok, 1e-9)) - log(1 + G).
-    if (want_q) logq = (float)(log((double)fmaxf(pn(xt_raw), 1e-9f)) - log1p(G));
+    // log q(token) = log(max(p_tok, 1e-9)) - log(1 + G), from the token's
+    // log-prob at the end.
+    q_from_p = want_q;
+    q_g = (float)G;
     }
   }
 
@@ -2457,6 +2484,8 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
     const RowLogprob<float> fr = finish_row<float>(M * iT, s_other, xt_raw * iT);
     a.token[r] = tok;
     a.logp[r] = fr.logp;
+    // log(max(p, 1e-9)) = max(log p, log 1e-9)
+    if (q_from_p) logq = fmaxf(fr.logp, -20.723265836946411f) - log1pf(q_g);
     if (a.logq) a.logq[r] = logq;
   }
 }
