@@ -2013,9 +2013,8 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
       klo = klo > 0u ? klo - 1u : 0u;
       // An entry's slot among the counts is its key - klo, counted when below
       // R = kmax - klo + 1.  When every key from klo to kmax is a positive
-      // number's, the slot is the raw bits minus klo's; when every one is a
-      // negative number's, a constant minus the raw bits: (bits ^ m) + c
-      // either way.
+      // number's, or every one a negative number's, slot4 forms 4 x the slot
+      // from the raw bits in one multiply-add.
       const bool pos = klo > 0x8000u, neg = kmax < 0x8000u;
       if (klo == 0u || kmax < klo || kmax - klo >= (uint32_t)NB || !(pos || neg)) {
         // The keys from x_lo up outnumber the counts (a flat row over many
@@ -2034,9 +2033,11 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
         sh_found = 0;
         sh_cut = 0x7fffffff;
       }
-      // body(slab k's vector, k, the lane inside the row, its constant), for
-      // every slab, with the two slot forms as template arguments.
-      auto pick = [](bool p, uint32_t u, uint32_t v) { return p ? u : v; };  // by value
+      // body(slab k's vector, k, the lane inside the row, its slot4 constant)
+      // for every slab.  pick takes its operands by value: a conditional on
+      // the two named constants would select between their addresses and
+      // keep them, and the lambdas' captures, in scratch memory.
+      auto pick = [](bool p, uint32_t u, uint32_t v) { return p ? u : v; };
       auto each_slab = [&](auto body) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < SL; ++k) {
@@ -2046,6 +2047,7 @@ __global__ __launch_bounds__(SNT) void sample_blocks_kernel(SampleArgs a) {
           }
         }
       };
+      // 4 x the slots of a vector's 8 entries (ps: the positive form)
       auto slots8 = [](u32x4 xv, uint32_t c, uint32_t (&t)[8], auto ps) __attribute__((always_inline)) {
         constexpr bool P_ = decltype(ps)::value;
         const uint32_t w[4] = {xv.x, xv.y, xv.z, xv.w};
