@@ -551,3 +551,29 @@ def test_signed_zero_ties(device, dtype, misaligned):
         for off in range(3):
             out = RI.sample_next_token_batch(xd, seed=17, offset=off, **kw)
             _check(x, out, seed=17, offset=off, what=f"signed zeros k={k} p={p} off={off}", **kw)
+
+
+
+@pytest.mark.parametrize("V", [151936, 50264])
+@pytest.mark.parametrize("temperature", [1.0, 0.7])
+def test_floor_excess_regimes(device, V, temperature):
+    """The reference's defaults (top_k 0, top_p 1) with log q on rows whose
+    floor excess G comes from very different parts of the row: N(0, 3)
+    (entries below -4 floored at T 1), shifted by +30 and +45 (the floored
+    band among large positive logits), a dominant token, log-probs (every
+    logit negative), and a third of a row pushed 40 down (thousands of
+    entries floored outright).  log q against the oracle's float64 value."""
+
+    B = 8
+    g = torch.Generator().manual_seed(71)
+    x = torch.randn(B, V, generator=g) * 3.0
+    x[1] += 30.0
+    x[2, 4321] += 25.0
+    x[3] = torch.log_softmax(x[3], dim=0)
+    x[4] = torch.randn(V, generator=g) * 3.0 + 45.0
+    x[5, : V // 3] -= 40.0
+    x = x.to(torch.bfloat16)
+    kw = dict(temperature=temperature, top_k=0, top_p=1.0, do_sample=True)
+    for off in range(3):
+        out = RI.sample_next_token_batch(x.to(device), seed=29, offset=off, **kw)
+        _check(x, out, seed=29, offset=off, what=f"excess V={V} T={temperature} off={off}", **kw)
