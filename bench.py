@@ -767,9 +767,11 @@ def measure_config(name, args, device, steps, warmup, with_cpu, cpu_seqs=None,
             "achieved": round(step_alg / (k_sum * 1e-3) / 1e9, 1),
             "frac": round(step_alg / (k_sum * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "note": "achieved = both sweeps' bytes over both kernels' time",
-            # the algorithmic roofline of a step that skips masked rows
-            # one read of the masked-in rows, one
-            # dlogits write, 21 B of side data per token, over the step time
+            # the single-sweep algorithmic bytes of a step that skips masked
+            # rows (one read of the masked-in rows, one dlogits write, 21 B of
+            # side data per token) over the step time; GSPO's sequence ratio
+            # needs a second read of the rows with a gradient, which this
+            # figure leaves out
             "baseline_skip_bytes": n_active * V * in_b + N * V * in_b + N * SIDE_BYTES,
             "baseline_skip_frac": round((n_active * V * in_b + N * V * in_b + N * SIDE_BYTES)
                                         / (v_el / steps) / 1e9 / HBM_PEAK_GBS, 4),
