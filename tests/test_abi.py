@@ -73,6 +73,23 @@ def test_host_validation_status_codes(lib):
                                       nv, nv, None, None, None, None, None, nat.BF16, 8, 8,
                                       None, None)
     assert rc == -1 and b"token-local" in lib.rrl_last_error()
+    # the weight transpose: negative sizes, null operands, short row strides
+    rc = lib.rrl_transpose16(None, -1, 4, 4, None, 4, None)
+    assert rc == -1 and b"negative" in lib.rrl_last_error()
+    assert lib.rrl_transpose16(None, 0, 4, 4, None, 0, None) == 0  # nothing to do
+    rc = lib.rrl_transpose16(None, 4, 4, 4, None, 4, None)
+    assert rc == -1 and b"null" in lib.rrl_last_error()
+    rc = lib.rrl_transpose16(16, 4, 8, 4, 16, 4, None)
+    assert rc == -1 and b"stride" in lib.rrl_last_error()
+    rc = lib.rrl_transpose16(16, 4, 8, 8, 16, 2, None)
+    assert rc == -1 and b"stride" in lib.rrl_last_error()
+    # the sampler: logits dtype and row count
+    rc = lib.rrl_sample_logprobs(16, nat.I32, 1, 8, 8, 1.0, 0, 1.0, 1, 0, 0, 16, 16, None, None,
+                                 None)
+    assert rc == -2 and b"float32, bfloat16 or float16" in lib.rrl_last_error()
+    rc = lib.rrl_sample_logprobs(16, nat.BF16, -1, 8, 8, 1.0, 0, 1.0, 1, 0, 0, 16, 16, None,
+                                 None, None)
+    assert rc == -1 and b"rows" in lib.rrl_last_error()
     # success clears the last error
     assert lib.rrl_abi_version() >= 1
 
